@@ -1,0 +1,165 @@
+/*
+ * nkt_moe.h -- C ABI of the MI355X (gfx950) MoE expert path.
+ *
+ * One handle describes one MoE layer shape.  All device buffers are owned by
+ * the caller and passed as plain pointers; every entry point enqueues work on
+ * the given HIP stream and returns without synchronising the host.  Entry
+ * points return NKT_OK (0) or NKT_ERR (-1) and write a message into
+ * err[0..err_len) on failure (the convention of the reference's native
+ * bridge, nano_ktrans/kernels/pim_native/host_quantized_bridge.c:157-167,
+ * 226-281, 640-648: handle + error buffer + int return code).
+ *
+ * Pair index: token t, top-k slot j  ->  p = t * top_k + j.
+ * Position:   the rank of a pair in (expert ascending, token ascending) order.
+ *
+ * Weight formats (device layout written by nkt_moe_pack_weight):
+ *   NKT_WEIGHT_F32        fp32 weights, fp32 activations
+ *   NKT_WEIGHT_BF16       bf16 weights
+ *   NKT_WEIGHT_INT8_PC    int8, one bf16 scale per output channel
+ *   NKT_WEIGHT_INT4_G128  int4, one bf16 scale per output channel per 128 inputs
+ * Source layout accepted by nkt_moe_pack_weight (device pointers):
+ *   dense:  [N, K] row-major (nn.Linear.weight), fp32 or bf16
+ *   int8:   int32 words [N, K/4],  byte j of word w is column 4w+j, stored q+128
+ *   int4:   int32 words [N, K/8],  nibble j of word w is column 8w+j, stored q+8
+ *           (GPTQLinearWeight.qweight, nano_ktrans/kernels/weight_loader.py:25-69)
+ *   scales: bf16 [N, groups] (groups = K/128 for int4, 1 for int8)
+ * "gate_up" is the packed [2I, H] projection (gate rows, then up rows;
+ * nano_ktrans/layers/expert_mlp.py:26-41, 56-72); "down" is [H, I].
+ */
+#ifndef NKT_MOE_H
+#define NKT_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NKT_OK 0
+#define NKT_ERR (-1)
+
+/* weight formats */
+#define NKT_WEIGHT_F32 0
+#define NKT_WEIGHT_BF16 1
+#define NKT_WEIGHT_INT8_PC 2
+#define NKT_WEIGHT_INT4_G128 3
+
+/* activation / logits dtypes */
+#define NKT_DTYPE_F32 0
+#define NKT_DTYPE_BF16 1
+
+/* routing flags (nano_ktrans/models/config.py:26-75 router_use_softmax,
+ * normalize_topk_prob) */
+#define NKT_ROUTE_SOFTMAX 1u
+#define NKT_ROUTE_RENORM 2u
+
+/* weight slots for nkt_moe_weight_bytes / nkt_moe_pack_weight / nkt_moe_bind_weights */
+#define NKT_SLOT_GATE_UP 0        /* packed code blocks, all experts        */
+#define NKT_SLOT_GATE_UP_SCALES 1 /* bf16 scales, all experts               */
+#define NKT_SLOT_DOWN 2
+#define NKT_SLOT_DOWN_SCALES 3
+#define NKT_SLOT_SHARED_GATE_UP 4 /* shared expert (one expert)             */
+#define NKT_SLOT_SHARED_GATE_UP_SCALES 5
+#define NKT_SLOT_SHARED_DOWN 6
+#define NKT_SLOT_SHARED_DOWN_SCALES 7
+#define NKT_SLOT_SHARED_GATE 8 /* shared_expert_gate.weight [1, H], act dtype */
+#define NKT_NUM_SLOTS 9
+
+/* workspace regions for nkt_moe_workspace_region */
+#define NKT_WS_TOPK_IDS 0     /* int32 [T, k]            */
+#define NKT_WS_TOPK_WEIGHTS 1 /* fp32  [T, k]            */
+#define NKT_WS_COUNTS 2       /* int32 [E]               */
+#define NKT_WS_OFFSETS 3      /* int32 [E + 1]           */
+#define NKT_WS_PERM 4         /* int32 [T * k]  pos -> p */
+#define NKT_WS_INV 5          /* int32 [T * k]  p -> pos */
+#define NKT_WS_H 6            /* act dtype [T*k, I]  SwiGLU activations by position */
+#define NKT_WS_Y 7            /* fp32 [T*k, H] expert outputs by position            */
+#define NKT_WS_SHARED_GATE 8  /* fp32 [T] sigmoid(x . g)                              */
+#define NKT_WS_SHARED_H 9     /* act dtype [T, I_s]                                    */
+#define NKT_WS_SHARED_Y 10    /* fp32 [T, H]                                           */
+#define NKT_WS_NUM_REGIONS 11
+
+/* Create a handle for one layer shape.
+ * Replaces the construction of HybridMoE's expert state
+ * (nano_ktrans/layers/hybrid_moe.py:55-290).  shared_inter = 0: no shared
+ * expert.  max_tokens bounds num_tokens of every later call.  Returns NULL on
+ * failure. */
+void* nkt_moe_create(int num_experts, int top_k, int hidden_size, int moe_intermediate_size,
+                     int shared_intermediate_size, int weight_format, int act_dtype,
+                     unsigned route_flags, int max_tokens, char* err, size_t err_len);
+
+void nkt_moe_destroy(void* handle);
+
+/* Bytes of device memory a weight slot needs (all experts of the layer). */
+int nkt_moe_weight_bytes(void* handle, int slot, size_t* bytes, char* err, size_t err_len);
+
+/* Repack one expert's projection from the source layout into the device
+ * layout inside dst (a buffer of nkt_moe_weight_bytes(slot) bytes; dst_scales
+ * likewise for the matching *_SCALES slot, NULL for dense formats).
+ * slot: NKT_SLOT_GATE_UP / NKT_SLOT_DOWN (expert in [0, E)) or
+ * NKT_SLOT_SHARED_GATE_UP / NKT_SLOT_SHARED_DOWN (expert 0).  Replaces the
+ * per-expert weight load of nano_ktrans/layers/expert_mlp.py:56-85 and
+ * nano_ktrans/kernels/weight_loader.py:278-325, 355-392. */
+int nkt_moe_pack_weight(void* handle, int slot, int expert, const void* src, const void* src_scales,
+                        void* dst, void* dst_scales, void* stream, char* err, size_t err_len);
+
+/* Bind the device weight buffers used by later forward calls.  ptrs has
+ * NKT_NUM_SLOTS entries (NULL where a slot does not apply). */
+int nkt_moe_bind_weights(void* handle, const void* const* ptrs, char* err, size_t err_len);
+
+/* Workspace size for num_tokens tokens, and the byte offset of each region. */
+int nkt_moe_workspace_bytes(void* handle, int num_tokens, size_t* bytes, char* err, size_t err_len);
+int nkt_moe_workspace_region(void* handle, int num_tokens, int region, size_t* offset,
+                             char* err, size_t err_len);
+
+/* K1 + K2: router softmax / top-k / renormalise, then the deterministic
+ * count / prefix-sum / permute.  Replaces nano_ktrans/layers/hybrid_moe.py:
+ * 3321-3329 (routing) and 3384-3386, 3512-3526 (per-expert token lists).
+ * router_logits: [T, E] in the handle's act dtype.  Results land in the
+ * workspace regions NKT_WS_TOPK_IDS .. NKT_WS_INV. */
+int nkt_moe_route(void* handle, const void* router_logits, int num_tokens, void* workspace,
+                  size_t workspace_bytes, void* stream, char* err, size_t err_len);
+
+/* K3: grouped SwiGLU expert GEMM for the routed experts (needs a prior
+ * nkt_moe_route on the same workspace).  Replaces the per-expert loop
+ * nano_ktrans/layers/hybrid_moe.py:3501-3533 / expert_mlp.py:20-41 and
+ * nano_ktrans/kernels/cpu_moe.py:419-450.  Writes NKT_WS_H and NKT_WS_Y. */
+int nkt_moe_experts(void* handle, const void* hidden_states, int num_tokens, void* workspace,
+                    size_t workspace_bytes, void* stream, char* err, size_t err_len);
+
+/* K3 as its two launches: phase 0 = gate_up GEMM + SwiGLU (reads
+ * hidden_states, writes NKT_WS_H), phase 1 = down GEMM (reads NKT_WS_H,
+ * writes NKT_WS_Y; hidden_states unused).  nkt_moe_experts is phase 0 then
+ * phase 1; callers may enqueue other work between the two. */
+int nkt_moe_experts_phase(void* handle, int phase, const void* hidden_states, int num_tokens,
+                          void* workspace, size_t workspace_bytes, void* stream, char* err,
+                          size_t err_len);
+
+/* K4 (+ K3 with one dense expert): shared expert and its sigmoid gate,
+ * nano_ktrans/models/mixtral.py:170-179, 215-218.  Writes NKT_WS_SHARED_*. */
+int nkt_moe_shared(void* handle, const void* hidden_states, int num_tokens, void* workspace,
+                   size_t workspace_bytes, void* stream, char* err, size_t err_len);
+
+/* K5: un-permute and weighted combine in ascending expert id order, plus the
+ * gated shared expert when the handle has one; out [T, H] in the act dtype.
+ * Replaces nano_ktrans/layers/hybrid_moe.py:3529-3533, 3570 and
+ * nano_ktrans/kernels/cpu_moe.py:528-538. */
+int nkt_moe_combine(void* handle, int num_tokens, void* out, void* workspace,
+                    size_t workspace_bytes, void* stream, char* err, size_t err_len);
+
+/* The whole layer: route, experts, shared expert, combine.  Replaces
+ * HybridMoE.forward (nano_ktrans/layers/hybrid_moe.py:3310-3570) plus the
+ * shared-expert add of nano_ktrans/models/mixtral.py:215-218. */
+int nkt_moe_forward(void* handle, const void* hidden_states, const void* router_logits,
+                    int num_tokens, void* out, void* workspace, size_t workspace_bytes,
+                    void* stream, char* err, size_t err_len);
+
+/* Library version string (static storage). */
+const char* nkt_moe_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NKT_MOE_H */

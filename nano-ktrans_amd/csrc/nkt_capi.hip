@@ -1,0 +1,515 @@
+// C ABI of the MoE expert path (declared in include/nkt_moe.h).
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <new>
+
+#include "../../include/nkt_moe.h"
+#include "nkt_common.h"
+#include "nkt_internal.h"
+
+namespace {
+
+using namespace nkt;
+
+struct Handle {
+  int E, k, H, I, Is, wf, act_bf16;
+  unsigned flags;
+  int max_tokens;
+  const void* w[NKT_NUM_SLOTS];
+};
+
+constexpr int kWsTiles = NKT_WS_NUM_REGIONS;       // int32 [max_tiles][4]
+constexpr int kWsNTiles = NKT_WS_NUM_REGIONS + 1;  // int32 [1]
+constexpr int kWsAll = NKT_WS_NUM_REGIONS + 2;
+
+void set_err(char* err, size_t len, const char* fmt, ...) {
+  if (!err || len == 0) return;
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(err, len, fmt, ap);
+  va_end(ap);
+}
+
+int bytes_per_weight_x2(int wf) {  // bytes per weight, times two
+  return wf == WF_F32 ? 8 : wf == WF_BF16 ? 4 : wf == WF_I8 ? 2 : 1;
+}
+
+// rows / cols of the projection in a slot
+bool slot_shape(const Handle* h, int slot, int* N, int* K, int* experts) {
+  switch (slot) {
+    case NKT_SLOT_GATE_UP:
+    case NKT_SLOT_GATE_UP_SCALES:
+      *N = 2 * h->I, *K = h->H, *experts = h->E;
+      return true;
+    case NKT_SLOT_DOWN:
+    case NKT_SLOT_DOWN_SCALES:
+      *N = h->H, *K = h->I, *experts = h->E;
+      return true;
+    case NKT_SLOT_SHARED_GATE_UP:
+    case NKT_SLOT_SHARED_GATE_UP_SCALES:
+      *N = 2 * h->Is, *K = h->H, *experts = 1;
+      return h->Is > 0;
+    case NKT_SLOT_SHARED_DOWN:
+    case NKT_SLOT_SHARED_DOWN_SCALES:
+      *N = h->H, *K = h->Is, *experts = 1;
+      return h->Is > 0;
+    default:
+      return false;
+  }
+}
+
+bool is_scale_slot(int slot) {
+  return slot == NKT_SLOT_GATE_UP_SCALES || slot == NKT_SLOT_DOWN_SCALES ||
+         slot == NKT_SLOT_SHARED_GATE_UP_SCALES || slot == NKT_SLOT_SHARED_DOWN_SCALES;
+}
+
+int64_t code_bytes(const Handle* h, int N, int K) {
+  return (int64_t)N * K * bytes_per_weight_x2(h->wf) / 2;
+}
+
+int64_t scale_elems(const Handle* h, int N, int K) {
+  if (h->wf == WF_I4) return (int64_t)N * (K / 128);
+  if (h->wf == WF_I8) return N;
+  return 0;
+}
+
+size_t slot_bytes(const Handle* h, int slot) {
+  if (slot == NKT_SLOT_SHARED_GATE) return h->Is > 0 ? (size_t)h->H * (h->act_bf16 ? 2 : 4) : 0;
+  int N, K, ne;
+  if (!slot_shape(h, slot, &N, &K, &ne)) return 0;
+  if (is_scale_slot(slot)) return (size_t)ne * scale_elems(h, N, K) * 2;
+  return (size_t)ne * code_bytes(h, N, K);
+}
+
+struct WsLayout {
+  size_t off[kWsAll];
+  size_t total;
+  int bm;
+  int max_tiles;
+};
+
+size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
+
+WsLayout ws_layout(const Handle* h, int T) {
+  WsLayout L;
+  const size_t P = (size_t)T * h->k;
+  const size_t es = h->act_bf16 ? 2 : 4;
+  L.bm = gemm_tile_m(T > 0 ? T : 1, h->k, h->E);
+  L.max_tiles = (int)(P / L.bm) + (int)(P < (size_t)h->E ? P : (size_t)h->E);
+  size_t sz[kWsAll];
+  sz[NKT_WS_TOPK_IDS] = P * 4;
+  sz[NKT_WS_TOPK_WEIGHTS] = P * 4;
+  sz[NKT_WS_COUNTS] = (size_t)h->E * 4;
+  sz[NKT_WS_OFFSETS] = (size_t)(h->E + 1) * 4;
+  sz[NKT_WS_PERM] = P * 4;
+  sz[NKT_WS_INV] = P * 4;
+  sz[NKT_WS_H] = P * h->I * es;
+  sz[NKT_WS_Y] = P * h->H * 4;
+  sz[NKT_WS_SHARED_GATE] = h->Is > 0 ? (size_t)T * 4 : 0;
+  sz[NKT_WS_SHARED_H] = h->Is > 0 ? (size_t)T * h->Is * es : 0;
+  sz[NKT_WS_SHARED_Y] = h->Is > 0 ? (size_t)T * h->H * 4 : 0;
+  sz[kWsTiles] = (size_t)L.max_tiles * 16;
+  sz[kWsNTiles] = 4;
+  size_t o = 0;
+  for (int i = 0; i < kWsAll; ++i) {
+    L.off[i] = o;
+    o += align_up(sz[i]);
+  }
+  L.total = o;
+  return L;
+}
+
+bool check_hip(hipError_t e, const char* what, char* err, size_t len) {
+  if (e == hipSuccess) return true;
+  set_err(err, len, "%s: %s", what, hipGetErrorString(e));
+  return false;
+}
+
+bool check_call(Handle* h, int T, void* ws, size_t ws_bytes, char* err, size_t len) {
+  if (!h) {
+    set_err(err, len, "null handle");
+    return false;
+  }
+  if (T < 0 || T > h->max_tokens) {
+    set_err(err, len, "num_tokens=%d outside [0, max_tokens=%d]", T, h->max_tokens);
+    return false;
+  }
+  const WsLayout L = ws_layout(h, T);
+  if (T > 0 && (!ws || ws_bytes < L.total)) {
+    set_err(err, len, "workspace too small: need %zu bytes, got %zu", L.total, ws_bytes);
+    return false;
+  }
+  return true;
+}
+
+bool check_weights(const Handle* h, bool shared, char* err, size_t len) {
+  const int need[] = {NKT_SLOT_GATE_UP, NKT_SLOT_DOWN};
+  for (int s : need)
+    if (!h->w[s]) {
+      set_err(err, len, "weight slot %d not bound", s);
+      return false;
+    }
+  if (h->wf == WF_I4 || h->wf == WF_I8) {
+    if (!h->w[NKT_SLOT_GATE_UP_SCALES] || !h->w[NKT_SLOT_DOWN_SCALES]) {
+      set_err(err, len, "scale slots not bound");
+      return false;
+    }
+  }
+  if (shared) {
+    if (!h->w[NKT_SLOT_SHARED_GATE_UP] || !h->w[NKT_SLOT_SHARED_DOWN] || !h->w[NKT_SLOT_SHARED_GATE]) {
+      set_err(err, len, "shared expert slots not bound");
+      return false;
+    }
+    if ((h->wf == WF_I4 || h->wf == WF_I8) &&
+        (!h->w[NKT_SLOT_SHARED_GATE_UP_SCALES] || !h->w[NKT_SLOT_SHARED_DOWN_SCALES])) {
+      set_err(err, len, "shared expert scale slots not bound");
+      return false;
+    }
+  }
+  return true;
+}
+
+template <typename T>
+T* ws_ptr(void* ws, const WsLayout& L, int region) {
+  return (T*)((uint8_t*)ws + L.off[region]);
+}
+
+GemmArgs expert_args(const Handle* h, int phase, bool shared, const void* in, void* ws,
+                     const WsLayout& L, int T) {
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  const int I = shared ? h->Is : h->I;
+  const int N = phase == PHASE_GATE_UP ? 2 * I : h->H;
+  const int K = phase == PHASE_GATE_UP ? h->H : I;
+  const int slot = shared ? (phase == PHASE_GATE_UP ? NKT_SLOT_SHARED_GATE_UP : NKT_SLOT_SHARED_DOWN)
+                          : (phase == PHASE_GATE_UP ? NKT_SLOT_GATE_UP : NKT_SLOT_DOWN);
+  a.w = (const uint8_t*)h->w[slot];
+  a.scales = (const uint16_t*)h->w[slot + 1];
+  a.w_expert_bytes = code_bytes(h, N, K);
+  a.s_expert_elems = scale_elems(h, N, K);
+  a.N = N;
+  a.K = K;
+  a.I = I;
+  a.in = in;
+  a.topk = h->k;
+  a.act_bf16 = h->act_bf16;
+  if (shared) {
+    a.perm = nullptr;
+    a.out = phase == PHASE_GATE_UP ? ws_ptr<void>(ws, L, NKT_WS_SHARED_H) : ws_ptr<void>(ws, L, NKT_WS_SHARED_Y);
+    a.tiles = nullptr;
+    a.n_tiles = nullptr;
+    a.num_rows = T;
+  } else {
+    a.perm = phase == PHASE_GATE_UP ? ws_ptr<int32_t>(ws, L, NKT_WS_PERM) : nullptr;
+    a.out = phase == PHASE_GATE_UP ? ws_ptr<void>(ws, L, NKT_WS_H) : ws_ptr<void>(ws, L, NKT_WS_Y);
+    a.tiles = ws_ptr<int32_t>(ws, L, kWsTiles);
+    a.n_tiles = ws_ptr<int32_t>(ws, L, kWsNTiles);
+    a.num_rows = T * h->k;
+  }
+  return a;
+}
+
+int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, hipStream_t st,
+             char* err, size_t len) {
+  if (!logits) {
+    set_err(err, len, "null router_logits");
+    return NKT_ERR;
+  }
+  int32_t* ids = ws_ptr<int32_t>(ws, L, NKT_WS_TOPK_IDS);
+  float* wts = ws_ptr<float>(ws, L, NKT_WS_TOPK_WEIGHTS);
+  if (!check_hip(launch_route(logits, h->act_bf16, T, h->E, h->k, h->flags, ids, wts, st),
+                 "route kernel", err, len))
+    return NKT_ERR;
+  if (!check_hip(launch_group(ids, T, h->k, h->E, L.bm, L.max_tiles,
+                              ws_ptr<int32_t>(ws, L, NKT_WS_COUNTS),
+                              ws_ptr<int32_t>(ws, L, NKT_WS_OFFSETS),
+                              ws_ptr<int32_t>(ws, L, NKT_WS_PERM),
+                              ws_ptr<int32_t>(ws, L, NKT_WS_INV), ws_ptr<int32_t>(ws, L, kWsTiles),
+                              ws_ptr<int32_t>(ws, L, kWsNTiles), st),
+                 "group kernel", err, len))
+    return NKT_ERR;
+  return NKT_OK;
+}
+
+int do_expert_phase(Handle* h, int phase, const void* x, int T, void* ws, const WsLayout& L,
+                    hipStream_t st, char* err, size_t len) {
+  if (phase == PHASE_GATE_UP && !x) {
+    set_err(err, len, "null hidden_states");
+    return NKT_ERR;
+  }
+  if (!check_weights(h, false, err, len)) return NKT_ERR;
+  if (phase == PHASE_GATE_UP) {
+    GemmArgs a = expert_args(h, PHASE_GATE_UP, false, x, ws, L, T);
+    if (!check_hip(launch_gemm(a, h->wf, PHASE_GATE_UP, L.bm, L.max_tiles, st), "gate_up gemm", err, len))
+      return NKT_ERR;
+  } else {
+    GemmArgs b = expert_args(h, PHASE_DOWN, false, ws_ptr<void>(ws, L, NKT_WS_H), ws, L, T);
+    if (!check_hip(launch_gemm(b, h->wf, PHASE_DOWN, L.bm, L.max_tiles, st), "down gemm", err, len))
+      return NKT_ERR;
+  }
+  return NKT_OK;
+}
+
+int do_experts(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipStream_t st,
+               char* err, size_t len) {
+  if (do_expert_phase(h, PHASE_GATE_UP, x, T, ws, L, st, err, len) != NKT_OK) return NKT_ERR;
+  return do_expert_phase(h, PHASE_DOWN, x, T, ws, L, st, err, len);
+}
+
+int do_shared(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipStream_t st,
+              char* err, size_t len) {
+  if (h->Is <= 0) {
+    set_err(err, len, "handle has no shared expert");
+    return NKT_ERR;
+  }
+  if (!x) {
+    set_err(err, len, "null hidden_states");
+    return NKT_ERR;
+  }
+  if (!check_weights(h, true, err, len)) return NKT_ERR;
+  if (!check_hip(launch_shared_gate(x, h->w[NKT_SLOT_SHARED_GATE], h->act_bf16, T, h->H,
+                                    ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE), st),
+                 "shared gate kernel", err, len))
+    return NKT_ERR;
+  const int bm = gemm_tile_m(T, 1, 1);
+  const int tiles = (T + bm - 1) / bm;
+  GemmArgs a = expert_args(h, PHASE_GATE_UP, true, x, ws, L, T);
+  if (!check_hip(launch_gemm(a, h->wf, PHASE_GATE_UP, bm, tiles, st), "shared gate_up gemm", err, len))
+    return NKT_ERR;
+  GemmArgs b = expert_args(h, PHASE_DOWN, true, ws_ptr<void>(ws, L, NKT_WS_SHARED_H), ws, L, T);
+  if (!check_hip(launch_gemm(b, h->wf, PHASE_DOWN, bm, tiles, st), "shared down gemm", err, len))
+    return NKT_ERR;
+  return NKT_OK;
+}
+
+int do_combine(Handle* h, int T, void* out, void* ws, const WsLayout& L, hipStream_t st, char* err,
+               size_t len) {
+  if (!out) {
+    set_err(err, len, "null output");
+    return NKT_ERR;
+  }
+  const bool sh = h->Is > 0;
+  if (!check_hip(launch_combine(ws_ptr<float>(ws, L, NKT_WS_Y), ws_ptr<int32_t>(ws, L, NKT_WS_TOPK_IDS),
+                                ws_ptr<float>(ws, L, NKT_WS_TOPK_WEIGHTS),
+                                ws_ptr<int32_t>(ws, L, NKT_WS_INV),
+                                sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_Y) : nullptr,
+                                sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE) : nullptr, T, h->k,
+                                h->H, out, h->act_bf16, st),
+                 "combine kernel", err, len))
+    return NKT_ERR;
+  return NKT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void* nkt_moe_create(int num_experts, int top_k, int hidden_size, int moe_intermediate_size,
+                     int shared_intermediate_size, int weight_format, int act_dtype,
+                     unsigned route_flags, int max_tokens, char* err, size_t err_len) {
+  if (num_experts < 1 || num_experts > kMaxExperts) {
+    set_err(err, err_len, "num_experts=%d outside [1, %d]", num_experts, kMaxExperts);
+    return nullptr;
+  }
+  if (top_k < 1 || top_k > kMaxTopK || top_k > num_experts) {
+    set_err(err, err_len, "top_k=%d outside [1, min(%d, num_experts)]", top_k, kMaxTopK);
+    return nullptr;
+  }
+  if (weight_format < NKT_WEIGHT_F32 || weight_format > NKT_WEIGHT_INT4_G128) {
+    set_err(err, err_len, "unknown weight_format %d", weight_format);
+    return nullptr;
+  }
+  if (act_dtype != NKT_DTYPE_F32 && act_dtype != NKT_DTYPE_BF16) {
+    set_err(err, err_len, "unknown act_dtype %d", act_dtype);
+    return nullptr;
+  }
+  if ((weight_format == NKT_WEIGHT_F32) != (act_dtype == NKT_DTYPE_F32)) {
+    set_err(err, err_len, "fp32 weights require fp32 activations and the other formats bf16");
+    return nullptr;
+  }
+  // the 128-wide K groups and 64-row down tiles need these multiples
+  if (hidden_size < 128 || hidden_size % 128 != 0) {
+    set_err(err, err_len, "hidden_size=%d must be a positive multiple of 128", hidden_size);
+    return nullptr;
+  }
+  if (moe_intermediate_size < 128 || moe_intermediate_size % 128 != 0) {
+    set_err(err, err_len, "moe_intermediate_size=%d must be a positive multiple of 128",
+            moe_intermediate_size);
+    return nullptr;
+  }
+  if (shared_intermediate_size < 0 || shared_intermediate_size % 128 != 0) {
+    set_err(err, err_len, "shared_intermediate_size=%d must be 0 or a multiple of 128",
+            shared_intermediate_size);
+    return nullptr;
+  }
+  if (max_tokens < 1 || (int64_t)max_tokens * top_k > (1 << 24)) {
+    set_err(err, err_len, "max_tokens=%d outside [1, 2^24 / top_k]", max_tokens);
+    return nullptr;
+  }
+  Handle* h = new (std::nothrow) Handle();
+  if (!h) {
+    set_err(err, err_len, "out of host memory");
+    return nullptr;
+  }
+  h->E = num_experts;
+  h->k = top_k;
+  h->H = hidden_size;
+  h->I = moe_intermediate_size;
+  h->Is = shared_intermediate_size;
+  h->wf = weight_format;
+  h->act_bf16 = act_dtype == NKT_DTYPE_BF16;
+  h->flags = route_flags;
+  h->max_tokens = max_tokens;
+  for (int i = 0; i < NKT_NUM_SLOTS; ++i) h->w[i] = nullptr;
+  return h;
+}
+
+void nkt_moe_destroy(void* handle) { delete (Handle*)handle; }
+
+int nkt_moe_weight_bytes(void* handle, int slot, size_t* bytes, char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!h || !bytes || slot < 0 || slot >= NKT_NUM_SLOTS) {
+    set_err(err, err_len, "bad arguments");
+    return NKT_ERR;
+  }
+  *bytes = slot_bytes(h, slot);
+  return NKT_OK;
+}
+
+int nkt_moe_pack_weight(void* handle, int slot, int expert, const void* src, const void* src_scales,
+                        void* dst, void* dst_scales, void* stream, char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!h) {
+    set_err(err, err_len, "null handle");
+    return NKT_ERR;
+  }
+  if (slot != NKT_SLOT_GATE_UP && slot != NKT_SLOT_DOWN && slot != NKT_SLOT_SHARED_GATE_UP &&
+      slot != NKT_SLOT_SHARED_DOWN) {
+    set_err(err, err_len, "slot %d is not a packable projection", slot);
+    return NKT_ERR;
+  }
+  int N, K, ne;
+  if (!slot_shape(h, slot, &N, &K, &ne)) {
+    set_err(err, err_len, "slot %d unused by this handle", slot);
+    return NKT_ERR;
+  }
+  if (expert < 0 || expert >= ne) {
+    set_err(err, err_len, "expert %d outside [0, %d)", expert, ne);
+    return NKT_ERR;
+  }
+  const bool quant = h->wf == WF_I4 || h->wf == WF_I8;
+  if (!src || !dst || (quant && (!src_scales || !dst_scales))) {
+    set_err(err, err_len, "null source or destination pointer");
+    return NKT_ERR;
+  }
+  uint8_t* d = (uint8_t*)dst + (int64_t)expert * code_bytes(h, N, K);
+  uint16_t* ds = quant ? (uint16_t*)dst_scales + (int64_t)expert * scale_elems(h, N, K) : nullptr;
+  if (!check_hip(launch_pack(h->wf, src, src_scales, N, K, d, ds, (hipStream_t)stream), "pack kernel",
+                 err, err_len))
+    return NKT_ERR;
+  return NKT_OK;
+}
+
+int nkt_moe_bind_weights(void* handle, const void* const* ptrs, char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!h || !ptrs) {
+    set_err(err, err_len, "bad arguments");
+    return NKT_ERR;
+  }
+  for (int i = 0; i < NKT_NUM_SLOTS; ++i) h->w[i] = ptrs[i];
+  return NKT_OK;
+}
+
+int nkt_moe_workspace_bytes(void* handle, int num_tokens, size_t* bytes, char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!h || !bytes || num_tokens < 0 || num_tokens > h->max_tokens) {
+    set_err(err, err_len, "bad arguments");
+    return NKT_ERR;
+  }
+  *bytes = ws_layout(h, num_tokens).total;
+  return NKT_OK;
+}
+
+int nkt_moe_workspace_region(void* handle, int num_tokens, int region, size_t* offset, char* err,
+                             size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!h || !offset || num_tokens < 0 || num_tokens > h->max_tokens || region < 0 ||
+      region >= NKT_WS_NUM_REGIONS) {
+    set_err(err, err_len, "bad arguments");
+    return NKT_ERR;
+  }
+  *offset = ws_layout(h, num_tokens).off[region];
+  return NKT_OK;
+}
+
+int nkt_moe_route(void* handle, const void* router_logits, int num_tokens, void* workspace,
+                  size_t workspace_bytes, void* stream, char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!check_call(h, num_tokens, workspace, workspace_bytes, err, err_len)) return NKT_ERR;
+  if (num_tokens == 0) return NKT_OK;
+  const WsLayout L = ws_layout(h, num_tokens);
+  return do_route(h, router_logits, num_tokens, workspace, L, (hipStream_t)stream, err, err_len);
+}
+
+int nkt_moe_experts(void* handle, const void* hidden_states, int num_tokens, void* workspace,
+                    size_t workspace_bytes, void* stream, char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!check_call(h, num_tokens, workspace, workspace_bytes, err, err_len)) return NKT_ERR;
+  if (num_tokens == 0) return NKT_OK;
+  const WsLayout L = ws_layout(h, num_tokens);
+  return do_experts(h, hidden_states, num_tokens, workspace, L, (hipStream_t)stream, err, err_len);
+}
+
+int nkt_moe_experts_phase(void* handle, int phase, const void* hidden_states, int num_tokens,
+                          void* workspace, size_t workspace_bytes, void* stream, char* err,
+                          size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!check_call(h, num_tokens, workspace, workspace_bytes, err, err_len)) return NKT_ERR;
+  if (phase != PHASE_GATE_UP && phase != PHASE_DOWN) {
+    set_err(err, err_len, "phase must be 0 (gate_up) or 1 (down), got %d", phase);
+    return NKT_ERR;
+  }
+  if (num_tokens == 0) return NKT_OK;
+  const WsLayout L = ws_layout(h, num_tokens);
+  return do_expert_phase(h, phase, hidden_states, num_tokens, workspace, L, (hipStream_t)stream, err,
+                         err_len);
+}
+
+int nkt_moe_shared(void* handle, const void* hidden_states, int num_tokens, void* workspace,
+                   size_t workspace_bytes, void* stream, char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!check_call(h, num_tokens, workspace, workspace_bytes, err, err_len)) return NKT_ERR;
+  if (num_tokens == 0) return NKT_OK;
+  const WsLayout L = ws_layout(h, num_tokens);
+  return do_shared(h, hidden_states, num_tokens, workspace, L, (hipStream_t)stream, err, err_len);
+}
+
+int nkt_moe_combine(void* handle, int num_tokens, void* out, void* workspace, size_t workspace_bytes,
+                    void* stream, char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!check_call(h, num_tokens, workspace, workspace_bytes, err, err_len)) return NKT_ERR;
+  if (num_tokens == 0) return NKT_OK;
+  const WsLayout L = ws_layout(h, num_tokens);
+  return do_combine(h, num_tokens, out, workspace, L, (hipStream_t)stream, err, err_len);
+}
+
+int nkt_moe_forward(void* handle, const void* hidden_states, const void* router_logits,
+                    int num_tokens, void* out, void* workspace, size_t workspace_bytes, void* stream,
+                    char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!check_call(h, num_tokens, workspace, workspace_bytes, err, err_len)) return NKT_ERR;
+  if (num_tokens == 0) return NKT_OK;
+  const WsLayout L = ws_layout(h, num_tokens);
+  hipStream_t st = (hipStream_t)stream;
+  if (do_route(h, router_logits, num_tokens, workspace, L, st, err, err_len) != NKT_OK) return NKT_ERR;
+  if (do_experts(h, hidden_states, num_tokens, workspace, L, st, err, err_len) != NKT_OK) return NKT_ERR;
+  if (h->Is > 0 && do_shared(h, hidden_states, num_tokens, workspace, L, st, err, err_len) != NKT_OK)
+    return NKT_ERR;
+  return do_combine(h, num_tokens, out, workspace, L, st, err, err_len);
+}
+
+const char* nkt_moe_version(void) { return "nkt_moe 0.1.0 gfx950"; }
+
+}  // extern "C"

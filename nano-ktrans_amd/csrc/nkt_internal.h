@@ -1,0 +1,74 @@
+// Launch wrappers shared between the kernel files and the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nkt {
+
+// Device weight layout: a projection W [N, K] of one expert is cut into
+// 1 KiB blocks of 16 rows x KB columns (KB = 16 fp32, 32 bf16, 64 int8,
+// 128 int4).  Lane l of a wavefront reads the 16 bytes at offset 16*l of a
+// block: row (l % 16) and the K values that lane feeds to the matrix core.
+// Blocks are ordered (expert, row block, K block), so a wavefront streaming
+// one 16-row tile over K reads consecutive kilobytes.
+//   int4 block:  lane word s (s = 0..3) = columns 32s + 8*(l/16) + 0..7,
+//                nibble j < 4 -> column offset 2j, nibble j >= 4 -> 2(j-4)+1,
+//                stored value q + 8.
+//   int8 block:  lane bytes [8s, 8s+8) (s = 0, 1) = columns 32s + 8*(l/16) + 0..7,
+//                stored value q + 128.
+//   bf16 block:  lane halves 0..7 = columns 8*(l/16) + 0..7.
+//   fp32 block:  lane float s (s = 0..3) = column 4s + l/16.
+// Scales (int formats, bf16): int4 [expert][row block][K/128][16 rows],
+// int8 [expert][N].
+__host__ __device__ constexpr int block_k(int wf) {
+  return wf == 0 ? 16 : wf == 1 ? 32 : wf == 2 ? 64 : 128;
+}
+
+struct GemmArgs {
+  const uint8_t* w;        // packed blocks, all experts
+  const uint16_t* scales;  // bf16 scales (int formats) or nullptr
+  int64_t w_expert_bytes;  // bytes per expert
+  int64_t s_expert_elems;  // scale elements per expert
+  int N;                   // weight rows (2I for gate_up, H for down)
+  int K;                   // inner dimension
+  int I;                   // gate_up: rows [0, I) gate, [I, 2I) up; output width I
+  const void* in;          // activations, row-major [rows, K], act dtype
+  const int32_t* perm;     // gather: position -> pair, row = pair / topk; nullptr: row = position
+  int topk;
+  void* out;               // gate_up: h [pos, I] act dtype; down: y [pos, N] fp32
+  const int32_t* tiles;    // [max_tiles][4] = expert, first position, rows, 0
+  const int32_t* n_tiles;  // device scalar; nullptr: dense tiles over num_rows (expert 0)
+  int num_rows;
+  int act_bf16;
+};
+
+enum GemmPhase : int { PHASE_GATE_UP = 0, PHASE_DOWN = 1 };
+
+hipError_t launch_route(const void* logits, int act_bf16, int T, int E, int k, unsigned flags,
+                        int32_t* ids, float* w, hipStream_t stream);
+
+hipError_t launch_group(const int32_t* ids, int T, int k, int E, int bm, int max_tiles,
+                        int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
+                        int32_t* tiles, int32_t* n_tiles, hipStream_t stream);
+
+// Tile shapes: returns the token-tile height (BM) used for num_tokens.
+int gemm_tile_m(int num_tokens, int topk, int num_experts);
+
+// Rows of weights (gate_up: output columns of h) covered by one workgroup.
+int gemm_rows_per_block(int wf, int phase, int bm);
+
+hipError_t launch_gemm(const GemmArgs& a, int wf, int phase, int bm, int grid_tiles,
+                       hipStream_t stream);
+
+hipError_t launch_pack(int wf, const void* src, const void* src_scales, int N, int K,
+                       uint8_t* dst, uint16_t* dst_scales, hipStream_t stream);
+
+hipError_t launch_shared_gate(const void* x, const void* gate_w, int act_bf16, int T, int H,
+                              float* gate_out, hipStream_t stream);
+
+hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, const int32_t* inv,
+                          const float* y_shared, const float* shared_gate, int T, int k, int H,
+                          void* out, int out_bf16, hipStream_t stream);
+
+}  // namespace nkt

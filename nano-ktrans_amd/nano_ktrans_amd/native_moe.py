@@ -1,0 +1,291 @@
+"""Device-resident MoE layer driven through the C ABI (include/nkt_moe.h).
+
+``NativeMoE`` owns one layer's packed expert weights (torch tensors in HBM,
+written once by ``nkt_moe_pack_weight``) and a workspace, and enqueues the
+five kernels on torch's current HIP stream.  No call synchronises the host.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Dict, Optional, Sequence, Union
+
+import torch
+
+from . import _native as N
+from .kernels.weight_loader import GPTQLinearWeight
+
+WeightLike = Union[torch.Tensor, GPTQLinearWeight]
+
+_FORMATS = {
+    "f32": N.WEIGHT_F32,
+    "bf16": N.WEIGHT_BF16,
+    "int8_per_channel": N.WEIGHT_INT8_PC,
+    "int4_g128": N.WEIGHT_INT4_G128,
+}
+
+
+def weight_format_of(w: WeightLike, act_dtype: torch.dtype) -> str:
+    """The device weight format a source weight maps to."""
+    if isinstance(w, GPTQLinearWeight):
+        if w.bits == 4 and w.group_size == 128:
+            return "int4_g128"
+        if w.bits == 8 and w.group_size == w.input_dim:
+            return "int8_per_channel"
+        raise NotImplementedError(
+            f"unsupported quantized weight: bits={w.bits} group_size={w.group_size} "
+            "(supported: int4 group 128, int8 one group per row)")
+    return "f32" if act_dtype == torch.float32 else "bf16"
+
+
+def _require_cuda(device: torch.device) -> None:
+    if device.type != "cuda" or not torch.cuda.is_available():
+        raise N.NativeError(
+            "the MoE expert path runs only on a ROCm GPU (gfx950); got device "
+            f"{device} with torch.cuda.is_available()={torch.cuda.is_available()}")
+
+
+class NativeMoE:
+    """One MoE layer: routing flags, shapes, packed weights and a workspace."""
+
+    def __init__(
+        self,
+        *,
+        num_experts: int,
+        top_k: int,
+        hidden_size: int,
+        intermediate_size: int,
+        shared_intermediate_size: int = 0,
+        weight_format: str = "bf16",
+        act_dtype: torch.dtype = torch.bfloat16,
+        use_softmax: bool = True,
+        renorm: bool = True,
+        max_tokens: int = 4096,
+        device: Optional[torch.device] = None,
+    ):
+        self.device = torch.device(device if device is not None else "cuda")
+        _require_cuda(self.device)
+        if self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        if weight_format not in _FORMATS:
+            raise ValueError(f"unknown weight_format {weight_format!r}")
+        if act_dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError(f"activations must be fp32 or bf16, got {act_dtype}")
+        self.lib = N.lib()
+        self.err = N.ErrBuf()
+        self.num_experts = num_experts
+        self.top_k = top_k
+        self.hidden_size = hidden_size
+        self.intermediate_size = intermediate_size
+        self.shared_intermediate_size = shared_intermediate_size
+        self.weight_format = weight_format
+        self.act_dtype = act_dtype
+        self.max_tokens = max_tokens
+        flags = (N.ROUTE_SOFTMAX if use_softmax else 0) | (N.ROUTE_RENORM if renorm else 0)
+        with torch.cuda.device(self.device):
+            h = self.lib.nkt_moe_create(
+                num_experts, top_k, hidden_size, intermediate_size, shared_intermediate_size,
+                _FORMATS[weight_format], N.DTYPE_F32 if act_dtype == torch.float32 else N.DTYPE_BF16,
+                flags, max_tokens, self.err.buf, self.err.size)
+        if not h:
+            raise N.NativeError(f"nkt_moe_create failed: {self.err.buf.value.decode()}")
+        self.handle = ctypes.c_void_p(h)
+        self.slots: Dict[int, torch.Tensor] = {}
+        for slot in range(N.NUM_SLOTS):
+            nbytes = ctypes.c_size_t(0)
+            self.err.check(self.lib.nkt_moe_weight_bytes(self.handle, slot, ctypes.byref(nbytes),
+                                                         self.err.buf, self.err.size), "nkt_moe_weight_bytes")
+            if nbytes.value:
+                self.slots[slot] = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
+        self._bind()
+        self._ws: Optional[torch.Tensor] = None
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h is not None and h.value:
+            try:
+                self.lib.nkt_moe_destroy(h)
+            except Exception:
+                pass
+
+    # ------------------------------------------------------------------ weights
+    def _bind(self) -> None:
+        arr = (ctypes.c_void_p * N.NUM_SLOTS)()
+        for slot in range(N.NUM_SLOTS):
+            t = self.slots.get(slot)
+            arr[slot] = t.data_ptr() if t is not None else None
+        self.err.check(self.lib.nkt_moe_bind_weights(self.handle, arr, self.err.buf, self.err.size),
+                       "nkt_moe_bind_weights")
+
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def _source(self, parts: Sequence[WeightLike]):
+        """Stack row blocks (gate then up, or a single projection) in the source layout."""
+        fmt = self.weight_format
+        if fmt in ("int4_g128", "int8_per_channel"):
+            for p in parts:
+                if not isinstance(p, GPTQLinearWeight) or weight_format_of(p, self.act_dtype) != fmt:
+                    raise ValueError(f"expected {fmt} GPTQLinearWeight parts")
+            q = torch.cat([p.qweight.to(torch.int32) for p in parts], dim=0)
+            s = torch.cat([p.scales.to(torch.float32) for p in parts], dim=0).to(torch.bfloat16)
+            return (q.to(self.device).contiguous(), s.to(self.device).contiguous())
+        dt = torch.float32 if fmt == "f32" else torch.bfloat16
+        for p in parts:
+            if isinstance(p, GPTQLinearWeight):
+                raise ValueError("dense weight format given a quantized weight")
+        w = torch.cat([p.to(dt) for p in parts], dim=0)
+        return (w.to(self.device).contiguous(), None)
+
+    def _pack(self, slot: int, expert: int, parts: Sequence[WeightLike], n: int, k: int) -> None:
+        src, scales = self._source(parts)
+        rows = src.shape[0]
+        if rows != n:
+            raise ValueError(f"slot {slot}: expected {n} rows, got {rows}")
+        cols = src.shape[1] * (8 if self.weight_format == "int4_g128" else 4 if self.weight_format == "int8_per_channel" else 1)
+        if cols != k:
+            raise ValueError(f"slot {slot}: expected {k} input columns, got {cols}")
+        dst = self.slots[slot]
+        dst_s = self.slots.get(slot + 1)
+        with torch.cuda.device(self.device):
+            self.err.check(self.lib.nkt_moe_pack_weight(
+                self.handle, slot, expert, src.data_ptr(), scales.data_ptr() if scales is not None else None,
+                dst.data_ptr(), dst_s.data_ptr() if dst_s is not None else None, self._stream(),
+                self.err.buf, self.err.size), "nkt_moe_pack_weight")
+        # src/scales may be freed now: the caching allocator only hands their
+        # memory to work enqueued later on this stream, after the pack kernel.
+
+    def load_expert(self, expert: int, gate: WeightLike, up: WeightLike, down: WeightLike) -> None:
+        """Ingest one routed expert: gate/up [I, H], down [H, I] (dense tensors or GPTQLinearWeight)."""
+        I, H = self.intermediate_size, self.hidden_size
+        self._pack(N.SLOT_GATE_UP, expert, [gate, up], 2 * I, H)
+        self._pack(N.SLOT_DOWN, expert, [down], H, I)
+
+    def load_shared_expert(self, gate: WeightLike, up: WeightLike, down: WeightLike,
+                           gate_weight: torch.Tensor) -> None:
+        """Ingest the shared expert and its ``shared_expert_gate.weight`` [1, H]."""
+        if self.shared_intermediate_size <= 0:
+            raise ValueError("this layer was created without a shared expert")
+        Is, H = self.shared_intermediate_size, self.hidden_size
+        self._pack(N.SLOT_SHARED_GATE_UP, 0, [gate, up], 2 * Is, H)
+        self._pack(N.SLOT_SHARED_DOWN, 0, [down], H, Is)
+        g = gate_weight.reshape(-1).to(self.act_dtype).to(self.device).contiguous()
+        if g.numel() != H:
+            raise ValueError(f"shared_expert_gate weight must have {H} elements")
+        self.slots[N.SLOT_SHARED_GATE].view(self.act_dtype).copy_(g)
+
+    # ---------------------------------------------------------------- workspace
+    def workspace_bytes(self, num_tokens: int) -> int:
+        nbytes = ctypes.c_size_t(0)
+        self.err.check(self.lib.nkt_moe_workspace_bytes(self.handle, num_tokens, ctypes.byref(nbytes),
+                                                        self.err.buf, self.err.size), "nkt_moe_workspace_bytes")
+        return nbytes.value
+
+    def workspace(self, num_tokens: int) -> torch.Tensor:
+        need = self.workspace_bytes(num_tokens)
+        if self._ws is None or self._ws.numel() < need:
+            self._ws = torch.empty(max(need, 256), dtype=torch.uint8, device=self.device)
+        return self._ws
+
+    def region(self, num_tokens: int, region: int, dtype: torch.dtype, shape) -> torch.Tensor:
+        """A view of one workspace region (valid after the call that fills it)."""
+        off = ctypes.c_size_t(0)
+        self.err.check(self.lib.nkt_moe_workspace_region(self.handle, num_tokens, region, ctypes.byref(off),
+                                                         self.err.buf, self.err.size), "nkt_moe_workspace_region")
+        ws = self.workspace(num_tokens)
+        n = 1
+        for s in shape:
+            n *= int(s)
+        esz = torch.tensor([], dtype=dtype).element_size()
+        return ws[off.value: off.value + n * esz].view(dtype).view(*shape)
+
+    # ------------------------------------------------------------------ compute
+    def _check_input(self, t: torch.Tensor, cols: int, name: str) -> torch.Tensor:
+        if t.device != self.device:
+            raise ValueError(f"{name} on {t.device}, layer on {self.device}")
+        if t.dtype != self.act_dtype:
+            raise ValueError(f"{name} dtype {t.dtype}, layer expects {self.act_dtype}")
+        t = t.reshape(-1, t.shape[-1])
+        if t.shape[1] != cols:
+            raise ValueError(f"{name} has {t.shape[1]} columns, expected {cols}")
+        return t.contiguous()
+
+    def route(self, router_logits: torch.Tensor):
+        """K1 + K2.  Returns (ids int32 [T,k], weights fp32 [T,k], counts [E], offsets [E+1],
+        perm [T*k], inv [T*k]) as views of the workspace."""
+        logits = self._check_input(router_logits, self.num_experts, "router_logits")
+        T = logits.shape[0]
+        ws = self.workspace(T)
+        with torch.cuda.device(self.device):
+            self.err.check(self.lib.nkt_moe_route(self.handle, logits.data_ptr(), T, ws.data_ptr(), ws.numel(),
+                                                  self._stream(), self.err.buf, self.err.size), "nkt_moe_route")
+        k, E = self.top_k, self.num_experts
+        return (self.region(T, N.WS_TOPK_IDS, torch.int32, (T, k)),
+                self.region(T, N.WS_TOPK_WEIGHTS, torch.float32, (T, k)),
+                self.region(T, N.WS_COUNTS, torch.int32, (E,)),
+                self.region(T, N.WS_OFFSETS, torch.int32, (E + 1,)),
+                self.region(T, N.WS_PERM, torch.int32, (T * k,)),
+                self.region(T, N.WS_INV, torch.int32, (T * k,)))
+
+    def experts(self, hidden_states: torch.Tensor):
+        """K3 after ``route``: returns (h [T*k, I] act dtype, y [T*k, H] fp32) by position."""
+        x = self._check_input(hidden_states, self.hidden_size, "hidden_states")
+        T = x.shape[0]
+        ws = self.workspace(T)
+        with torch.cuda.device(self.device):
+            self.err.check(self.lib.nkt_moe_experts(self.handle, x.data_ptr(), T, ws.data_ptr(), ws.numel(),
+                                                    self._stream(), self.err.buf, self.err.size), "nkt_moe_experts")
+        P = T * self.top_k
+        return (self.region(T, N.WS_H, self.act_dtype, (P, self.intermediate_size)),
+                self.region(T, N.WS_Y, torch.float32, (P, self.hidden_size)))
+
+    def expert_phase(self, phase: int, hidden_states: Optional[torch.Tensor], num_tokens: int) -> None:
+        """One K3 launch after ``route``: phase 0 gate_up + SwiGLU, phase 1 down."""
+        xp = None
+        if phase == 0:
+            xp = self._check_input(hidden_states, self.hidden_size, "hidden_states").data_ptr()
+        ws = self.workspace(num_tokens)
+        with torch.cuda.device(self.device):
+            self.err.check(self.lib.nkt_moe_experts_phase(self.handle, phase, xp, num_tokens, ws.data_ptr(),
+                                                          ws.numel(), self._stream(), self.err.buf,
+                                                          self.err.size), "nkt_moe_experts_phase")
+
+    def shared(self, hidden_states: torch.Tensor):
+        """K4 + K3 on the shared expert: returns (gate fp32 [T], y_shared fp32 [T, H])."""
+        x = self._check_input(hidden_states, self.hidden_size, "hidden_states")
+        T = x.shape[0]
+        ws = self.workspace(T)
+        with torch.cuda.device(self.device):
+            self.err.check(self.lib.nkt_moe_shared(self.handle, x.data_ptr(), T, ws.data_ptr(), ws.numel(),
+                                                   self._stream(), self.err.buf, self.err.size), "nkt_moe_shared")
+        return (self.region(T, N.WS_SHARED_GATE, torch.float32, (T,)),
+                self.region(T, N.WS_SHARED_Y, torch.float32, (T, self.hidden_size)))
+
+    def combine(self, num_tokens: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """K5 after ``route``/``experts`` (and ``shared`` when the layer has one)."""
+        T = num_tokens
+        if out is None:
+            out = torch.empty(T, self.hidden_size, dtype=self.act_dtype, device=self.device)
+        ws = self.workspace(T)
+        with torch.cuda.device(self.device):
+            self.err.check(self.lib.nkt_moe_combine(self.handle, T, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                                    self._stream(), self.err.buf, self.err.size), "nkt_moe_combine")
+        return out
+
+    def forward(self, hidden_states: torch.Tensor, router_logits: torch.Tensor,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The whole layer; returns [T, H] in the activation dtype."""
+        x = self._check_input(hidden_states, self.hidden_size, "hidden_states")
+        logits = self._check_input(router_logits, self.num_experts, "router_logits")
+        T = x.shape[0]
+        if logits.shape[0] != T:
+            raise ValueError(f"router_logits has {logits.shape[0]} rows, hidden_states {T}")
+        if out is None:
+            out = torch.empty(T, self.hidden_size, dtype=self.act_dtype, device=self.device)
+        if T == 0:
+            return out
+        ws = self.workspace(T)
+        with torch.cuda.device(self.device):
+            self.err.check(self.lib.nkt_moe_forward(self.handle, x.data_ptr(), logits.data_ptr(), T, out.data_ptr(),
+                                                    ws.data_ptr(), ws.numel(), self._stream(),
+                                                    self.err.buf, self.err.size), "nkt_moe_forward")
+        return out

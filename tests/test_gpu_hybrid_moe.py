@@ -1,0 +1,172 @@
+"""HybridMoE as a drop-in: the reference's constructor and forward(hidden_states,
+router_logits), expert weights from gpu_experts modules (Mixtral w1/w2/w3, Qwen3
+packed gate_up) or from safetensors checkpoints (dense and GPTQ), optional shared
+expert.  Compared with the oracle at the bf16 tolerance (max-abs 2e-2, rel-L2 1e-2)."""
+import json
+import sys
+from dataclasses import replace
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+import oracle as O
+from moe_cases import Layer, MoEConfig, oracle_forward
+from nano_ktrans_amd.kernels.quantized_ops import (quantize_symmetric_int8_per_channel,
+                                                   quantize_symmetric_w4a32, to_bf16_scales)
+from nano_ktrans_amd.layers.expert_mlp import PackedSparseExpertMLP, SparseExpertMLP
+from nano_ktrans_amd.layers.hybrid_moe import HybridMoE
+from nano_ktrans_amd.models.config import MIXTRAL_SPEC, QWEN3_MOE_SPEC, QWEN3_MOE_UNPACKED_SPEC
+
+pytestmark = pytest.mark.gpu
+
+
+def announce(msg):
+    sys.__stderr__.write(f"[gpu-case] {msg}\n")
+    sys.__stderr__.flush()
+
+
+def _init(module, seed):
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for p in module.parameters():
+            p.copy_(torch.randn(p.shape, generator=g) * 0.02)
+    return module
+
+
+def _check(out, ref):
+    got = out.float().cpu().numpy()
+    err_abs = float(np.max(np.abs(got - O.bf16_round(ref))))
+    err_rel = O.rel_l2(got, ref)
+    announce(f"  max_abs={err_abs:.3e} rel_l2={err_rel:.3e}")
+    assert err_abs <= 2e-2 and err_rel <= 1e-2
+
+
+def _inputs(T, H, E, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    router = torch.randn(E, H, generator=g) * 0.02
+    logits = (x.float() @ router.T).to(torch.bfloat16)
+    return x, logits
+
+
+def _bf16(t):
+    return t.detach().to(torch.bfloat16).to(torch.float32).cpu()
+
+
+def test_mixtral_modules_dense_bf16(gpu_device):
+    announce("HybridMoE mixtral modules dense bf16")
+    E, k, H, I, T = 8, 2, 256, 512, 16
+    experts = nn.ModuleDict({str(e): _init(SparseExpertMLP(H, I), e).to(gpu_device, torch.bfloat16)
+                             for e in range(E)})
+    moe = HybridMoE(E, k, H, I, experts, torch.ones(E, dtype=torch.bool), 0, "",
+                    router_use_softmax=MIXTRAL_SPEC.router_use_softmax,
+                    normalize_topk_prob=MIXTRAL_SPEC.normalize_topk_prob,
+                    expert_key_template=MIXTRAL_SPEC.expert_key_template,
+                    expert_proj_names=MIXTRAL_SPEC.expert_proj_names)
+    x, logits = _inputs(T, H, E)
+    out = moe(x.to(gpu_device), logits.to(gpu_device))
+    assert out.shape == (T, H) and out.dtype == torch.bfloat16
+    cfg = MoEConfig("m", H, E, k, I, 0, False, True, "bf16", "bf16")
+    layer = Layer(cfg, torch.zeros(E, H), [
+        {"gate": _bf16(experts[str(e)].w1.weight), "up": _bf16(experts[str(e)].w3.weight),
+         "down": _bf16(experts[str(e)].w2.weight)} for e in range(E)])
+    _check(out, oracle_forward(layer, x, logits))
+    # the routing API returns the reference's (weights in logits dtype, int64 ids)
+    w, ids = moe.route(logits.to(gpu_device))
+    oids, ow = O.route(logits.float().numpy(), k, False, True, True)
+    assert ids.dtype == torch.int64 and np.array_equal(ids.cpu().numpy(), oids)
+    assert w.dtype == torch.bfloat16 and np.array_equal(w.float().cpu().numpy(), ow)
+
+
+def test_qwen3_packed_modules_quantized_int4(gpu_device):
+    announce("HybridMoE qwen3 packed modules int4 at ingest")
+    E, k, H, I, T = 16, 8, 2048, 768, 12
+    experts = nn.ModuleDict({str(e): _init(PackedSparseExpertMLP(H, I), 100 + e).to(gpu_device, torch.bfloat16)
+                             for e in range(E)})
+    moe = HybridMoE(E, k, H, I, experts, torch.ones(E, dtype=torch.bool), 0, "",
+                    router_use_softmax=True, normalize_topk_prob=True, experts_are_packed=True,
+                    expert_key_template=QWEN3_MOE_SPEC.expert_key_template,
+                    expert_proj_names=QWEN3_MOE_SPEC.expert_proj_names, quantization="int4_g128")
+    x, logits = _inputs(T, H, E, seed=1)
+    out = moe(x.to(gpu_device), logits.to(gpu_device))
+    q = lambda w: to_bf16_scales(quantize_symmetric_w4a32(w.detach().float(), group_size=128))
+    layer = Layer(MoEConfig("q", H, E, k, I), torch.zeros(E, H), [
+        {"gate": q(experts[str(e)].gate_up_proj[:I]), "up": q(experts[str(e)].gate_up_proj[I:]),
+         "down": q(experts[str(e)].down_proj.weight)} for e in range(E)])
+    _check(out, oracle_forward(layer, x, logits))
+
+
+def test_safetensors_dense_and_gptq_checkpoints(gpu_device, tmp_path):
+    from safetensors.torch import save_file
+
+    announce("HybridMoE from safetensors: dense mixtral + gptq int4 qwen3")
+    E, k, H, I, T = 8, 2, 256, 256, 9
+    g = torch.Generator().manual_seed(3)
+    dense = {}
+    weights = []
+    for e in range(E):
+        w = {p: (torch.randn(s, generator=g) * 0.02).to(torch.bfloat16)
+             for p, s in (("w1", (I, H)), ("w3", (I, H)), ("w2", (H, I)))}
+        weights.append(w)
+        for p, t in w.items():
+            dense[f"model.layers.0.block_sparse_moe.experts.{e}.{p}.weight"] = t
+    d1 = tmp_path / "dense"
+    d1.mkdir()
+    save_file(dense, str(d1 / "model.safetensors"))
+    mask = torch.zeros(E, dtype=torch.bool)  # nothing in gpu_experts: every expert comes from disk
+    moe = HybridMoE(E, k, H, I, nn.ModuleDict(), mask, 0, str(d1), router_use_softmax=False)
+    x, logits = _inputs(T, H, E, seed=2)
+    out = moe(x.to(gpu_device), logits.to(gpu_device))
+    layer = Layer(MoEConfig("d", H, E, k, I, 0, False, True, "bf16", "bf16"), torch.zeros(E, H), [
+        {"gate": w["w1"].float(), "up": w["w3"].float(), "down": w["w2"].float()} for w in weights])
+    _check(out, oracle_forward(layer, x, logits))
+
+    # GPTQ int4 checkpoint in the on-disk layout: qweight [in/8, out], scales [groups, out]
+    gptq = {}
+    qlayers = []
+    for e in range(E):
+        qe = {}
+        for p, s in (("gate_proj", (I, H)), ("up_proj", (I, H)), ("down_proj", (H, I))):
+            qw = to_bf16_scales(quantize_symmetric_w4a32(torch.randn(s, generator=g) * 0.02, group_size=128))
+            pre = f"model.layers.0.mlp.experts.{e}.{p}"
+            gptq[f"{pre}.qweight"] = qw.qweight.T.contiguous()
+            gptq[f"{pre}.scales"] = qw.scales.T.contiguous().to(torch.float16 if e % 2 else torch.float32)
+            gptq[f"{pre}.g_idx"] = (torch.arange(qw.input_dim) // 128).to(torch.int32)
+            # fp16 scales of bf16 values stay exact only when they are fp16-representable
+            qe[p] = replace(qw, scales=gptq[f"{pre}.scales"].T.float())
+        qlayers.append({"gate": qe["gate_proj"], "up": qe["up_proj"], "down": qe["down_proj"]})
+    d2 = tmp_path / "gptq"
+    d2.mkdir()
+    save_file(gptq, str(d2 / "model.safetensors"))
+    (d2 / "quantize_config.json").write_text(json.dumps({"bits": 4, "group_size": 128, "sym": True}))
+    moe = HybridMoE(E, k, H, I, nn.ModuleDict(), mask, 0, str(d2), router_use_softmax=True,
+                    normalize_topk_prob=True, expert_key_template=QWEN3_MOE_UNPACKED_SPEC.expert_key_template,
+                    expert_proj_names=QWEN3_MOE_UNPACKED_SPEC.expert_proj_names)
+    out = moe(x.to(gpu_device), logits.to(gpu_device))
+    # the device keeps bf16 scales: the oracle sees the same rounding
+    qlayers = [{p: to_bf16_scales(w) for p, w in q.items()} for q in qlayers]
+    layer = Layer(MoEConfig("g", H, E, k, I), torch.zeros(E, H), qlayers)
+    _check(out, oracle_forward(layer, x, logits))
+
+
+def test_shared_expert_int8(gpu_device):
+    announce("HybridMoE qwen2-moe shared expert int8")
+    E, k, H, I, Is, T = 12, 4, 2048, 1408, 5632, 10
+    experts = nn.ModuleDict({str(e): _init(SparseExpertMLP(H, I), 200 + e).to(gpu_device, torch.bfloat16)
+                             for e in range(E)})
+    shared = _init(SparseExpertMLP(H, Is), 7).to(gpu_device, torch.bfloat16)
+    gate = _init(nn.Linear(H, 1, bias=False), 8).to(gpu_device, torch.bfloat16)
+    moe = HybridMoE(E, k, H, I, experts, torch.ones(E, dtype=torch.bool), 0, "", router_use_softmax=True,
+                    normalize_topk_prob=False, quantization="int8_per_channel",
+                    shared_expert=shared, shared_expert_gate=gate)
+    x, logits = _inputs(T, H, E, seed=4)
+    out = moe(x.to(gpu_device), logits.to(gpu_device))
+    q = lambda w: to_bf16_scales(quantize_symmetric_int8_per_channel(w.detach().float()))
+    layer = Layer(MoEConfig("s", H, E, k, I, Is, True, False, "bf16", "int8_per_channel"), torch.zeros(E, H), [
+        {"gate": q(experts[str(e)].w1.weight), "up": q(experts[str(e)].w3.weight),
+         "down": q(experts[str(e)].w2.weight)} for e in range(E)],
+        shared={"gate": q(shared.w1.weight), "up": q(shared.w3.weight), "down": q(shared.w2.weight)},
+        shared_gate=gate.weight.detach().float().reshape(-1).cpu())
+    _check(out, oracle_forward(layer, x, logits))

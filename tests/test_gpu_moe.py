@@ -1,0 +1,157 @@
+"""The MoE layer on the GPU (K1..K5 through nkt_moe_forward) against the oracle.
+
+Tolerances (written here, checked per case): bf16 activations max-abs 2e-2 and
+rel-L2 1e-2; fp32 activations with dense fp32 weights rel-L2 1e-4.  Routing,
+counts and the permutation inside the forward are checked bit-exact."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from moe_cases import CONFIGS, build_inputs, build_layer, native_layer, oracle_forward, tolerances
+
+pytestmark = pytest.mark.gpu
+
+
+def announce(msg):
+    sys.__stderr__.write(f"[gpu-case] {msg}\n")
+    sys.__stderr__.flush()
+
+
+_LAYERS = {}
+
+
+def _layer(name, E=None, I=None, device="cuda"):
+    key = (name, E, I)
+    if key not in _LAYERS:
+        cfg = CONFIGS[name]
+        if I is not None:
+            from dataclasses import replace
+            cfg = replace(cfg, I=I)
+        _LAYERS.clear()  # keep at most one layer's weights alive
+        layer = build_layer(cfg, device=device, num_experts=E)
+        _LAYERS[key] = (layer, native_layer(layer, torch.device(device)))
+    return _LAYERS[key]
+
+
+def _check(layer, native, T, seed=7):
+    cfg = layer.cfg
+    x, logits = build_inputs(layer, T, seed=seed, device="cuda")
+    out = native.forward(x, logits)
+    torch.cuda.synchronize()
+    ref, parts = oracle_forward(layer, x, logits, return_parts=True)
+    # routing inside the forward is bit-exact
+    ids = native.region(T, 0, torch.int32, (T, cfg.k)).cpu().numpy()
+    assert np.array_equal(ids, parts["ids"])
+    perm = native.region(T, 4, torch.int32, (T * cfg.k,)).cpu().numpy()
+    assert np.array_equal(perm, parts["perm"])
+    got = out.float().cpu().numpy()
+    if cfg.act == "bf16":
+        ref_cast = O.bf16_round(ref)
+    else:
+        ref_cast = ref
+    max_abs, rel = tolerances(cfg)
+    err_abs = float(np.max(np.abs(got - ref_cast))) if got.size else 0.0
+    err_rel = O.rel_l2(got, ref)
+    announce(f"  {cfg.name} T={T}: max_abs={err_abs:.3e} rel_l2={err_rel:.3e}")
+    assert err_abs <= max_abs, f"max-abs {err_abs} > {max_abs}"
+    assert err_rel <= rel, f"rel-L2 {err_rel} > {rel}"
+    return out
+
+
+@pytest.mark.parametrize("T", [1, 16, 100])
+def test_tiny_mixtral_fp32(gpu_device, T):
+    announce(f"forward tiny_mixtral_fp32 T={T}")
+    layer, native = _layer("tiny_mixtral_fp32")
+    _check(layer, native, T)
+
+
+@pytest.mark.parametrize("T", [1, 4, 16, 64, 300])
+def test_qwen3_int4_cut_experts(gpu_device, T):
+    announce(f"forward qwen3_int4 E=32 T={T}")
+    layer, native = _layer("qwen3_int4", E=32)
+    _check(layer, native, T)
+
+
+@pytest.mark.parametrize("T", [1, 16])
+def test_qwen3_int4_full(gpu_device, T):
+    announce(f"forward qwen3_int4 full T={T}")
+    layer, native = _layer("qwen3_int4")
+    _check(layer, native, T)
+
+
+@pytest.mark.parametrize("T", [16, 200, 512])
+def test_qwen3_int8_cut_experts(gpu_device, T):
+    announce(f"forward qwen3_int8 E=32 T={T}")
+    layer, native = _layer("qwen3_int8", E=32)
+    _check(layer, native, T)
+
+
+def test_qwen3_int8_full_prefill(gpu_device):
+    announce("forward qwen3_int8 full T=2048")
+    layer, native = _layer("qwen3_int8")
+    _check(layer, native, 2048)
+
+
+def test_qwen3_int8_batch_invariance_at_4096(gpu_device):
+    """Full-size property: a token's output does not depend on the other tokens in the batch
+    (each output element accumulates over K in the same order whatever the tile)."""
+    announce("forward qwen3_int8 full T=4096 batch invariance")
+    layer, native = _layer("qwen3_int8")
+    x, logits = build_inputs(layer, 4096, seed=21, device="cuda")
+    full = native.forward(x, logits).clone()
+    part = native.forward(x[:97].contiguous(), logits[:97].contiguous()).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(full[:97], part)
+    # and the first 97 tokens agree with the oracle
+    ref = oracle_forward(layer, x[:97], logits[:97])
+    assert O.rel_l2(part.float().cpu().numpy(), ref) < 1e-2
+
+
+@pytest.mark.parametrize("T", [1, 16])
+def test_mixtral_int4_full(gpu_device, T):
+    announce(f"forward mixtral_int4 full T={T}")
+    layer, native = _layer("mixtral_int4")
+    _check(layer, native, T)
+
+
+def test_mixtral_int4_cut_intermediate_prefill(gpu_device):
+    announce("forward mixtral_int4 I=1024 T=300")
+    layer, native = _layer("mixtral_int4", I=1024)
+    _check(layer, native, 300)
+
+
+@pytest.mark.parametrize("T", [1, 16, 200])
+def test_qwen15_shared_full(gpu_device, T):
+    announce(f"forward qwen15_int8_shared full T={T}")
+    layer, native = _layer("qwen15_int8_shared")
+    _check(layer, native, T)
+
+
+def test_forward_deterministic(gpu_device):
+    announce("forward determinism qwen3_int4 E=32 T=64")
+    layer, native = _layer("qwen3_int4", E=32)
+    x, logits = build_inputs(layer, 64, seed=3, device="cuda")
+    a = native.forward(x, logits).clone()
+    for _ in range(3):
+        b = native.forward(x, logits)
+        assert torch.equal(a, b)
+
+
+def test_stages_match_forward(gpu_device):
+    """route -> experts -> shared -> combine through the separate entry points equals forward."""
+    announce("stages vs forward qwen15_int8_shared T=16")
+    layer, native = _layer("qwen15_int8_shared")
+    x, logits = build_inputs(layer, 16, seed=9, device="cuda")
+    a = native.forward(x, logits).clone()
+    native.route(logits)
+    h, y = native.experts(x)
+    gate, ysh = native.shared(x)
+    b = native.combine(16)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    # K4 alone: sigmoid(x . g)
+    ref_gate = torch.sigmoid(x.float().cpu() @ layer.shared_gate.cpu())
+    assert torch.allclose(gate.cpu(), ref_gate, rtol=1e-5, atol=1e-6)

@@ -1,0 +1,105 @@
+"""K1 + K2 on the GPU against the oracle: routing ids and weights, per-expert counts,
+offsets and the permutation must be bit-exact."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from moe_cases import CONFIGS, build_inputs, build_layer
+
+pytestmark = pytest.mark.gpu
+
+
+def announce(msg):
+    sys.__stderr__.write(f"[gpu-case] {msg}\n")
+    sys.__stderr__.flush()
+
+
+def _router_only(E, k, softmax, renorm, act_dtype, device, max_tokens=8192):
+    from nano_ktrans_amd.native_moe import NativeMoE
+
+    wfmt = "f32" if act_dtype == torch.float32 else "bf16"
+    return NativeMoE(num_experts=E, top_k=k, hidden_size=128, intermediate_size=128, weight_format=wfmt,
+                     act_dtype=act_dtype, use_softmax=softmax, renorm=renorm, max_tokens=max_tokens,
+                     device=device)
+
+
+def _check_route(native, logits, k, softmax, renorm, bf16):
+    E = logits.shape[1]
+    ids, w, counts, offsets, perm, inv = native.route(logits)
+    torch.cuda.synchronize()
+    oids, ow = O.route(logits.float().cpu().numpy(), k, softmax, renorm, bf16)
+    ocounts, ooffsets, operm, oinv = O.group(oids, E)
+    g_ids = ids.cpu().numpy()
+    g_w = w.cpu().numpy()
+    bad = np.argwhere(g_ids != oids)
+    assert bad.size == 0, f"ids differ at {bad[:5].tolist()}: gpu {g_ids[bad[0][0]]} oracle {oids[bad[0][0]]}"
+    assert np.array_equal(g_w.view(np.uint32), ow.view(np.uint32)), \
+        f"weights differ: max |d| = {np.max(np.abs(g_w - ow))}"
+    assert np.array_equal(counts.cpu().numpy(), ocounts)
+    assert np.array_equal(offsets.cpu().numpy(), ooffsets)
+    assert np.array_equal(perm.cpu().numpy(), operm)
+    assert np.array_equal(inv.cpu().numpy(), oinv)
+
+
+@pytest.mark.parametrize("name,T", [
+    ("tiny_mixtral_fp32", 16), ("tiny_mixtral_fp32", 1),
+    ("qwen3_int4", 1), ("qwen3_int4", 4), ("qwen3_int4", 16),
+    ("qwen3_int8", 512), ("qwen3_int8", 4096),
+    ("mixtral_int4", 1), ("mixtral_int4", 16), ("mixtral_int4", 2048),
+    ("qwen15_int8_shared", 1), ("qwen15_int8_shared", 16), ("qwen15_int8_shared", 1024),
+])
+def test_route_matches_oracle_on_benchmark_configs(gpu_device, name, T):
+    cfg = CONFIGS[name]
+    announce(f"route {name} T={T}")
+    # the router weights are all routing needs: build them alone
+    g = torch.Generator().manual_seed(cfg.seed)
+    router = torch.randn(cfg.E, cfg.H, generator=g) * 0.02
+    from moe_cases import Layer
+    layer = Layer(cfg, router, [])
+    x, logits = build_inputs(layer, T, seed=100 + T)
+    native = _router_only(cfg.E, cfg.k, cfg.softmax, cfg.renorm, cfg.act_dtype, gpu_device)
+    _check_route(native, logits.to(gpu_device), cfg.k, cfg.softmax, cfg.renorm, cfg.act == "bf16")
+
+
+@pytest.mark.parametrize("E,k", [(8, 1), (8, 2), (60, 4), (64, 8), (100, 6), (128, 8), (128, 16), (256, 8)])
+@pytest.mark.parametrize("softmax,renorm", [(True, True), (True, False), (False, True)])
+@pytest.mark.parametrize("act_dtype", [torch.bfloat16, torch.float32])
+def test_route_ties_and_edges(gpu_device, E, k, softmax, renorm, act_dtype):
+    announce(f"route edges E={E} k={k} softmax={softmax} renorm={renorm} {act_dtype}")
+    rng = np.random.default_rng(E * 100 + k)
+    T = 97
+    cases = []
+    # heavy ties: logits on a coarse grid
+    cases.append(np.round(rng.standard_normal((T, E)) * 2) / 2)
+    # all equal
+    cases.append(np.zeros((5, E)))
+    # one hot
+    oh = np.zeros((min(E, 40), E))
+    oh[np.arange(oh.shape[0]), np.arange(oh.shape[0])] = 5.0
+    cases.append(oh)
+    # very wide spread: exp underflows to subnormals and zero
+    cases.append(rng.standard_normal((T, E)) * 60.0)
+    # signed zeros and negatives
+    z = np.zeros((3, E))
+    z[:, ::2] = -0.0
+    z[:, 1] = -1.0
+    cases.append(z)
+    native = _router_only(E, k, softmax, renorm, act_dtype, gpu_device)
+    for c in cases:
+        logits = torch.from_numpy(c.astype(np.float32)).to(act_dtype).to(gpu_device)
+        _check_route(native, logits, k, softmax, renorm, act_dtype == torch.bfloat16)
+
+
+def test_route_repeatable(gpu_device):
+    announce("route repeatable")
+    native = _router_only(128, 8, True, True, torch.bfloat16, gpu_device)
+    logits = (torch.randn(4096, 128, generator=torch.Generator().manual_seed(5)) * 0.9).to(torch.bfloat16)
+    logits = logits.to(gpu_device)
+    first = [t.clone() for t in native.route(logits)]
+    for _ in range(3):
+        again = native.route(logits)
+        for a, b in zip(first, again):
+            assert torch.equal(a, b)
