@@ -159,3 +159,32 @@ def tolerances(cfg: MoEConfig):
     if cfg.act == "f32":
         return math.inf, 1e-4
     return 2e-2, 1e-2
+
+
+def bf16_ulp(x: np.ndarray) -> np.ndarray:
+    """Spacing of bf16 values at |x| (8 significant bits)."""
+    _, ex = np.frexp(np.abs(np.asarray(x, dtype=np.float64)))
+    return np.ldexp(1.0, ex - 8)
+
+
+def compare(got: np.ndarray, ref: np.ndarray, cfg: MoEConfig):
+    """Check a GPU output against the oracle's fp32 result.
+
+    bf16 outputs: every element within max(2e-2, one bf16 ulp of the oracle value) of the
+    oracle rounded to bf16 -- where |y| >= 4 one bf16 ulp exceeds 2e-2, so a single flip of
+    the final rounding must be allowed there -- and rel-L2 <= 1e-2 against the fp32 oracle.
+    fp32 outputs: rel-L2 <= 1e-4.  Returns (max-abs vs the rounded oracle, rel-L2)."""
+    got = np.asarray(got, dtype=np.float32)
+    if cfg.act == "f32":
+        rel = O.rel_l2(got, ref)
+        assert rel <= 1e-4, f"rel-L2 {rel} > 1e-4"
+        return float(np.max(np.abs(got - ref))) if got.size else 0.0, rel
+    ref_b = O.bf16_round(ref)
+    d = np.abs(got.astype(np.float64) - ref_b)
+    bound = np.maximum(2e-2, bf16_ulp(ref_b))
+    worst = np.unravel_index(np.argmax(d - bound), d.shape) if d.size else None
+    assert d.size == 0 or np.all(d <= bound), \
+        f"|d|={d[worst]} > {bound[worst]} at {worst} (ref {ref_b[worst]}, got {got[worst]})"
+    rel = O.rel_l2(got, ref)
+    assert rel <= 1e-2, f"rel-L2 {rel} > 1e-2"
+    return float(np.max(d)) if d.size else 0.0, rel
