@@ -219,18 +219,35 @@ int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, 
   }
   int32_t* ids = ws_ptr<int32_t>(ws, L, NKT_WS_TOPK_IDS);
   float* wts = ws_ptr<float>(ws, L, NKT_WS_TOPK_WEIGHTS);
+  int32_t* counts = ws_ptr<int32_t>(ws, L, NKT_WS_COUNTS);
+  int32_t* offsets = ws_ptr<int32_t>(ws, L, NKT_WS_OFFSETS);
+  int32_t* perm = ws_ptr<int32_t>(ws, L, NKT_WS_PERM);
+  int32_t* inv = ws_ptr<int32_t>(ws, L, NKT_WS_INV);
+  int32_t* tiles = ws_ptr<int32_t>(ws, L, kWsTiles);
+  int32_t* n_tiles = ws_ptr<int32_t>(ws, L, kWsNTiles);
+  if (route_group_fused(T, h->k)) {
+    if (!check_hip(launch_route_group(logits, h->act_bf16, T, h->E, h->k, h->flags, L.bm, L.max_tiles,
+                                      ids, wts, counts, offsets, perm, inv, tiles, n_tiles, st),
+                   "route+group kernel", err, len))
+      return NKT_ERR;
+    return NKT_OK;
+  }
   if (!check_hip(launch_route(logits, h->act_bf16, T, h->E, h->k, h->flags, ids, wts, st),
                  "route kernel", err, len))
     return NKT_ERR;
-  if (!check_hip(launch_group(ids, T, h->k, h->E, L.bm, L.max_tiles,
-                              ws_ptr<int32_t>(ws, L, NKT_WS_COUNTS),
-                              ws_ptr<int32_t>(ws, L, NKT_WS_OFFSETS),
-                              ws_ptr<int32_t>(ws, L, NKT_WS_PERM),
-                              ws_ptr<int32_t>(ws, L, NKT_WS_INV), ws_ptr<int32_t>(ws, L, kWsTiles),
-                              ws_ptr<int32_t>(ws, L, kWsNTiles), st),
+  if (!check_hip(launch_group(ids, T, h->k, h->E, L.bm, L.max_tiles, counts, offsets, perm, inv, tiles,
+                              n_tiles, st),
                  "group kernel", err, len))
     return NKT_ERR;
   return NKT_OK;
+}
+
+// K3 launch for one projection: the decode form for tiles of at most 16
+// positions, the tiled MFMA form otherwise.
+hipError_t launch_expert_gemm(const Handle* h, const GemmArgs& a, int phase, int bm, int tiles,
+                              hipStream_t st) {
+  if (bm == 16 && gemv_supported(h->wf, phase, a.N, a.K, a.I)) return launch_gemv(a, h->wf, phase, tiles, st);
+  return launch_gemm(a, h->wf, phase, bm, tiles, st);
 }
 
 int do_expert_phase(Handle* h, int phase, const void* x, int T, void* ws, const WsLayout& L,
@@ -242,11 +259,11 @@ int do_expert_phase(Handle* h, int phase, const void* x, int T, void* ws, const 
   if (!check_weights(h, false, err, len)) return NKT_ERR;
   if (phase == PHASE_GATE_UP) {
     GemmArgs a = expert_args(h, PHASE_GATE_UP, false, x, ws, L, T);
-    if (!check_hip(launch_gemm(a, h->wf, PHASE_GATE_UP, L.bm, L.max_tiles, st), "gate_up gemm", err, len))
+    if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, L.bm, L.max_tiles, st), "gate_up gemm", err, len))
       return NKT_ERR;
   } else {
     GemmArgs b = expert_args(h, PHASE_DOWN, false, ws_ptr<void>(ws, L, NKT_WS_H), ws, L, T);
-    if (!check_hip(launch_gemm(b, h->wf, PHASE_DOWN, L.bm, L.max_tiles, st), "down gemm", err, len))
+    if (!check_hip(launch_expert_gemm(h, b, PHASE_DOWN, L.bm, L.max_tiles, st), "down gemm", err, len))
       return NKT_ERR;
   }
   return NKT_OK;
@@ -276,10 +293,10 @@ int do_shared(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipS
   const int bm = gemm_tile_m(T, 1, 1);
   const int tiles = (T + bm - 1) / bm;
   GemmArgs a = expert_args(h, PHASE_GATE_UP, true, x, ws, L, T);
-  if (!check_hip(launch_gemm(a, h->wf, PHASE_GATE_UP, bm, tiles, st), "shared gate_up gemm", err, len))
+  if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, bm, tiles, st), "shared gate_up gemm", err, len))
     return NKT_ERR;
   GemmArgs b = expert_args(h, PHASE_DOWN, true, ws_ptr<void>(ws, L, NKT_WS_SHARED_H), ws, L, T);
-  if (!check_hip(launch_gemm(b, h->wf, PHASE_DOWN, bm, tiles, st), "shared down gemm", err, len))
+  if (!check_hip(launch_expert_gemm(h, b, PHASE_DOWN, bm, tiles, st), "shared down gemm", err, len))
     return NKT_ERR;
   return NKT_OK;
 }

@@ -31,44 +31,42 @@ __global__ void __launch_bounds__(256) shared_gate_kernel(const void* __restrict
   if (lane == 0) out[t] = 1.0f / (1.0f + __expf(-s));
 }
 
+// One workgroup per (token, 1024-column slice); one thread per 4 columns.
+template <int K>
 __global__ void __launch_bounds__(256) combine_kernel(
     const float* __restrict__ y, const int32_t* __restrict__ ids, const float* __restrict__ w,
     const int32_t* __restrict__ inv, const float* __restrict__ y_shared,
-    const float* __restrict__ shared_gate, int num_tokens, int k, int H, void* __restrict__ out,
+    const float* __restrict__ shared_gate, int num_tokens, int H, void* __restrict__ out,
     int out_bf16) {
   const int t = blockIdx.x;
+  const int c = blockIdx.y * blockDim.x + threadIdx.x;  // float4 column index
   // order the token's slots by expert id: rank[j] = #{i : id_i < id_j}
   // (ids of one token are distinct), then gather by rank with static indices
-  int sid[kMaxTopK], spos[kMaxTopK], rank[kMaxTopK];
-  float sw[kMaxTopK];
+  int sid[K], spos[K], rank[K];
+  float sw[K];
 #pragma unroll
-  for (int j = 0; j < kMaxTopK; ++j) {
-    sid[j] = 0x7fffffff;
-    spos[j] = 0;
-    sw[j] = 0.f;
-    if (j < k) {
-      sid[j] = ids[(int64_t)t * k + j];
-      // positions index y [T*k, H]; keep a corrupt entry from reading outside it
-      spos[j] = min(max(inv[(int64_t)t * k + j], 0), num_tokens * k - 1);
-      sw[j] = w[(int64_t)t * k + j];
-    }
+  for (int j = 0; j < K; ++j) {
+    sid[j] = ids[(int64_t)t * K + j];
+    // positions index y [T*K, H]; keep a corrupt entry from reading outside it
+    spos[j] = min(max(inv[(int64_t)t * K + j], 0), num_tokens * K - 1);
+    sw[j] = w[(int64_t)t * K + j];
   }
 #pragma unroll
-  for (int j = 0; j < kMaxTopK; ++j) {
+  for (int j = 0; j < K; ++j) {
     int r = 0;
 #pragma unroll
-    for (int i = 0; i < kMaxTopK; ++i) r += (sid[i] < sid[j]) ? 1 : 0;
+    for (int i = 0; i < K; ++i) r += (sid[i] < sid[j]) ? 1 : 0;
     rank[j] = r;
   }
-  int order_pos[kMaxTopK];
-  float order_w[kMaxTopK];
+  int order_pos[K];
+  float order_w[K];
 #pragma unroll
-  for (int r = 0; r < kMaxTopK; ++r) {
+  for (int r = 0; r < K; ++r) {
     int p = 0;
     float wt = 0.f;
 #pragma unroll
-    for (int j = 0; j < kMaxTopK; ++j) {
-      if (j < k && rank[j] == r) {
+    for (int j = 0; j < K; ++j) {
+      if (rank[j] == r) {
         p = spos[j];
         wt = sw[j];
       }
@@ -76,30 +74,28 @@ __global__ void __launch_bounds__(256) combine_kernel(
     order_pos[r] = p;
     order_w[r] = wt;
   }
-  const int n = k;
-  const float sg = shared_gate ? shared_gate[t] : 0.f;
-  const int H4 = H / 4;
-  for (int c = threadIdx.x; c < H4; c += blockDim.x) {
-    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (4 * c >= H) return;
+  // every load first, then the fixed-order sum
+  f32x4 v[K];
 #pragma unroll
-    for (int j = 0; j < kMaxTopK; ++j) {
-      if (j < n) {
-        const f32x4 v = *(const f32x4*)(y + (int64_t)order_pos[j] * H + 4 * c);
-        acc += order_w[j] * v;
-      }
-    }
-    if (y_shared) {
-      const f32x4 v = *(const f32x4*)(y_shared + (int64_t)t * H + 4 * c);
-      acc += sg * v;
-    }
-    if (out_bf16) {
-      u32x2 pk;
-      pk[0] = pack_bf16x2(acc[0], acc[1]);
-      pk[1] = pack_bf16x2(acc[2], acc[3]);
-      *(u32x2*)((uint16_t*)out + (int64_t)t * H + 4 * c) = pk;
-    } else {
-      *(f32x4*)((float*)out + (int64_t)t * H + 4 * c) = acc;
-    }
+  for (int j = 0; j < K; ++j) v[j] = *(const f32x4*)(y + (int64_t)order_pos[j] * H + 4 * c);
+  f32x4 vs = f32x4{0.f, 0.f, 0.f, 0.f};
+  float sg = 0.f;
+  if (y_shared) {
+    vs = *(const f32x4*)(y_shared + (int64_t)t * H + 4 * c);
+    sg = shared_gate[t];
+  }
+  f32x4 acc = order_w[0] * v[0];
+#pragma unroll
+  for (int j = 1; j < K; ++j) acc += order_w[j] * v[j];
+  if (y_shared) acc += sg * vs;
+  if (out_bf16) {
+    u32x2 pk;
+    pk[0] = pack_bf16x2(acc[0], acc[1]);
+    pk[1] = pack_bf16x2(acc[2], acc[3]);
+    *(u32x2*)((uint16_t*)out + (int64_t)t * H + 4 * c) = pk;
+  } else {
+    *(f32x4*)((float*)out + (int64_t)t * H + 4 * c) = acc;
   }
 }
 
@@ -115,8 +111,33 @@ hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, co
                           const float* y_shared, const float* shared_gate, int T, int k, int H,
                           void* out, int out_bf16, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, stream, y, ids, w, inv, y_shared,
-                     shared_gate, T, k, H, out, out_bf16);
+  dim3 grid(T, (H / 4 + 255) / 256), block(256);
+#define NKT_COMBINE_CASE(KK)                                                                   \
+  case KK:                                                                                     \
+    hipLaunchKernelGGL(combine_kernel<KK>, grid, block, 0, stream, y, ids, w, inv, y_shared,   \
+                       shared_gate, T, H, out, out_bf16);                                      \
+    break;
+  switch (k) {
+    NKT_COMBINE_CASE(1)
+    NKT_COMBINE_CASE(2)
+    NKT_COMBINE_CASE(3)
+    NKT_COMBINE_CASE(4)
+    NKT_COMBINE_CASE(5)
+    NKT_COMBINE_CASE(6)
+    NKT_COMBINE_CASE(7)
+    NKT_COMBINE_CASE(8)
+    NKT_COMBINE_CASE(9)
+    NKT_COMBINE_CASE(10)
+    NKT_COMBINE_CASE(11)
+    NKT_COMBINE_CASE(12)
+    NKT_COMBINE_CASE(13)
+    NKT_COMBINE_CASE(14)
+    NKT_COMBINE_CASE(15)
+    NKT_COMBINE_CASE(16)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef NKT_COMBINE_CASE
   return hipGetLastError();
 }
 

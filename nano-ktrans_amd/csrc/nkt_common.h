@@ -14,6 +14,9 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 constexpr int kWave = 64;
 constexpr int kMaxExperts = 256;  // router: at most 4 logits per lane
 constexpr int kMaxTopK = 16;
+// route + group in one workgroup up to this many tokens / (token, slot) pairs
+constexpr int kFusedRouteMaxTokens = 64;
+constexpr int kFusedRouteMaxPairs = 1024;
 
 // Weight formats (values match NKT_WEIGHT_* in include/nkt_moe.h).
 enum WeightFormat : int { WF_F32 = 0, WF_BF16 = 1, WF_I8 = 2, WF_I4 = 3 };

@@ -1,0 +1,342 @@
+// K3, decode form: grouped SwiGLU expert GEMM for tiles of at most 16
+// positions (decode-sized groups).
+//
+// Replaces, for small batches, the per-routed-expert loop of
+// nano_ktrans/layers/hybrid_moe.py:3501-3533 (SparseExpertMLP /
+// PackedSparseExpertMLP.forward, nano_ktrans/layers/expert_mlp.py:20-41) and
+// the quantized loop of nano_ktrans/kernels/cpu_moe.py:419-450.
+//
+// One wave owns one (tile, row set, K part): a tile is up to 16 positions of
+// one expert, a row set is RT 16-row output tiles (gate_up: RT gate tiles and
+// the RT matching up tiles, so SwiGLU is local), the K part is every S-th
+// 128-wide K group.  The wave reads its weight blocks straight from HBM, one
+// 16-byte load per lane per 1 KiB block.  Normally K is split over S waves
+// of one workgroup so that each wave owns two groups and issues all of their
+// loads at once (many short waves stream HBM better than few long ones); for
+// long K the wave streams its groups through a D-deep register ring whose
+// refills are issued right after the slot is consumed, always (past the last
+// group they re-read it, an L2 hit), so the loop has no branch, store or
+// barrier.  The matrix core takes the weights as the A operand and the tile's
+// activations, loaded in the B-operand lane layout, as B.  The S partial sums
+// meet in LDS and are added in K-part order.
+//
+// Dequantisation is the same as the prefill kernel's: codes enter the matrix
+// core as exact bf16 integers with an offset (int4: 136 + q, int8: 128 + q),
+// the offset times the group's activation sum is removed per group, the bf16
+// scale multiplies each group's fp32 partial (int4) or the row total (int8).
+#include "nkt_common.h"
+#include "nkt_internal.h"
+
+namespace nkt {
+
+// 16-row output tiles per wave
+constexpr int kGemvRtGateUp = 1;
+constexpr int kGemvRtDown = 2;
+
+namespace {
+
+__device__ __forceinline__ u32x4 dq_i4(uint32_t w) {
+  u32x4 a;
+  a[0] = (w & 0x000F000Fu) | 0x43004300u;
+  a[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
+  a[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
+  a[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  return a;
+}
+
+__device__ __forceinline__ uint32_t bf16pair_u8(uint32_t w, int lo_byte) {
+  const float f0 = (float)((w >> (8 * lo_byte)) & 0xffu);
+  const float f1 = (float)((w >> (8 * lo_byte + 8)) & 0xffu);
+  return __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+}
+
+__device__ __forceinline__ u32x4 dq_i8(uint32_t w0, uint32_t w1) {
+  u32x4 a;
+  a[0] = bf16pair_u8(w0, 0);
+  a[1] = bf16pair_u8(w0, 2);
+  a[2] = bf16pair_u8(w1, 0);
+  a[3] = bf16pair_u8(w1, 2);
+  return a;
+}
+
+__device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
+
+__device__ __forceinline__ f32x4 bf16x4_to_f32(u32x2 v) {
+  return f32x4{__uint_as_float(v[0] << 16), __uint_as_float(v[0] & 0xffff0000u),
+               __uint_as_float(v[1] << 16), __uint_as_float(v[1] & 0xffff0000u)};
+}
+
+// One ring slot: one K group of NT weight tiles (+ int4 scales) and the
+// lane's token activations for the group's 4 MFMA steps.
+template <int WF, int NT>
+struct Slot {
+  static constexpr int NBLK = 128 / block_k(WF);
+  u32x4 w[NT][NBLK];
+  u32x2 s[NT];
+  u32x4 x[4];
+};
+
+// Weight loads address a uniform per-expert base plus a 32-bit offset
+// (global_load ... saddr form: one offset register per load).
+template <int WF, int NT>
+__device__ __forceinline__ void load_slot(Slot<WF, NT>& r, const uint8_t* wexp, const uint16_t* sexp,
+                                          const uint32_t (&rbo)[NT], const uint32_t (&sbo)[NT],
+                                          const uint8_t* xrow, int g, uint32_t lane) {
+  constexpr int NBLK = Slot<WF, NT>::NBLK;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+#pragma unroll
+    for (int i = 0; i < NBLK; ++i)
+      r.w[t][i] = *(const u32x4*)(wexp + (rbo[t] + (uint32_t)(g * NBLK + i) * 1024u + lane * 16u));
+    if (WF == WF_I4) r.s[t] = *(const u32x2*)(sexp + (sbo[t] + (uint32_t)g * 16u + 4u * (lane >> 4)));
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) r.x[s] = *(const u32x4*)(xrow + (g * 128 + 32 * s) * 2);
+}
+
+// Adds one group's contribution to acc; use == false computes it and adds
+// nothing (a select, so no load is ever control-dependent).
+template <int WF, int NT>
+__device__ __forceinline__ void compute_slot(const Slot<WF, NT>& r, f32x4 (&acc)[NT], bool use) {
+  constexpr bool IS_INT = WF == WF_I4 || WF == WF_I8;
+  float xs = 0.f;
+  if (IS_INT) {
+    // sum of the group's 128 activations of the lane's token (lanes l, l^16,
+    // l^32, l^48 hold its four 32-wide quarters)
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        xs += __uint_as_float(r.x[s][h] << 16);
+        xs += __uint_as_float(r.x[s][h] & 0xffff0000u);
+      }
+    xs += __shfl_xor(xs, 16);
+    xs += __shfl_xor(xs, 32);
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    f32x4 tmp;
+    if (WF == WF_I4) {
+      const float c = -136.0f * xs;
+      tmp = f32x4{c, c, c, c};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) tmp = mfma_bf16(dq_i4(r.w[t][0][s]), r.x[s], tmp);
+      tmp = bf16x4_to_f32(r.s[t]) * tmp;
+    } else if (WF == WF_I8) {
+      const float c = -128.0f * xs;
+      tmp = f32x4{c, c, c, c};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        tmp = mfma_bf16(dq_i8(r.w[t][s >> 1][2 * (s & 1)], r.w[t][s >> 1][2 * (s & 1) + 1]), r.x[s], tmp);
+    } else {
+      tmp = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) tmp = mfma_bf16(r.w[t][s], r.x[s], tmp);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[t][v] = use ? acc[t][v] + tmp[v] : acc[t][v];
+  }
+}
+
+}  // namespace
+
+// Waves per workgroup: S K-parts of P row sets.
+__host__ __device__ constexpr int gemv_rowsets_per_wg(int S) { return S == 1 ? 4 : S == 2 ? 2 : 1; }
+
+// Grid: x = blocks of P row sets, y = tile slots (a slot past the routed tile
+// count exits at once).  NG > 0: each wave issues the loads of all its (at
+// most NG) groups at once and then consumes them; NG == 0: each wave streams
+// its groups through the D-deep ring.
+template <int WF, int PHASE, int RT, int S, int NG, int D>
+__global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(GemmArgs a, int n_rowsets) {
+  constexpr int P = gemv_rowsets_per_wg(S);
+  constexpr int NT = (PHASE == PHASE_GATE_UP) ? 2 * RT : RT;
+  __shared__ f32x4 red[S > 1 ? S * P : 1][NT][64];
+
+  const int tile = blockIdx.y;
+  const int n_tiles = a.n_tiles ? a.n_tiles[0] : (a.num_rows + 15) / 16;
+  if (tile >= n_tiles) return;
+
+  const uint32_t lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int kpart = wave % S;
+  const int rs_raw = blockIdx.x * P + wave / S;
+  const bool rs_ok = rs_raw < n_rowsets;
+  const int rowset = rs_ok ? rs_raw : 0;
+  const int G = a.K / 128;
+  const int NKB = a.K / block_k(WF);
+
+  int expert, row0, rows;
+  if (a.n_tiles) {
+    const int4 rec = *(const int4*)(a.tiles + 4 * tile);
+    expert = rec.x;
+    row0 = rec.y;
+    rows = rec.z;
+  } else {
+    expert = 0;
+    row0 = tile * 16;
+    rows = min(16, a.num_rows - row0);
+  }
+  const int col = lane & 15;
+  int src = row0 + (col < rows ? col : 0);
+  if (a.perm) src = a.perm[src] / a.topk;
+  const uint8_t* xrow = (const uint8_t*)a.in + (int64_t)src * a.K * 2 + 16 * (lane >> 4);
+
+  const uint8_t* wexp = a.w + (int64_t)expert * a.w_expert_bytes;
+  const uint16_t* sexp = a.scales + (int64_t)expert * a.s_expert_elems;
+  const int orow0 = rowset * RT * 16;  // first output row of the row set
+  uint32_t rbo[NT], sbo[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int wrow = (PHASE == PHASE_GATE_UP) ? (t < RT ? orow0 + 16 * t : a.I + orow0 + 16 * (t - RT))
+                                              : orow0 + 16 * t;
+    const uint32_t rb = (uint32_t)(wrow >> 4);
+    rbo[t] = rb * (uint32_t)NKB * 1024u;
+    sbo[t] = rb * (uint32_t)G * 16u;
+  }
+
+  // this wave's groups: kpart + S*i, i < n
+  const int n = kpart < G ? (G - kpart + S - 1) / S : 0;
+  const int n_last = n > 0 ? n - 1 : 0;
+  const int g_base = kpart < G ? kpart : 0;
+
+  f32x4 acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (NG > 0) {
+    Slot<WF, NT> sl[NG > 0 ? NG : 1];
+#pragma unroll
+    for (int i = 0; i < NG; ++i)
+      load_slot<WF, NT>(sl[i], wexp, sexp, rbo, sbo, xrow, g_base + S * min(i, n_last), lane);
+    __builtin_amdgcn_sched_barrier(0);  // every load above the first use
+#pragma unroll
+    for (int i = 0; i < NG; ++i) compute_slot<WF, NT>(sl[i], acc, i < n);
+  } else {
+    Slot<WF, NT> ring[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+      load_slot<WF, NT>(ring[d], wexp, sexp, rbo, sbo, xrow, g_base + S * min(d, n_last), lane);
+    // sched_barrier: the scheduler would otherwise sink each refill down to
+    // its use in the next iteration (shorter live ranges, no latency hiding)
+    __builtin_amdgcn_sched_barrier(0);
+    for (int i0 = 0; i0 < n; i0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        compute_slot<WF, NT>(ring[d], acc, i0 + d < n);
+        __builtin_amdgcn_sched_barrier(0);
+        load_slot<WF, NT>(ring[d], wexp, sexp, rbo, sbo, xrow, g_base + S * min(i0 + d + D, n_last), lane);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+
+  if (S > 1) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) red[S > 1 ? wave : 0][t][lane] = acc[t];
+    __syncthreads();
+    if (kpart != 0) return;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f32x4 s = red[S > 1 ? wave : 0][t][lane];
+#pragma unroll
+      for (int k = 1; k < S; ++k) s += red[S > 1 ? wave + k : 0][t][lane];
+      acc[t] = s;
+    }
+  }
+  if (!rs_ok) return;
+
+  const int t_out = lane & 15;
+  if (t_out >= rows) return;
+  const int64_t pos = row0 + t_out;
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    const int orow = orow0 + 16 * r + 4 * (lane >> 4);
+    f32x4 s0 = acc[r];
+    if (PHASE == PHASE_GATE_UP) {
+      f32x4 s1 = acc[RT + r];
+      if (WF == WF_I8) {
+        s0 *= bf16x4_to_f32(*(const u32x2*)(sexp + orow));
+        s1 *= bf16x4_to_f32(*(const u32x2*)(sexp + a.I + orow));
+      }
+      float h[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) h[v] = silu(s0[v]) * s1[v];
+      u32x2 pk;
+      pk[0] = pack_bf16x2(h[0], h[1]);
+      pk[1] = pack_bf16x2(h[2], h[3]);
+      *(u32x2*)((uint16_t*)a.out + pos * a.I + orow) = pk;
+    } else {
+      if (WF == WF_I8) s0 *= bf16x4_to_f32(*(const u32x2*)(sexp + orow));
+      *(f32x4*)((float*)a.out + pos * a.N + orow) = s0;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// launch
+// ---------------------------------------------------------------------------
+namespace {
+
+template <int WF, int PHASE, int RT, int S, int NG>
+hipError_t launch_gemv_s(const GemmArgs& a, int max_tiles, int n_rowsets, hipStream_t stream) {
+  constexpr int P = gemv_rowsets_per_wg(S);
+  constexpr int D = (WF == WF_BF16) ? 2 : 3;
+  dim3 grid((n_rowsets + P - 1) / P, max_tiles);
+  hipLaunchKernelGGL((gemv_kernel<WF, PHASE, RT, S, NG, D>), grid, dim3(S * P * 64), 0, stream, a, n_rowsets);
+  return hipGetLastError();
+}
+
+// Every wave takes kGemvGroupsPerWave K groups, all loads in flight at once
+// (many short waves stream HBM better than few long ones); K too long for
+// eight such waves streams through the ring instead.
+constexpr int kGemvGroupsPerWave = 2;
+
+template <int WF, int PHASE, int RT>
+hipError_t launch_gemv_rt(const GemmArgs& a, int max_tiles, hipStream_t stream) {
+  const int out_dim = (PHASE == PHASE_GATE_UP) ? a.I : a.N;
+  const int n_rowsets = out_dim / (RT * 16);
+  const int G = a.K / 128;
+  constexpr int NG = kGemvGroupsPerWave;
+  const int need = (G + NG - 1) / NG;
+  if (need <= 1) return launch_gemv_s<WF, PHASE, RT, 1, NG>(a, max_tiles, n_rowsets, stream);
+  if (need <= 2) return launch_gemv_s<WF, PHASE, RT, 2, NG>(a, max_tiles, n_rowsets, stream);
+  if (need <= 3) return launch_gemv_s<WF, PHASE, RT, 3, NG>(a, max_tiles, n_rowsets, stream);
+  if (need <= 4) return launch_gemv_s<WF, PHASE, RT, 4, NG>(a, max_tiles, n_rowsets, stream);
+  if (need <= 6) return launch_gemv_s<WF, PHASE, RT, 6, NG>(a, max_tiles, n_rowsets, stream);
+  if (need <= 8) return launch_gemv_s<WF, PHASE, RT, 8, NG>(a, max_tiles, n_rowsets, stream);
+  if (need <= 16) return launch_gemv_s<WF, PHASE, RT, 8, 2 * NG>(a, max_tiles, n_rowsets, stream);
+  return launch_gemv_s<WF, PHASE, RT, 8, 0>(a, max_tiles, n_rowsets, stream);
+}
+
+template <int WF>
+hipError_t launch_gemv_wf(const GemmArgs& a, int phase, int max_tiles, hipStream_t stream) {
+  if (phase == PHASE_GATE_UP) return launch_gemv_rt<WF, PHASE_GATE_UP, kGemvRtGateUp>(a, max_tiles, stream);
+  return launch_gemv_rt<WF, PHASE_DOWN, kGemvRtDown>(a, max_tiles, stream);
+}
+
+}  // namespace
+
+bool gemv_supported(int wf, int phase, int N, int K, int I) {
+  if (wf != WF_BF16 && wf != WF_I8 && wf != WF_I4) return false;
+  if (K % 128 != 0) return false;
+  const int out_dim = phase == PHASE_GATE_UP ? I : N;
+  const int rows_per_set = (phase == PHASE_GATE_UP ? kGemvRtGateUp : kGemvRtDown) * 16;
+  return out_dim % rows_per_set == 0;
+}
+
+hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream) {
+  if (max_tiles <= 0) return hipSuccess;
+  switch (wf) {
+    case WF_BF16:
+      return launch_gemv_wf<WF_BF16>(a, phase, max_tiles, stream);
+    case WF_I8:
+      return launch_gemv_wf<WF_I8>(a, phase, max_tiles, stream);
+    case WF_I4:
+      return launch_gemv_wf<WF_I4>(a, phase, max_tiles, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace nkt

@@ -48,6 +48,13 @@ enum GemmPhase : int { PHASE_GATE_UP = 0, PHASE_DOWN = 1 };
 hipError_t launch_route(const void* logits, int act_bf16, int T, int E, int k, unsigned flags,
                         int32_t* ids, float* w, hipStream_t stream);
 
+// K1 + K2 in one workgroup when route_group_fused(T, k).
+bool route_group_fused(int T, int k);
+hipError_t launch_route_group(const void* logits, int act_bf16, int T, int E, int k,
+                              unsigned flags, int bm, int max_tiles, int32_t* ids, float* w,
+                              int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
+                              int32_t* tiles, int32_t* n_tiles, hipStream_t stream);
+
 hipError_t launch_group(const int32_t* ids, int T, int k, int E, int bm, int max_tiles,
                         int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
                         int32_t* tiles, int32_t* n_tiles, hipStream_t stream);
@@ -60,6 +67,10 @@ int gemm_rows_per_block(int wf, int phase, int bm);
 
 hipError_t launch_gemm(const GemmArgs& a, int wf, int phase, int bm, int grid_tiles,
                        hipStream_t stream);
+
+// Decode form of K3 (tiles of at most 16 positions, split-K in a workgroup).
+bool gemv_supported(int wf, int phase, int N, int K, int I);
+hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream);
 
 hipError_t launch_pack(int wf, const void* src, const void* src_scales, int N, int K,
                        uint8_t* dst, uint16_t* dst_scales, hipStream_t stream);

@@ -1,6 +1,6 @@
 // K1: router softmax + top-k + renormalise, one wavefront per token.
 // K2: deterministic count / prefix-sum / permute of the (token, slot) pairs
-//     by expert, plus the tile list the grouped expert GEMM walks.
+//     by expert, plus the tile list the grouped expert GEMMs walk.
 //
 // Routing semantics follow nano_ktrans/layers/hybrid_moe.py:3321-3329:
 //   softmax arches: p = softmax_fp32(logits) rounded to the logits dtype,
@@ -8,8 +8,19 @@
 //   Mixtral:        top-k of the logits, softmax over the k selected values.
 // Grouping follows hybrid_moe.py:3512-3526 / cpu_moe.py:515-523: experts in
 // ascending id, tokens in ascending order within an expert.
-// The order of every floating-point operation is fixed (see route_expf and
-// the lane/butterfly layout below) so the result is reproducible bit for bit.
+// The order of every floating-point operation is fixed (route_expf, the
+// lane/butterfly layout of the softmax sum, slot-order k-way sums) so the
+// result is reproducible bit for bit.
+//
+// Top-k selection is a radix select over the 32-bit order-preserving keys:
+// 32 ballot/popcount rounds find the k-th largest key, ties at that key are
+// taken in ascending expert id, and each selected element's slot is its rank
+// under (value descending, id ascending), counted with scalar broadcasts.  No
+// cross-lane shuffles sit on the selection's critical path.
+//
+// Small batches run route and grouping in one launch (one workgroup of 16
+// waves); large batches use a wave-per-token route launch and a grouping
+// launch.
 #include "nkt_common.h"
 #include "nkt_internal.h"
 
@@ -27,31 +38,36 @@ __device__ __forceinline__ float from_ordered_bits(uint32_t o) {
   return __uint_as_float(u);
 }
 
+// number of set bits of m below this lane
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                        __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+__device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
+
+// Route one token with the whole wavefront.  sv/si: this wave's 16-entry LDS
+// scratch (selected values / ids in slot order).  Returns, in lanes < k, the
+// slot's expert id and weight; lanes >= k return id -1.
 template <int VPL, bool BF16>
-__global__ void __launch_bounds__(256) route_kernel(const void* __restrict__ logits, int T, int E,
-                                                    int k, unsigned flags,
-                                                    int32_t* __restrict__ ids_out,
-                                                    float* __restrict__ w_out) {
+__device__ __forceinline__ void route_token(const void* __restrict__ logits, int t, int E, int k,
+                                            unsigned flags, float* sv, int* si, int* out_id,
+                                            float* out_w) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (t >= T) return;
-
   float v[VPL];
   bool valid[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int e = lane + 64 * j;
     valid[j] = e < E;
-    float x = -__builtin_huge_valf();
-    if (valid[j]) {
-      const int64_t idx = (int64_t)t * E + e;
-      if (BF16)
-        x = bf16_bits_to_f32(((const uint16_t*)logits)[idx]);
-      else
-        x = ((const float*)logits)[idx];
-    }
-    v[j] = x;
+    const int64_t idx = (int64_t)t * E + (valid[j] ? e : 0);
+    float x;
+    if (BF16)
+      x = bf16_bits_to_f32(((const uint16_t*)logits)[idx]);
+    else
+      x = ((const float*)logits)[idx];
+    v[j] = valid[j] ? x : -__builtin_huge_valf();
   }
 
   const bool use_softmax = flags & 1u;
@@ -78,106 +94,143 @@ __global__ void __launch_bounds__(256) route_kernel(const void* __restrict__ log
     }
   }
 
-  // top-k by repeated wave-wide maximum of (value desc, id asc)
-  uint32_t taken = 0;
-  int sel_id[kMaxTopK];
-  float sel_val[kMaxTopK];
+  // ---- radix select of the k-th largest key ------------------------------
+  uint32_t key[VPL];
 #pragma unroll
-  for (int jj = 0; jj < kMaxTopK; ++jj) {
-    sel_id[jj] = 0;
-    sel_val[jj] = 0.0f;
-    if (jj < k) {
-      uint64_t best = 0;
+  for (int j = 0; j < VPL; ++j) key[j] = valid[j] ? ordered_bits(v[j]) : 0u;  // valid keys > 0
+  uint32_t tau = 0;
+#pragma unroll 4
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = tau | (1u << b);
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) cnt += __popcll(ballot64(key[j] >= cand));
+    tau = (cnt >= k) ? cand : tau;
+  }
+  int above = 0;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) above += __popcll(ballot64(key[j] > tau));
+  const int need_eq = k - above;  // >= 1 ties at tau, lowest ids first
+  bool sel[VPL];
+  int eq_before = 0;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const uint64_t m = ballot64(key[j] == tau);
+    const int r = eq_before + lanes_below(m);
+    sel[j] = key[j] > tau || (key[j] == tau && r < need_eq);
+    eq_before += __popcll(m);
+  }
+
+  // ---- slot = rank under (value desc, id asc) among the selected ---------
+  int rank[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) rank[j] = 0;
+#pragma unroll
+  for (int j2 = 0; j2 < VPL; ++j2) {
+    uint64_t m = ballot64(sel[j2]);
+    while (m) {
+      const int ln = __builtin_ctzll(m);
+      m &= m - 1;
+      const uint32_t ks = (uint32_t)__builtin_amdgcn_readlane((int)key[j2], ln);
+      const int is = ln + 64 * j2;
 #pragma unroll
       for (int j = 0; j < VPL; ++j) {
-        const int e = lane + 64 * j;
-        if (valid[j] && !(taken & (1u << j))) {
-          const uint64_t key = ((uint64_t)ordered_bits(v[j]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e);
-          best = key > best ? key : best;
-        }
+        const int id = lane + 64 * j;
+        rank[j] += (ks > key[j] || (ks == key[j] && is < id)) ? 1 : 0;
       }
-      best = wave_max_u64(best);
-      const int id = (int)(0xffffffffu - (uint32_t)best);
-      if ((id & 63) == lane) taken |= 1u << (id >> 6);
-      sel_id[jj] = id;
-      sel_val[jj] = from_ordered_bits((uint32_t)(best >> 32));
     }
   }
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    if (sel[j]) {
+      sv[rank[j]] = v[j];
+      si[rank[j]] = lane + 64 * j;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-  float w[kMaxTopK];
+  // ---- weights, k-way sums in slot order ---------------------------------
+  float s = 0.0f;
+  float m0 = sv[0];
   if (use_softmax) {
-#pragma unroll
-    for (int jj = 0; jj < kMaxTopK; ++jj) w[jj] = sel_val[jj];
     if (renorm) {
-      float s = sel_val[0];
-#pragma unroll
-      for (int jj = 1; jj < kMaxTopK; ++jj)
-        if (jj < k) s = s + sel_val[jj];
+      for (int jj = 0; jj < k; ++jj) s = (jj == 0) ? sv[0] : s + sv[jj];
       if (BF16) s = bf16_round(s);
-#pragma unroll
-      for (int jj = 0; jj < kMaxTopK; ++jj) {
-        float q = sel_val[jj] / s;
-        w[jj] = BF16 ? bf16_round(q) : q;
-      }
     }
   } else {
-    const float m = sel_val[0];
-    float ex[kMaxTopK];
-    float s = 0.0f;
-#pragma unroll
-    for (int jj = 0; jj < kMaxTopK; ++jj) {
-      ex[jj] = 0.0f;
-      if (jj < k) {
-        ex[jj] = route_expf(sel_val[jj] - m);
-        s = (jj == 0) ? ex[jj] : s + ex[jj];
-      }
-    }
-#pragma unroll
-    for (int jj = 0; jj < kMaxTopK; ++jj) {
-      float q = ex[jj] / s;
-      w[jj] = BF16 ? bf16_round(q) : q;
+    for (int jj = 0; jj < k; ++jj) {
+      const float e = route_expf(sv[jj] - m0);
+      s = (jj == 0) ? e : s + e;
     }
   }
-
-  // lane jj writes slot jj
-  int my_id = 0;
-  float my_w = 0.0f;
-#pragma unroll
-  for (int jj = 0; jj < kMaxTopK; ++jj) {
-    if (lane == jj) {
-      my_id = sel_id[jj];
-      my_w = w[jj];
-    }
-  }
+  int id = -1;
+  float w = 0.0f;
   if (lane < k) {
-    ids_out[(int64_t)t * k + lane] = my_id;
-    w_out[(int64_t)t * k + lane] = my_w;
+    id = si[lane];
+    const float val = sv[lane];
+    if (use_softmax) {
+      w = val;
+      if (renorm) {
+        const float q = val / s;
+        w = BF16 ? bf16_round(q) : q;
+      }
+    } else {
+      const float q = route_expf(val - m0) / s;
+      w = BF16 ? bf16_round(q) : q;
+    }
+  }
+  *out_id = id;
+  *out_w = w;
+  __builtin_amdgcn_wave_barrier();  // sv/si are reused by this wave's next token
+}
+
+template <int VPL, bool BF16>
+__global__ void __launch_bounds__(256) route_kernel(const void* __restrict__ logits, int T, int E,
+                                                    int k, unsigned flags,
+                                                    int32_t* __restrict__ ids_out,
+                                                    float* __restrict__ w_out) {
+  __shared__ float sv[4][kMaxTopK];
+  __shared__ int si[4][kMaxTopK];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  int id;
+  float w;
+  route_token<VPL, BF16>(logits, t, E, k, flags, sv[wave], si[wave], &id, &w);
+  if (lane < k) {
+    ids_out[(int64_t)t * k + lane] = id;
+    w_out[(int64_t)t * k + lane] = w;
   }
 }
 
 // ---------------------------------------------------------------------------
-// K2: one workgroup of 16 waves.  Wave w owns a contiguous range of pairs (in
+// K2 body: one workgroup of 16 waves groups the P = T*k pairs whose expert
+// ids sit in ids (global or LDS).  Wave w owns a contiguous range of pairs (in
 // pair order = token order).  Pass 1 counts per (wave, expert); a column scan
 // gives each wave its starting slot inside every expert's segment; pass 2
-// walks the range 64 pairs at a time and ranks equal experts inside the
-// chunk with ballots, so the permutation is stable in token order and
-// independent of scheduling.
+// walks the range 64 pairs at a time and ranks equal experts inside the chunk
+// with ballots, so the permutation is stable in token order and independent
+// of scheduling.  Then the tile list: (expert, first position, rows) for
+// every BM-row slice of every expert's segment, experts ascending.
 // ---------------------------------------------------------------------------
 constexpr int kGroupWaves = 16;
 
-__global__ void __launch_bounds__(1024) group_kernel(const int32_t* __restrict__ ids, int T, int k,
-                                                     int E, int bm, int max_tiles,
-                                                     int32_t* __restrict__ counts,
-                                                     int32_t* __restrict__ offsets,
-                                                     int32_t* __restrict__ perm,
-                                                     int32_t* __restrict__ inv,
-                                                     int32_t* __restrict__ tiles,
-                                                     int32_t* __restrict__ n_tiles) {
-  __shared__ int32_t hist[kGroupWaves][kMaxExperts];
-  __shared__ int32_t tot[kMaxExperts];
-  __shared__ int32_t off_s[kMaxExperts + 1];
-  __shared__ int32_t tile_off[kMaxExperts + 1];
+struct GroupLds {
+  int32_t hist[kGroupWaves][kMaxExperts];
+  int32_t tot[kMaxExperts];
+  int32_t off_s[kMaxExperts + 1];
+  int32_t tile_off[kMaxExperts + 1];
+};
 
+__device__ __forceinline__ void group_body(const int32_t* ids, int T, int k, int E, int bm,
+                                           int max_tiles, int32_t* __restrict__ counts,
+                                           int32_t* __restrict__ offsets,
+                                           int32_t* __restrict__ perm, int32_t* __restrict__ inv,
+                                           int32_t* __restrict__ tiles,
+                                           int32_t* __restrict__ n_tiles, GroupLds& L) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -187,12 +240,12 @@ __global__ void __launch_bounds__(1024) group_kernel(const int32_t* __restrict__
   const int pbeg = min(P, wave * ppw);
   const int pend = min(P, pbeg + ppw);
 
-  for (int i = tid; i < kGroupWaves * kMaxExperts; i += blockDim.x) (&hist[0][0])[i] = 0;
+  for (int i = tid; i < kGroupWaves * kMaxExperts; i += blockDim.x) (&L.hist[0][0])[i] = 0;
   __syncthreads();
 
   for (int p = pbeg + lane; p < pend; p += 64) {
     const int e = ids[p];
-    if (e >= 0 && e < E) atomicAdd(&hist[wave][e], 1);
+    if (e >= 0 && e < E) atomicAdd(&L.hist[wave][e], 1);
   }
   __syncthreads();
 
@@ -200,42 +253,52 @@ __global__ void __launch_bounds__(1024) group_kernel(const int32_t* __restrict__
   if (tid < E) {
     int run = 0;
     for (int w = 0; w < kGroupWaves; ++w) {
-      const int h = hist[w][tid];
-      hist[w][tid] = run;
+      const int h = L.hist[w][tid];
+      L.hist[w][tid] = run;
       run += h;
     }
-    tot[tid] = run;
+    L.tot[tid] = run;
   }
   __syncthreads();
 
-  // exclusive scan over experts (wave 0, 4 experts per lane)
+  // exclusive scans over experts (wave 0, 4 experts per lane): positions and tiles
   if (wave == 0) {
-    int local[4];
-    int sum = 0;
+    int local[4], tl[4];
+    int sum = 0, tsum = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = lane * 4 + i;
-      local[i] = (e < E) ? tot[e] : 0;
+      local[i] = (e < E) ? L.tot[e] : 0;
+      tl[i] = (local[i] + bm - 1) / bm;
       sum += local[i];
+      tsum += tl[i];
     }
     const int incl = wave_inclusive_scan(sum);
-    int run = incl - sum;
+    const int tincl = wave_inclusive_scan(tsum);
+    int run = incl - sum, trun = tincl - tsum;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = lane * 4 + i;
-      if (e < E) off_s[e] = run;
+      if (e < E) {
+        L.off_s[e] = run;
+        L.tile_off[e] = trun;
+      }
       run += local[i];
+      trun += tl[i];
     }
-    if (lane == 63) off_s[E] = incl;
+    if (lane == 63) {
+      L.off_s[E] = incl;
+      L.tile_off[E] = tincl;
+    }
   }
   __syncthreads();
 
   if (tid < E) {
-    counts[tid] = tot[tid];
-    offsets[tid] = off_s[tid];
-    for (int w = 0; w < kGroupWaves; ++w) hist[w][tid] += off_s[tid];
+    counts[tid] = L.tot[tid];
+    offsets[tid] = L.off_s[tid];
+    for (int w = 0; w < kGroupWaves; ++w) L.hist[w][tid] += L.off_s[tid];
   }
-  if (tid == 0) offsets[E] = off_s[E];
+  if (tid == 0) offsets[E] = L.off_s[E];
   __syncthreads();
 
   int nbits = 1;
@@ -243,7 +306,7 @@ __global__ void __launch_bounds__(1024) group_kernel(const int32_t* __restrict__
   for (int base = pbeg; base < pend; base += 64) {
     const int p = base + lane;
     const bool valid = p < pend;
-    int e = valid ? ids[p] : 0;
+    const int e = valid ? ids[p] : 0;
     const bool ok = valid && e >= 0 && e < E;
     uint64_t same = __ballot(ok);
     for (int b = 0; b < nbits; ++b) {
@@ -252,61 +315,89 @@ __global__ void __launch_bounds__(1024) group_kernel(const int32_t* __restrict__
       same &= bit ? bb : ~bb;
     }
     if (ok) {
-      const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-      const int rank = __popcll(same & lt);
+      const int rank = lanes_below(same);
       const int cnt = __popcll(same);
-      const int pos = hist[wave][e] + rank;
+      const int pos = L.hist[wave][e] + rank;
       perm[pos] = p;
       inv[p] = pos;
       __builtin_amdgcn_s_waitcnt(0);
-      if (rank == cnt - 1) hist[wave][e] += cnt;
+      if (rank == cnt - 1) L.hist[wave][e] += cnt;
     }
   }
-  __syncthreads();
 
-  // tile list for the grouped GEMM: (expert, first position, rows)
-  if (wave == 0) {
-    int local[4];
-    int sum = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = lane * 4 + i;
-      local[i] = (e < E) ? (tot[e] + bm - 1) / bm : 0;
-      sum += local[i];
-    }
-    const int incl = wave_inclusive_scan(sum);
-    int run = incl - sum;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = lane * 4 + i;
-      if (e < E) tile_off[e] = run;
-      run += local[i];
-    }
-    if (lane == 63) tile_off[E] = incl;
-  }
-  __syncthreads();
-  if (tid < E) {
-    const int c = tot[tid];
+  // tile list for the grouped GEMMs: (expert, first position, rows)
+  for (int e = wave; e < E; e += kGroupWaves) {
+    const int c = L.tot[e];
     const int nt = (c + bm - 1) / bm;
-    for (int m = 0; m < nt; ++m) {
-      const int ti = tile_off[tid] + m;
+    for (int m = lane; m < nt; m += 64) {
+      const int ti = L.tile_off[e] + m;
       if (ti < max_tiles) {
-        tiles[4 * ti + 0] = tid;
-        tiles[4 * ti + 1] = off_s[tid] + m * bm;
-        tiles[4 * ti + 2] = min(bm, c - m * bm);
-        tiles[4 * ti + 3] = 0;
+        int4 rec;
+        rec.x = e;
+        rec.y = L.off_s[e] + m * bm;
+        rec.z = min(bm, c - m * bm);
+        rec.w = 0;
+        *(int4*)(tiles + 4 * ti) = rec;
       }
     }
   }
-  if (tid == 0) n_tiles[0] = min(tile_off[E], max_tiles);
+  if (tid == 0) n_tiles[0] = min(L.tile_off[E], max_tiles);
 }
+
+__global__ void __launch_bounds__(1024) group_kernel(const int32_t* __restrict__ ids, int T, int k,
+                                                     int E, int bm, int max_tiles,
+                                                     int32_t* __restrict__ counts,
+                                                     int32_t* __restrict__ offsets,
+                                                     int32_t* __restrict__ perm,
+                                                     int32_t* __restrict__ inv,
+                                                     int32_t* __restrict__ tiles,
+                                                     int32_t* __restrict__ n_tiles) {
+  __shared__ GroupLds L;
+  group_body(ids, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, L);
+}
+
+// Route and group in one workgroup of 16 waves (small batches): wave w routes
+// tokens w, w + 16, ...; the ids stay in LDS for the grouping.
+template <int VPL, bool BF16>
+__global__ void __launch_bounds__(1024) route_group_kernel(
+    const void* __restrict__ logits, int T, int E, int k, unsigned flags, int bm, int max_tiles,
+    int32_t* __restrict__ ids_out, float* __restrict__ w_out, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ inv,
+    int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles) {
+  __shared__ GroupLds L;
+  __shared__ int32_t ids_s[kFusedRouteMaxPairs];
+  __shared__ float sv[kGroupWaves][kMaxTopK];
+  __shared__ int si[kGroupWaves][kMaxTopK];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  for (int t = wave; t < T; t += kGroupWaves) {
+    int id;
+    float w;
+    route_token<VPL, BF16>(logits, t, E, k, flags, sv[wave], si[wave], &id, &w);
+    if (lane < k) {
+      ids_s[t * k + lane] = id;
+      ids_out[(int64_t)t * k + lane] = id;
+      w_out[(int64_t)t * k + lane] = w;
+    }
+  }
+  __syncthreads();
+  group_body(ids_s, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, L);
+}
+
+#define NKT_VPL_SWITCH(E, CASE) \
+  switch ((E + 63) / 64) {      \
+    CASE(1)                     \
+    CASE(2)                     \
+    CASE(3)                     \
+    CASE(4)                     \
+    default:                    \
+      return hipErrorInvalidValue; \
+  }
 
 hipError_t launch_route(const void* logits, int act_bf16, int T, int E, int k, unsigned flags,
                         int32_t* ids, float* w, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
-  const int tokens_per_block = 4;
-  dim3 grid((T + tokens_per_block - 1) / tokens_per_block), block(64 * tokens_per_block);
-  const int vpl = (E + 63) / 64;
+  dim3 grid((T + 3) / 4), block(256);
 #define NKT_ROUTE_CASE(V)                                                                    \
   case V:                                                                                    \
     if (act_bf16)                                                                            \
@@ -316,14 +407,7 @@ hipError_t launch_route(const void* logits, int act_bf16, int T, int E, int k, u
       hipLaunchKernelGGL((route_kernel<V, false>), grid, block, 0, stream, logits, T, E, k,  \
                          flags, ids, w);                                                     \
     break;
-  switch (vpl) {
-    NKT_ROUTE_CASE(1)
-    NKT_ROUTE_CASE(2)
-    NKT_ROUTE_CASE(3)
-    NKT_ROUTE_CASE(4)
-    default:
-      return hipErrorInvalidValue;
-  }
+  NKT_VPL_SWITCH(E, NKT_ROUTE_CASE)
 #undef NKT_ROUTE_CASE
   return hipGetLastError();
 }
@@ -333,6 +417,31 @@ hipError_t launch_group(const int32_t* ids, int T, int k, int E, int bm, int max
                         int32_t* tiles, int32_t* n_tiles, hipStream_t stream) {
   hipLaunchKernelGGL(group_kernel, dim3(1), dim3(64 * kGroupWaves), 0, stream, ids, T, k, E, bm,
                      max_tiles, counts, offsets, perm, inv, tiles, n_tiles);
+  return hipGetLastError();
+}
+
+bool route_group_fused(int T, int k) { return T <= kFusedRouteMaxTokens && T * k <= kFusedRouteMaxPairs; }
+
+hipError_t launch_route_group(const void* logits, int act_bf16, int T, int E, int k,
+                              unsigned flags, int bm, int max_tiles, int32_t* ids, float* w,
+                              int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
+                              int32_t* tiles, int32_t* n_tiles, hipStream_t stream) {
+  if (T <= 0) return hipSuccess;
+  if (!route_group_fused(T, k)) return hipErrorInvalidValue;
+  dim3 grid(1), block(64 * kGroupWaves);
+#define NKT_RG_CASE(V)                                                                          \
+  case V:                                                                                       \
+    if (act_bf16)                                                                               \
+      hipLaunchKernelGGL((route_group_kernel<V, true>), grid, block, 0, stream, logits, T, E, k, \
+                         flags, bm, max_tiles, ids, w, counts, offsets, perm, inv, tiles,       \
+                         n_tiles);                                                              \
+    else                                                                                        \
+      hipLaunchKernelGGL((route_group_kernel<V, false>), grid, block, 0, stream, logits, T, E,  \
+                         k, flags, bm, max_tiles, ids, w, counts, offsets, perm, inv, tiles,    \
+                         n_tiles);                                                              \
+    break;
+  NKT_VPL_SWITCH(E, NKT_RG_CASE)
+#undef NKT_RG_CASE
   return hipGetLastError();
 }
 
