@@ -22,7 +22,10 @@ struct Handle {
 
 constexpr int kWsTiles = NKT_WS_NUM_REGIONS;       // int32 [max_tiles][4]
 constexpr int kWsNTiles = NKT_WS_NUM_REGIONS + 1;  // int32 [1]
-constexpr int kWsAll = NKT_WS_NUM_REGIONS + 2;
+constexpr int kWsXsum = NKT_WS_NUM_REGIONS + 2;    // fp32 [T, H/128]   group sums of x (prefill form)
+constexpr int kWsHsum = NKT_WS_NUM_REGIONS + 3;    // fp32 [T*k, I/128] group sums of h
+constexpr int kWsShHsum = NKT_WS_NUM_REGIONS + 4;  // fp32 [T, I_s/128] group sums of the shared h
+constexpr int kWsAll = NKT_WS_NUM_REGIONS + 5;
 
 void set_err(char* err, size_t len, const char* fmt, ...) {
   if (!err || len == 0) return;
@@ -87,8 +90,16 @@ struct WsLayout {
   size_t off[kWsAll];
   size_t total;
   int bm;
+  int bm_shared;
   int max_tiles;
 };
+
+// the prefill form covers both projections of the routed (or shared) experts
+bool prefill_form_ok(const Handle* h, bool shared) {
+  const int I = shared ? h->Is : h->I;
+  return gemm2_supported(h->wf, PHASE_GATE_UP, 2 * I, h->H, I) &&
+         gemm2_supported(h->wf, PHASE_DOWN, h->H, I, I);
+}
 
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
@@ -96,7 +107,8 @@ WsLayout ws_layout(const Handle* h, int T) {
   WsLayout L;
   const size_t P = (size_t)T * h->k;
   const size_t es = h->act_bf16 ? 2 : 4;
-  L.bm = gemm_tile_m(T > 0 ? T : 1, h->k, h->E);
+  L.bm = gemm_tile_m(T > 0 ? T : 1, h->k, h->E, h->wf, prefill_form_ok(h, false));
+  L.bm_shared = gemm_tile_m(T > 0 ? T : 1, 1, 1, h->wf, prefill_form_ok(h, true));
   L.max_tiles = (int)(P / L.bm) + (int)(P < (size_t)h->E ? P : (size_t)h->E);
   size_t sz[kWsAll];
   sz[NKT_WS_TOPK_IDS] = P * 4;
@@ -112,6 +124,9 @@ WsLayout ws_layout(const Handle* h, int T) {
   sz[NKT_WS_SHARED_Y] = h->Is > 0 ? (size_t)T * h->H * 4 : 0;
   sz[kWsTiles] = (size_t)L.max_tiles * 16;
   sz[kWsNTiles] = 4;
+  sz[kWsXsum] = (size_t)T * (h->H / 128) * 4;
+  sz[kWsHsum] = P * (h->I / 128) * 4;
+  sz[kWsShHsum] = h->Is > 0 ? (size_t)T * (h->Is / 128) * 4 : 0;
   size_t o = 0;
   for (int i = 0; i < kWsAll; ++i) {
     L.off[i] = o;
@@ -195,6 +210,9 @@ GemmArgs expert_args(const Handle* h, int phase, bool shared, const void* in, vo
   a.in = in;
   a.topk = h->k;
   a.act_bf16 = h->act_bf16;
+  float* hs = ws_ptr<float>(ws, L, shared ? kWsShHsum : kWsHsum);
+  a.xsum = phase == PHASE_GATE_UP ? ws_ptr<float>(ws, L, kWsXsum) : hs;
+  a.hsum = phase == PHASE_GATE_UP ? hs : nullptr;
   if (shared) {
     a.perm = nullptr;
     a.out = phase == PHASE_GATE_UP ? ws_ptr<void>(ws, L, NKT_WS_SHARED_H) : ws_ptr<void>(ws, L, NKT_WS_SHARED_Y);
@@ -243,10 +261,20 @@ int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, 
 }
 
 // K3 launch for one projection: the decode form for tiles of at most 16
-// positions, the tiled MFMA form otherwise.
+// positions, the prefill form for its tiles, the tiled form otherwise.
+// The prefill form's gate_up first sums the activations per 128-wide group
+// (int formats; the down projection reads the sums gate_up writes).
 hipError_t launch_expert_gemm(const Handle* h, const GemmArgs& a, int phase, int bm, int tiles,
                               hipStream_t st) {
   if (bm == 16 && gemv_supported(h->wf, phase, a.N, a.K, a.I)) return launch_gemv(a, h->wf, phase, tiles, st);
+  if (bm == kPrefillTileM && gemm2_supported(h->wf, phase, a.N, a.K, a.I)) {
+    if (phase == PHASE_GATE_UP && (h->wf == WF_I4 || h->wf == WF_I8)) {
+      const hipError_t e = launch_group_sums(a.in, (a.perm ? a.num_rows / a.topk : a.num_rows), a.K,
+                                             const_cast<float*>(a.xsum), st);
+      if (e != hipSuccess) return e;
+    }
+    return launch_gemm2(a, h->wf, phase, tiles, st);
+  }
   return launch_gemm(a, h->wf, phase, bm, tiles, st);
 }
 
@@ -290,7 +318,7 @@ int do_shared(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipS
                                     ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE), st),
                  "shared gate kernel", err, len))
     return NKT_ERR;
-  const int bm = gemm_tile_m(T, 1, 1);
+  const int bm = L.bm_shared;
   const int tiles = (T + bm - 1) / bm;
   GemmArgs a = expert_args(h, PHASE_GATE_UP, true, x, ws, L, T);
   if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, bm, tiles, st), "shared gate_up gemm", err, len))
@@ -364,6 +392,16 @@ void* nkt_moe_create(int num_experts, int top_k, int hidden_size, int moe_interm
   if (max_tokens < 1 || (int64_t)max_tokens * top_k > (1 << 24)) {
     set_err(err, err_len, "max_tokens=%d outside [1, 2^24 / top_k]", max_tokens);
     return nullptr;
+  }
+  {
+    // the expert kernels address an activation matrix with 32-bit byte offsets
+    const int64_t t = max_tokens, kmax = shared_intermediate_size > hidden_size ? shared_intermediate_size : hidden_size;
+    const int64_t most = t * kmax * 2 > t * top_k * moe_intermediate_size * 2 ? t * kmax * 2
+                                                                               : t * top_k * moe_intermediate_size * 2;
+    if (most >= ((int64_t)1 << 32)) {
+      set_err(err, err_len, "max_tokens=%d too large: activations would exceed 4 GiB", max_tokens);
+      return nullptr;
+    }
   }
   Handle* h = new (std::nothrow) Handle();
   if (!h) {

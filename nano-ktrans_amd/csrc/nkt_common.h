@@ -112,6 +112,56 @@ __device__ __forceinline__ int wave_inclusive_scan(int v) {
 }
 
 // ---------------------------------------------------------------------------
+// weight dequantisation into MFMA A operands (exact bf16 integers)
+//   int4: one u32 holds 8 nibbles in MFMA column order (nibble j<4 -> column
+//         2j, j>=4 -> 2(j-4)+1); step s of dq_i4(w >> 4s) gives bf16 128 + n
+//         for columns 2s', 2s'+1 pairs (n = stored nibble = q + 8).
+//   int8: two u32 hold 8 bytes (stored q + 128) -> 8 bf16 values 0..255.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ u32x4 dq_i4(uint32_t w) {
+  u32x4 a;
+  a[0] = (w & 0x000F000Fu) | 0x43004300u;
+  a[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
+  a[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
+  a[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  return a;
+}
+
+__device__ __forceinline__ uint32_t bf16pair_u8(uint32_t w, int lo_byte) {
+  const float f0 = (float)((w >> (8 * lo_byte)) & 0xffu);
+  const float f1 = (float)((w >> (8 * lo_byte + 8)) & 0xffu);
+  return __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+}
+
+__device__ __forceinline__ u32x4 dq_i8(uint32_t w0, uint32_t w1) {
+  u32x4 a;
+  a[0] = bf16pair_u8(w0, 0);
+  a[1] = bf16pair_u8(w0, 2);
+  a[2] = bf16pair_u8(w1, 0);
+  a[3] = bf16pair_u8(w1, 2);
+  return a;
+}
+
+__device__ __forceinline__ f32x4 bf16x4_to_f32(u32x2 v) {
+  return f32x4{__uint_as_float(v[0] << 16), __uint_as_float(v[0] & 0xffff0000u),
+               __uint_as_float(v[1] << 16), __uint_as_float(v[1] & 0xffff0000u)};
+}
+
+__device__ __forceinline__ float silu_f32(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
+
+// Workgroup barrier for LDS traffic only: waits for this wave's LDS
+// operations, not for its outstanding global loads (a full __syncthreads
+// fence would also drain the weight prefetch).
+__device__ __forceinline__ void lds_barrier() {
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt, expcnt untouched
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
+// ---------------------------------------------------------------------------
 // MFMA wrappers (gfx950)
 //   16x16x32 bf16: lane l supplies A[l%16][8*(l/16) .. +7] and
 //   B[8*(l/16) .. +7][l%16]; D[4*(l/16)+v][l%16] lands in register v.

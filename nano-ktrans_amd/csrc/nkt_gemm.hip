@@ -342,9 +342,10 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(GemmArgs a) {
 // ---------------------------------------------------------------------------
 // configuration table
 // ---------------------------------------------------------------------------
-int gemm_tile_m(int num_tokens, int topk, int num_experts) {
+int gemm_tile_m(int num_tokens, int topk, int num_experts, int wf, bool prefill_form) {
   const double avg = (double)num_tokens * topk / (double)num_experts;
   if (avg <= 12.0) return 16;
+  if (wf != WF_F32 && prefill_form) return kPrefillTileM;
   if (avg <= 40.0) return 32;
   return 64;
 }

@@ -35,37 +35,6 @@ constexpr int kGemvRtDown = 2;
 
 namespace {
 
-__device__ __forceinline__ u32x4 dq_i4(uint32_t w) {
-  u32x4 a;
-  a[0] = (w & 0x000F000Fu) | 0x43004300u;
-  a[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-  a[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-  a[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
-  return a;
-}
-
-__device__ __forceinline__ uint32_t bf16pair_u8(uint32_t w, int lo_byte) {
-  const float f0 = (float)((w >> (8 * lo_byte)) & 0xffu);
-  const float f1 = (float)((w >> (8 * lo_byte + 8)) & 0xffu);
-  return __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
-}
-
-__device__ __forceinline__ u32x4 dq_i8(uint32_t w0, uint32_t w1) {
-  u32x4 a;
-  a[0] = bf16pair_u8(w0, 0);
-  a[1] = bf16pair_u8(w0, 2);
-  a[2] = bf16pair_u8(w1, 0);
-  a[3] = bf16pair_u8(w1, 2);
-  return a;
-}
-
-__device__ __forceinline__ float silu(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
-
-__device__ __forceinline__ f32x4 bf16x4_to_f32(u32x2 v) {
-  return f32x4{__uint_as_float(v[0] << 16), __uint_as_float(v[0] & 0xffff0000u),
-               __uint_as_float(v[1] << 16), __uint_as_float(v[1] & 0xffff0000u)};
-}
-
 // One ring slot: one K group of NT weight tiles (+ int4 scales) and the
 // lane's token activations for the group's 4 MFMA steps.
 template <int WF, int NT>
@@ -261,7 +230,7 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
       }
       float h[4];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) h[v] = silu(s0[v]) * s1[v];
+      for (int v = 0; v < 4; ++v) h[v] = silu_f32(s0[v]) * s1[v];
       u32x2 pk;
       pk[0] = pack_bf16x2(h[0], h[1]);
       pk[1] = pack_bf16x2(h[2], h[3]);

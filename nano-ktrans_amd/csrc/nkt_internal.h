@@ -41,9 +41,14 @@ struct GemmArgs {
   const int32_t* n_tiles;  // device scalar; nullptr: dense tiles over num_rows (expert 0)
   int num_rows;
   int act_bf16;
+  const float* xsum;       // prefill, int formats: group sums of the input rows [rows, K/128]
+  float* hsum;             // prefill gate_up: group sums of the stored h [positions, I/128]
 };
 
 enum GemmPhase : int { PHASE_GATE_UP = 0, PHASE_DOWN = 1 };
+
+// positions per tile of the prefill form of K3
+constexpr int kPrefillTileM = 64;
 
 hipError_t launch_route(const void* logits, int act_bf16, int T, int E, int k, unsigned flags,
                         int32_t* ids, float* w, hipStream_t stream);
@@ -59,8 +64,11 @@ hipError_t launch_group(const int32_t* ids, int T, int k, int E, int bm, int max
                         int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
                         int32_t* tiles, int32_t* n_tiles, hipStream_t stream);
 
-// Tile shapes: returns the token-tile height (BM) used for num_tokens.
-int gemm_tile_m(int num_tokens, int topk, int num_experts);
+// Tile shapes: returns the token-tile height (BM) used for num_tokens:
+// 16 for decode-sized expert groups (gemv form), else kPrefillTileM when
+// the prefill form takes the shape (prefill_form), else 32 / 64 (the tiled
+// form that also serves fp32 weights).
+int gemm_tile_m(int num_tokens, int topk, int num_experts, int wf, bool prefill_form);
 
 // Rows of weights (gate_up: output columns of h) covered by one workgroup.
 int gemm_rows_per_block(int wf, int phase, int bm);
@@ -71,6 +79,12 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int phase, int bm, int grid_ti
 // Decode form of K3 (tiles of at most 16 positions, split-K in a workgroup).
 bool gemv_supported(int wf, int phase, int N, int K, int I);
 hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream);
+
+// Prefill form of K3 (tiles of 128 positions, bf16 / int8 / int4 weights).
+bool gemm2_supported(int wf, int phase, int N, int K, int I);
+hipError_t launch_gemm2(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream);
+// fp32 sums of every 128-wide K group of the rows of a bf16 matrix [rows, K]
+hipError_t launch_group_sums(const void* x, int rows, int K, float* out, hipStream_t stream);
 
 hipError_t launch_pack(int wf, const void* src, const void* src_scales, int N, int K,
                        uint8_t* dst, uint16_t* dst_scales, hipStream_t stream);
