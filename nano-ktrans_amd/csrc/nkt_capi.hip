@@ -25,7 +25,8 @@ constexpr int kWsNTiles = NKT_WS_NUM_REGIONS + 1;  // int32 [1]
 constexpr int kWsXsum = NKT_WS_NUM_REGIONS + 2;    // fp32 [T, H/128]   group sums of x (prefill form)
 constexpr int kWsHsum = NKT_WS_NUM_REGIONS + 3;    // fp32 [T*k, I/128] group sums of h
 constexpr int kWsShHsum = NKT_WS_NUM_REGIONS + 4;  // fp32 [T, I_s/128] group sums of the shared h
-constexpr int kWsAll = NKT_WS_NUM_REGIONS + 5;
+constexpr int kWsHist = NKT_WS_NUM_REGIONS + 5;   // int32 [blocks, E] per-block expert histograms
+constexpr int kWsAll = NKT_WS_NUM_REGIONS + 6;
 
 void set_err(char* err, size_t len, const char* fmt, ...) {
   if (!err || len == 0) return;
@@ -127,6 +128,7 @@ WsLayout ws_layout(const Handle* h, int T) {
   sz[kWsXsum] = (size_t)T * (h->H / 128) * 4;
   sz[kWsHsum] = P * (h->I / 128) * 4;
   sz[kWsShHsum] = h->Is > 0 ? (size_t)T * (h->Is / 128) * 4 : 0;
+  sz[kWsHist] = (size_t)group_hist_blocks((int)P) * h->E * 4;
   size_t o = 0;
   for (int i = 0; i < kWsAll; ++i) {
     L.off[i] = o;
@@ -253,9 +255,9 @@ int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, 
   if (!check_hip(launch_route(logits, h->act_bf16, T, h->E, h->k, h->flags, ids, wts, st),
                  "route kernel", err, len))
     return NKT_ERR;
-  if (!check_hip(launch_group(ids, T, h->k, h->E, L.bm, L.max_tiles, counts, offsets, perm, inv, tiles,
-                              n_tiles, st),
-                 "group kernel", err, len))
+  if (!check_hip(launch_group_multi(ids, T, h->k, h->E, L.bm, L.max_tiles, ws_ptr<int32_t>(ws, L, kWsHist), counts,
+                                    offsets, perm, inv, tiles, n_tiles, st),
+                 "group kernels", err, len))
     return NKT_ERR;
   return NKT_OK;
 }

@@ -35,7 +35,6 @@ namespace {
 constexpr int kBM = 64;           // positions per tile
 constexpr int kCT = kBM / 16;     // 16-position MFMA column tiles
 constexpr int kRT = 4;            // 16-row weight tiles per wave
-constexpr int kLdsRow = 128 + 8;  // bf16 per LDS row: 256 B + 16 B pad (conflict-free reads)
 constexpr int kXcds = 8;          // MI355X: accelerator complex dies, each with its own L2
 
 template <int WF>

@@ -60,9 +60,11 @@ hipError_t launch_route_group(const void* logits, int act_bf16, int T, int E, in
                               int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
                               int32_t* tiles, int32_t* n_tiles, hipStream_t stream);
 
-hipError_t launch_group(const int32_t* ids, int T, int k, int E, int bm, int max_tiles,
-                        int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
-                        int32_t* tiles, int32_t* n_tiles, hipStream_t stream);
+// K2 over many workgroups (large batches): hist holds group_hist_blocks(T*k) x E int32.
+int group_hist_blocks(int P);
+hipError_t launch_group_multi(const int32_t* ids, int T, int k, int E, int bm, int max_tiles, int32_t* hist,
+                              int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* tiles,
+                              int32_t* n_tiles, hipStream_t stream);
 
 // Tile shapes: returns the token-tile height (BM) used for num_tokens:
 // 16 for decode-sized expert groups (gemv form), else kPrefillTileM when

@@ -344,16 +344,173 @@ __device__ __forceinline__ void group_body(const int32_t* ids, int T, int k, int
   if (tid == 0) n_tiles[0] = min(L.tile_off[E], max_tiles);
 }
 
-__global__ void __launch_bounds__(1024) group_kernel(const int32_t* __restrict__ ids, int T, int k,
-                                                     int E, int bm, int max_tiles,
-                                                     int32_t* __restrict__ counts,
-                                                     int32_t* __restrict__ offsets,
-                                                     int32_t* __restrict__ perm,
-                                                     int32_t* __restrict__ inv,
-                                                     int32_t* __restrict__ tiles,
-                                                     int32_t* __restrict__ n_tiles) {
-  __shared__ GroupLds L;
-  group_body(ids, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, L);
+// ---------------------------------------------------------------------------
+// K2 for large batches, over many workgroups: count_kernel writes one
+// histogram per block of kPairsPerBlock consecutive pairs; scatter_kernel
+// (same blocks) turns the histograms into each block's start inside every
+// expert's segment, ranks its pairs with ballots (stable in pair order) and
+// writes perm / inv; block 0 also writes counts, offsets and the tile list.
+// ---------------------------------------------------------------------------
+constexpr int kScatterWaves = 16;
+constexpr int kPairsPerWave = 128;
+constexpr int kPairsPerBlock = kScatterWaves * kPairsPerWave;
+
+__global__ void __launch_bounds__(1024) count_kernel(const int32_t* __restrict__ ids, int P, int E,
+                                                     int32_t* __restrict__ hist) {
+  __shared__ int32_t h[kMaxExperts];
+  const int tid = threadIdx.x;
+  if (tid < E) h[tid] = 0;
+  __syncthreads();
+  const int p0 = blockIdx.x * kPairsPerBlock;
+  for (int p = p0 + tid; p < min(P, p0 + kPairsPerBlock); p += 1024) {
+    const int e = ids[p];
+    if (e >= 0 && e < E) atomicAdd(&h[e], 1);
+  }
+  __syncthreads();
+  if (tid < E) hist[(int64_t)blockIdx.x * E + tid] = h[tid];
+}
+
+__global__ void __launch_bounds__(1024) scatter_kernel(const int32_t* __restrict__ ids, int P, int E, int bm,
+                                                       int max_tiles, const int32_t* __restrict__ hist,
+                                                       int32_t* __restrict__ counts,
+                                                       int32_t* __restrict__ offsets,
+                                                       int32_t* __restrict__ perm, int32_t* __restrict__ inv,
+                                                       int32_t* __restrict__ tiles,
+                                                       int32_t* __restrict__ n_tiles) {
+  __shared__ int32_t tot[kMaxExperts], pre[kMaxExperts], off_s[kMaxExperts + 1], tile_off[kMaxExperts + 1];
+  __shared__ int32_t whist[kScatterWaves][kMaxExperts];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int nb = gridDim.x;
+  const int b = blockIdx.x;
+  // totals per expert and the pairs of earlier blocks, blocks in order
+  if (tid < E) {
+    int t = 0, q = 0;
+#pragma unroll 8
+    for (int bb = 0; bb < nb; ++bb) {
+      const int c = hist[(int64_t)bb * E + tid];
+      q += bb < b ? c : 0;
+      t += c;
+    }
+    tot[tid] = t;
+    pre[tid] = q;
+  }
+  for (int i = tid; i < kScatterWaves * kMaxExperts; i += 1024) (&whist[0][0])[i] = 0;
+  __syncthreads();
+  // exclusive scans over experts (wave 0, 4 experts per lane): positions and tiles
+  if (wave == 0) {
+    int local[4], tl[4];
+    int sum = 0, tsum = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane * 4 + i;
+      local[i] = (e < E) ? tot[e] : 0;
+      tl[i] = (local[i] + bm - 1) / bm;
+      sum += local[i];
+      tsum += tl[i];
+    }
+    const int incl = wave_inclusive_scan(sum);
+    const int tincl = wave_inclusive_scan(tsum);
+    int run = incl - sum, trun = tincl - tsum;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = lane * 4 + i;
+      if (e < E) {
+        off_s[e] = run;
+        tile_off[e] = trun;
+      }
+      run += local[i];
+      trun += tl[i];
+    }
+    if (lane == 63) {
+      off_s[E] = incl;
+      tile_off[E] = tincl;
+    }
+  }
+  // per-wave histogram of this block's pairs (wave w: kPairsPerWave consecutive pairs)
+  const int pbeg = min(P, b * kPairsPerBlock + wave * kPairsPerWave);
+  const int pend = min(P, pbeg + kPairsPerWave);
+  for (int p = pbeg + lane; p < pend; p += 64) {
+    const int e = ids[p];
+    if (e >= 0 && e < E) atomicAdd(&whist[wave][e], 1);
+  }
+  __syncthreads();
+  // each wave's start inside every expert's segment
+  if (tid < E) {
+    int run = off_s[tid] + pre[tid];
+#pragma unroll
+    for (int w = 0; w < kScatterWaves; ++w) {
+      const int c = whist[w][tid];
+      whist[w][tid] = run;
+      run += c;
+    }
+  }
+  if (b == 0) {
+    if (tid < E) {
+      counts[tid] = tot[tid];
+      offsets[tid] = off_s[tid];
+    }
+    if (tid == 0) {
+      offsets[E] = off_s[E];
+      n_tiles[0] = min(tile_off[E], max_tiles);
+    }
+    for (int e = wave; e < E; e += kScatterWaves) {
+      const int c = tot[e];
+      const int nt = (c + bm - 1) / bm;
+      for (int m = lane; m < nt; m += 64) {
+        const int ti = tile_off[e] + m;
+        if (ti < max_tiles) {
+          int4 rec;
+          rec.x = e;
+          rec.y = off_s[e] + m * bm;
+          rec.z = min(bm, c - m * bm);
+          rec.w = 0;
+          *(int4*)(tiles + 4 * ti) = rec;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  int nbits = 1;
+  while ((1 << nbits) < E) ++nbits;
+  for (int base = pbeg; base < pend; base += 64) {
+    const int p = base + lane;
+    const bool valid = p < pend;
+    const int e = valid ? ids[p] : 0;
+    const bool ok = valid && e >= 0 && e < E;
+    uint64_t same = __ballot(ok);
+    for (int bit = 0; bit < nbits; ++bit) {
+      const bool on = (e >> bit) & 1;
+      const uint64_t bb = __ballot(ok && on);
+      same &= on ? bb : ~bb;
+    }
+    if (ok) {
+      const int rank = lanes_below(same);
+      const int cnt = __popcll(same);
+      const int pos = whist[wave][e] + rank;
+      perm[pos] = p;
+      inv[p] = pos;
+      __builtin_amdgcn_s_waitcnt(0);
+      if (rank == cnt - 1) whist[wave][e] += cnt;
+    }
+  }
+}
+
+int group_hist_blocks(int P) { return (P + kPairsPerBlock - 1) / kPairsPerBlock; }
+
+hipError_t launch_group_multi(const int32_t* ids, int T, int k, int E, int bm, int max_tiles, int32_t* hist,
+                              int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* tiles,
+                              int32_t* n_tiles, hipStream_t stream) {
+  const int P = T * k;
+  const int nb = group_hist_blocks(P);
+  if (nb <= 0) return hipSuccess;
+  hipLaunchKernelGGL(count_kernel, dim3(nb), dim3(1024), 0, stream, ids, P, E, hist);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(scatter_kernel, dim3(nb), dim3(1024), 0, stream, ids, P, E, bm, max_tiles, hist, counts,
+                     offsets, perm, inv, tiles, n_tiles);
+  return hipGetLastError();
 }
 
 // Route and group in one workgroup of 16 waves (small batches): wave w routes
@@ -409,14 +566,6 @@ hipError_t launch_route(const void* logits, int act_bf16, int T, int E, int k, u
     break;
   NKT_VPL_SWITCH(E, NKT_ROUTE_CASE)
 #undef NKT_ROUTE_CASE
-  return hipGetLastError();
-}
-
-hipError_t launch_group(const int32_t* ids, int T, int k, int E, int bm, int max_tiles,
-                        int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
-                        int32_t* tiles, int32_t* n_tiles, hipStream_t stream) {
-  hipLaunchKernelGGL(group_kernel, dim3(1), dim3(64 * kGroupWaves), 0, stream, ids, T, k, E, bm,
-                     max_tiles, counts, offsets, perm, inv, tiles, n_tiles);
   return hipGetLastError();
 }
 
