@@ -26,7 +26,8 @@ constexpr int kWsXsum = NKT_WS_NUM_REGIONS + 2;    // fp32 [T, H/128]   group su
 constexpr int kWsHsum = NKT_WS_NUM_REGIONS + 3;    // fp32 [T*k, I/128] group sums of h
 constexpr int kWsShHsum = NKT_WS_NUM_REGIONS + 4;  // fp32 [T, I_s/128] group sums of the shared h
 constexpr int kWsHist = NKT_WS_NUM_REGIONS + 5;   // int32 [blocks, E] per-block expert histograms
-constexpr int kWsAll = NKT_WS_NUM_REGIONS + 6;
+constexpr int kWsTileSrc = NKT_WS_NUM_REGIONS + 6; // int32 [max_tiles, 16] decode tiles' input rows
+constexpr int kWsAll = NKT_WS_NUM_REGIONS + 7;
 
 void set_err(char* err, size_t len, const char* fmt, ...) {
   if (!err || len == 0) return;
@@ -129,6 +130,7 @@ WsLayout ws_layout(const Handle* h, int T) {
   sz[kWsHsum] = P * (h->I / 128) * 4;
   sz[kWsShHsum] = h->Is > 0 ? (size_t)T * (h->Is / 128) * 4 : 0;
   sz[kWsHist] = (size_t)group_hist_blocks((int)P) * h->E * 4;
+  sz[kWsTileSrc] = L.bm == kTileSrcCols ? (size_t)L.max_tiles * kTileSrcCols * 4 : 0;
   size_t o = 0;
   for (int i = 0; i < kWsAll; ++i) {
     L.off[i] = o;
@@ -227,6 +229,7 @@ GemmArgs expert_args(const Handle* h, int phase, bool shared, const void* in, vo
     a.tiles = ws_ptr<int32_t>(ws, L, kWsTiles);
     a.n_tiles = ws_ptr<int32_t>(ws, L, kWsNTiles);
     a.num_rows = T * h->k;
+    if (phase == PHASE_GATE_UP && L.bm == kTileSrcCols) a.tile_src = ws_ptr<int32_t>(ws, L, kWsTileSrc);
   }
   return a;
 }
@@ -245,9 +248,10 @@ int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, 
   int32_t* inv = ws_ptr<int32_t>(ws, L, NKT_WS_INV);
   int32_t* tiles = ws_ptr<int32_t>(ws, L, kWsTiles);
   int32_t* n_tiles = ws_ptr<int32_t>(ws, L, kWsNTiles);
+  int32_t* tile_src = L.bm == kTileSrcCols ? ws_ptr<int32_t>(ws, L, kWsTileSrc) : nullptr;
   if (route_group_fused(T, h->k)) {
     if (!check_hip(launch_route_group(logits, h->act_bf16, T, h->E, h->k, h->flags, L.bm, L.max_tiles,
-                                      ids, wts, counts, offsets, perm, inv, tiles, n_tiles, st),
+                                      ids, wts, counts, offsets, perm, inv, tiles, n_tiles, tile_src, st),
                    "route+group kernel", err, len))
       return NKT_ERR;
     return NKT_OK;
@@ -256,7 +260,7 @@ int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, 
                  "route kernel", err, len))
     return NKT_ERR;
   if (!check_hip(launch_group_multi(ids, T, h->k, h->E, L.bm, L.max_tiles, ws_ptr<int32_t>(ws, L, kWsHist), counts,
-                                    offsets, perm, inv, tiles, n_tiles, st),
+                                    offsets, perm, inv, tiles, n_tiles, tile_src, st),
                  "group kernels", err, len))
     return NKT_ERR;
   return NKT_OK;

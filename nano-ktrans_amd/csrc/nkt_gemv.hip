@@ -17,8 +17,11 @@
 // refills are issued right after the slot is consumed, always (past the last
 // group they re-read it, an L2 hit), so the loop has no branch, store or
 // barrier.  The matrix core takes the weights as the A operand and the tile's
-// activations, loaded in the B-operand lane layout, as B.  The S partial sums
-// meet in LDS and are added in K-part order.
+// activations as B: in the B-operand lane layout (four loads per group), or,
+// for single-position tiles, one load per group spread over the B layout by
+// DPP row broadcasts.  Gathered rows come from the per-tile source rows K2
+// writes (indexed by tile, so their load overlaps the tile record's).  The S
+// partial sums meet in LDS and are added in K-part order.
 //
 // Dequantisation is the same as the prefill kernel's: codes enter the matrix
 // core as exact bf16 integers with an offset (int4: 136 + q, int8: 128 + q),
@@ -35,23 +38,28 @@ constexpr int kGemvRtDown = 2;
 
 namespace {
 
-// One ring slot: one K group of NT weight tiles (+ int4 scales) and the
-// lane's token activations for the group's 4 MFMA steps.
+// One K group of NT weight tiles (+ int4 scales).
 template <int WF, int NT>
-struct Slot {
+struct WSlot {
   static constexpr int NBLK = 128 / block_k(WF);
   u32x4 w[NT][NBLK];
   u32x2 s[NT];
+};
+
+// A ring slot: weights plus the group's activations in the B-operand layout.
+template <int WF, int NT>
+struct RSlot {
+  WSlot<WF, NT> w;
   u32x4 x[4];
 };
 
 // Weight loads address a uniform per-expert base plus a 32-bit offset
 // (global_load ... saddr form: one offset register per load).
 template <int WF, int NT>
-__device__ __forceinline__ void load_slot(Slot<WF, NT>& r, const uint8_t* wexp, const uint16_t* sexp,
-                                          const uint32_t (&rbo)[NT], const uint32_t (&sbo)[NT],
-                                          const uint8_t* xrow, int g, uint32_t lane) {
-  constexpr int NBLK = Slot<WF, NT>::NBLK;
+__device__ __forceinline__ void load_w(WSlot<WF, NT>& r, const uint8_t* wexp, const uint16_t* sexp,
+                                       const uint32_t (&rbo)[NT], const uint32_t (&sbo)[NT], int g,
+                                       uint32_t lane) {
+  constexpr int NBLK = WSlot<WF, NT>::NBLK;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
 #pragma unroll
@@ -59,29 +67,75 @@ __device__ __forceinline__ void load_slot(Slot<WF, NT>& r, const uint8_t* wexp, 
       r.w[t][i] = *(const u32x4*)(wexp + (rbo[t] + (uint32_t)(g * NBLK + i) * 1024u + lane * 16u));
     if (WF == WF_I4) r.s[t] = *(const u32x2*)(sexp + (sbo[t] + (uint32_t)g * 16u + 4u * (lane >> 4)));
   }
+}
+
+// B operand of group g, one load per MFMA step: lane l holds
+// x[row of column l%16][128g + 32s + 8(l/16) .. +7] in x[s].
+__device__ __forceinline__ void load_x_full(u32x4 (&x)[4], const uint8_t* xrow, int g) {
 #pragma unroll
-  for (int s = 0; s < 4; ++s) r.x[s] = *(const u32x4*)(xrow + (g * 128 + 32 * s) * 2);
+  for (int s = 0; s < 4; ++s) x[s] = *(const u32x4*)(xrow + (g * 128 + 32 * s) * 2);
+}
+
+// Sum of the group's 128 activations of the lane's column (lanes l, l^16,
+// l^32, l^48 hold its four 32-wide quarters).
+__device__ __forceinline__ float group_sum_full(const u32x4 (&x)[4]) {
+  float xs = 0.f;
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      xs += __uint_as_float(x[s][h] << 16);
+      xs += __uint_as_float(x[s][h] & 0xffff0000u);
+    }
+  xs += __shfl_xor(xs, 16);
+  xs += __shfl_xor(xs, 32);
+  return xs;
+}
+
+// Single-position tiles (most decode tiles) load their activations compactly:
+// lane j = l%16 of row q = l/16 loads chunk s = j%4, i.e.
+// x[row][128g + 32s + 8q .. +7] (lanes j >= 4 repeat j%4).  DPP row_newbcast:s
+// copies lane s of every 16-lane row to the whole row, which is exactly the B
+// operand of step s: one load and 16 lane moves in place of four loads.
+template <int N>
+__device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x150 + N, 0xf, 0xf, false);
+}
+
+template <int N>
+__device__ __forceinline__ u32x4 row_bcast4(u32x4 v) {
+  return u32x4{row_bcast<N>(v[0]), row_bcast<N>(v[1]), row_bcast<N>(v[2]), row_bcast<N>(v[3])};
+}
+
+__device__ __forceinline__ void single_operands(u32x4 xc, u32x4 (&xb)[4]) {
+  xb[0] = row_bcast4<0>(xc);
+  xb[1] = row_bcast4<1>(xc);
+  xb[2] = row_bcast4<2>(xc);
+  xb[3] = row_bcast4<3>(xc);
+}
+
+// Group sum of a single-position load: the 16 distinct chunks sit in lanes
+// (j%4, q); every lane ends with the total.
+__device__ __forceinline__ float single_group_sum(u32x4 xc) {
+  float v = 0.f;
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    v += __uint_as_float(xc[h] << 16);
+    v += __uint_as_float(xc[h] & 0xffff0000u);
+  }
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
 }
 
 // Adds one group's contribution to acc; use == false computes it and adds
-// nothing (a select, so no load is ever control-dependent).
+// nothing (a select, so no load is ever control-dependent).  xs: the group
+// sum of the lane's column (int formats).
 template <int WF, int NT>
-__device__ __forceinline__ void compute_slot(const Slot<WF, NT>& r, f32x4 (&acc)[NT], bool use) {
-  constexpr bool IS_INT = WF == WF_I4 || WF == WF_I8;
-  float xs = 0.f;
-  if (IS_INT) {
-    // sum of the group's 128 activations of the lane's token (lanes l, l^16,
-    // l^32, l^48 hold its four 32-wide quarters)
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        xs += __uint_as_float(r.x[s][h] << 16);
-        xs += __uint_as_float(r.x[s][h] & 0xffff0000u);
-      }
-    xs += __shfl_xor(xs, 16);
-    xs += __shfl_xor(xs, 32);
-  }
+__device__ __forceinline__ void mma_group(const WSlot<WF, NT>& r, const u32x4 (&xb)[4], float xs,
+                                          f32x4 (&acc)[NT], bool use) {
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     f32x4 tmp;
@@ -89,18 +143,18 @@ __device__ __forceinline__ void compute_slot(const Slot<WF, NT>& r, f32x4 (&acc)
       const float c = -136.0f * xs;
       tmp = f32x4{c, c, c, c};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) tmp = mfma_bf16(dq_i4(r.w[t][0][s]), r.x[s], tmp);
+      for (int s = 0; s < 4; ++s) tmp = mfma_bf16(dq_i4(r.w[t][0][s]), xb[s], tmp);
       tmp = bf16x4_to_f32(r.s[t]) * tmp;
     } else if (WF == WF_I8) {
       const float c = -128.0f * xs;
       tmp = f32x4{c, c, c, c};
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        tmp = mfma_bf16(dq_i8(r.w[t][s >> 1][2 * (s & 1)], r.w[t][s >> 1][2 * (s & 1) + 1]), r.x[s], tmp);
+        tmp = mfma_bf16(dq_i8(r.w[t][s >> 1][2 * (s & 1)], r.w[t][s >> 1][2 * (s & 1) + 1]), xb[s], tmp);
     } else {
       tmp = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) tmp = mfma_bf16(r.w[t][s], r.x[s], tmp);
+      for (int s = 0; s < 4; ++s) tmp = mfma_bf16(r.w[t][s], xb[s], tmp);
     }
 #pragma unroll
     for (int v = 0; v < 4; ++v) acc[t][v] = use ? acc[t][v] + tmp[v] : acc[t][v];
@@ -123,10 +177,13 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
   __shared__ f32x4 red[S > 1 ? S * P : 1][NT][64];
 
   const int tile = blockIdx.y;
-  const int n_tiles = a.n_tiles ? a.n_tiles[0] : (a.num_rows + 15) / 16;
-  if (tile >= n_tiles) return;
-
   const uint32_t lane = threadIdx.x & 63;
+  const int col = lane & 15;
+  // the input row of the lane's column comes straight from the tile index, so
+  // this load is issued first and waiting for it never waits for weights
+  int src = 0;
+  if (a.tile_src) src = a.tile_src[tile * kTileSrcCols + col];
+
   const int wave = threadIdx.x >> 6;
   const int kpart = wave % S;
   const int rs_raw = blockIdx.x * P + wave / S;
@@ -135,6 +192,8 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
   const int G = a.K / 128;
   const int NKB = a.K / block_k(WF);
 
+  // routed tiles: K2 writes every record up to the grid's max_tiles, those
+  // past the last tile with no rows (no wait for the tile count)
   int expert, row0, rows;
   if (a.n_tiles) {
     const int4 rec = *(const int4*)(a.tiles + 4 * tile);
@@ -146,10 +205,9 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
     row0 = tile * 16;
     rows = min(16, a.num_rows - row0);
   }
-  const int col = lane & 15;
-  int src = row0 + (col < rows ? col : 0);
-  if (a.perm) src = a.perm[src] / a.topk;
-  const uint8_t* xrow = (const uint8_t*)a.in + (int64_t)src * a.K * 2 + 16 * (lane >> 4);
+  if (rows <= 0) return;
+  if (!a.tile_src) src = row0 + (col < rows ? col : 0);  // rows read in place
+  const uint8_t* xbase = (const uint8_t*)a.in + 16 * (lane >> 4);
 
   const uint8_t* wexp = a.w + (int64_t)expert * a.w_expert_bytes;
   const uint16_t* sexp = a.scales + (int64_t)expert * a.s_expert_elems;
@@ -168,33 +226,64 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
   const int n = kpart < G ? (G - kpart + S - 1) / S : 0;
   const int n_last = n > 0 ? n - 1 : 0;
   const int g_base = kpart < G ? kpart : 0;
+  constexpr bool IS_INT = WF == WF_I4 || WF == WF_I8;
 
   f32x4 acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (NG > 0) {
-    Slot<WF, NT> sl[NG > 0 ? NG : 1];
+    // weights first: the activation addresses may still wait for src
+    WSlot<WF, NT> sl[NG > 0 ? NG : 1];
 #pragma unroll
-    for (int i = 0; i < NG; ++i)
-      load_slot<WF, NT>(sl[i], wexp, sexp, rbo, sbo, xrow, g_base + S * min(i, n_last), lane);
-    __builtin_amdgcn_sched_barrier(0);  // every load above the first use
+    for (int i = 0; i < NG; ++i) load_w<WF, NT>(sl[i], wexp, sexp, rbo, sbo, g_base + S * min(i, n_last), lane);
+    __builtin_amdgcn_sched_barrier(0);
+    // the B operands and group sums of the wave's groups; only these differ
+    // between the two activation forms (the weight math after the branch is
+    // shared, so nothing that waits for weights is hoisted above it)
+    u32x4 xb[NG > 0 ? NG : 1][4];
+    float xs[NG > 0 ? NG : 1];
+    if (rows == 1) {
+      const uint8_t* xtok = xbase + (int64_t)__builtin_amdgcn_readlane(src, 0) * a.K * 2 + 64 * (lane & 3);
+      u32x4 xc[NG > 0 ? NG : 1];
 #pragma unroll
-    for (int i = 0; i < NG; ++i) compute_slot<WF, NT>(sl[i], acc, i < n);
+      for (int i = 0; i < NG; ++i) xc[i] = *(const u32x4*)(xtok + (g_base + S * min(i, n_last)) * 256);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NG; ++i) {
+        single_operands(xc[i], xb[i]);
+        xs[i] = IS_INT ? single_group_sum(xc[i]) : 0.f;
+      }
+    } else {
+      const uint8_t* xrow = xbase + (int64_t)src * a.K * 2;
+#pragma unroll
+      for (int i = 0; i < NG; ++i) load_x_full(xb[i], xrow, g_base + S * min(i, n_last));
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NG; ++i) xs[i] = IS_INT ? group_sum_full(xb[i]) : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < NG; ++i) mma_group<WF, NT>(sl[i], xb[i], xs[i], acc, i < n);
   } else {
-    Slot<WF, NT> ring[D];
+    const uint8_t* xrow = xbase + (int64_t)src * a.K * 2;
+    RSlot<WF, NT> ring[D];
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-      load_slot<WF, NT>(ring[d], wexp, sexp, rbo, sbo, xrow, g_base + S * min(d, n_last), lane);
+    for (int d = 0; d < D; ++d) {
+      const int g = g_base + S * min(d, n_last);
+      load_w<WF, NT>(ring[d].w, wexp, sexp, rbo, sbo, g, lane);
+      load_x_full(ring[d].x, xrow, g);
+    }
     // sched_barrier: the scheduler would otherwise sink each refill down to
     // its use in the next iteration (shorter live ranges, no latency hiding)
     __builtin_amdgcn_sched_barrier(0);
     for (int i0 = 0; i0 < n; i0 += D) {
 #pragma unroll
       for (int d = 0; d < D; ++d) {
-        compute_slot<WF, NT>(ring[d], acc, i0 + d < n);
+        mma_group<WF, NT>(ring[d].w, ring[d].x, IS_INT ? group_sum_full(ring[d].x) : 0.f, acc, i0 + d < n);
         __builtin_amdgcn_sched_barrier(0);
-        load_slot<WF, NT>(ring[d], wexp, sexp, rbo, sbo, xrow, g_base + S * min(i0 + d + D, n_last), lane);
+        const int g = g_base + S * min(i0 + d + D, n_last);
+        load_w<WF, NT>(ring[d].w, wexp, sexp, rbo, sbo, g, lane);
+        load_x_full(ring[d].x, xrow, g);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -296,6 +385,7 @@ bool gemv_supported(int wf, int phase, int N, int K, int I) {
 
 hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream) {
   if (max_tiles <= 0) return hipSuccess;
+  if (a.perm && !a.tile_src) return hipErrorInvalidValue;  // gathered rows come from tile_src
   switch (wf) {
     case WF_BF16:
       return launch_gemv_wf<WF_BF16>(a, phase, max_tiles, stream);

@@ -43,12 +43,16 @@ struct GemmArgs {
   int act_bf16;
   const float* xsum;       // prefill, int formats: group sums of the input rows [rows, K/128]
   float* hsum;             // prefill gate_up: group sums of the stored h [positions, I/128]
+  const int32_t* tile_src; // decode gate_up: [max_tiles][kTileSrcCols] input row of each tile column
 };
 
 enum GemmPhase : int { PHASE_GATE_UP = 0, PHASE_DOWN = 1 };
 
 // positions per tile of the prefill form of K3
 constexpr int kPrefillTileM = 64;
+// positions per tile of the decode form; K2 then also writes, per tile, the
+// input row of each of its kTileSrcCols columns (0 past the tile's rows)
+constexpr int kTileSrcCols = 16;
 
 hipError_t launch_route(const void* logits, int act_bf16, int T, int E, int k, unsigned flags,
                         int32_t* ids, float* w, hipStream_t stream);
@@ -58,13 +62,13 @@ bool route_group_fused(int T, int k);
 hipError_t launch_route_group(const void* logits, int act_bf16, int T, int E, int k,
                               unsigned flags, int bm, int max_tiles, int32_t* ids, float* w,
                               int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
-                              int32_t* tiles, int32_t* n_tiles, hipStream_t stream);
+                              int32_t* tiles, int32_t* n_tiles, int32_t* tile_src, hipStream_t stream);
 
 // K2 over many workgroups (large batches): hist holds group_hist_blocks(T*k) x E int32.
 int group_hist_blocks(int P);
 hipError_t launch_group_multi(const int32_t* ids, int T, int k, int E, int bm, int max_tiles, int32_t* hist,
                               int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* tiles,
-                              int32_t* n_tiles, hipStream_t stream);
+                              int32_t* n_tiles, int32_t* tile_src, hipStream_t stream);
 
 // Tile shapes: returns the token-tile height (BM) used for num_tokens:
 // 16 for decode-sized expert groups (gemv form), else kPrefillTileM when

@@ -230,7 +230,8 @@ __device__ __forceinline__ void group_body(const int32_t* ids, int T, int k, int
                                            int32_t* __restrict__ offsets,
                                            int32_t* __restrict__ perm, int32_t* __restrict__ inv,
                                            int32_t* __restrict__ tiles,
-                                           int32_t* __restrict__ n_tiles, GroupLds& L) {
+                                           int32_t* __restrict__ n_tiles,
+                                           int32_t* __restrict__ tile_src, GroupLds& L) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -320,27 +321,32 @@ __device__ __forceinline__ void group_body(const int32_t* ids, int T, int k, int
       const int pos = L.hist[wave][e] + rank;
       perm[pos] = p;
       inv[p] = pos;
-      __builtin_amdgcn_s_waitcnt(0);
+      if (tile_src) {
+        const int rel = pos - L.off_s[e];
+        const int ti = L.tile_off[e] + rel / bm;
+        if (ti < max_tiles) tile_src[ti * kTileSrcCols + rel % bm] = p / k;
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): every lane has read its start
       if (rank == cnt - 1) L.hist[wave][e] += cnt;
     }
   }
 
-  // tile list for the grouped GEMMs: (expert, first position, rows)
+  // tile list for the grouped GEMMs: (expert, first position, rows); lane
+  // group lane/16 takes a tile, its 16 lanes the tile's source-row padding
   for (int e = wave; e < E; e += kGroupWaves) {
     const int c = L.tot[e];
     const int nt = (c + bm - 1) / bm;
-    for (int m = lane; m < nt; m += 64) {
+    for (int m = lane >> 4; m < nt; m += 4) {
       const int ti = L.tile_off[e] + m;
       if (ti < max_tiles) {
-        int4 rec;
-        rec.x = e;
-        rec.y = L.off_s[e] + m * bm;
-        rec.z = min(bm, c - m * bm);
-        rec.w = 0;
-        *(int4*)(tiles + 4 * ti) = rec;
+        const int rows = min(bm, c - m * bm);
+        if ((lane & 15) == 0) *(int4*)(tiles + 4 * ti) = int4{e, L.off_s[e] + m * bm, rows, 0};
+        if (tile_src && (lane & 15) >= rows) tile_src[ti * kTileSrcCols + (lane & 15)] = 0;
       }
     }
   }
+  // records past the last tile say "no rows" (the decode form reads every record up to max_tiles)
+  for (int ti = L.tile_off[E] + tid; ti < max_tiles; ti += blockDim.x) *(int4*)(tiles + 4 * ti) = int4{0, 0, 0, 0};
   if (tid == 0) n_tiles[0] = min(L.tile_off[E], max_tiles);
 }
 
@@ -370,13 +376,14 @@ __global__ void __launch_bounds__(1024) count_kernel(const int32_t* __restrict__
   if (tid < E) hist[(int64_t)blockIdx.x * E + tid] = h[tid];
 }
 
-__global__ void __launch_bounds__(1024) scatter_kernel(const int32_t* __restrict__ ids, int P, int E, int bm,
+__global__ void __launch_bounds__(1024) scatter_kernel(const int32_t* __restrict__ ids, int P, int k, int E, int bm,
                                                        int max_tiles, const int32_t* __restrict__ hist,
                                                        int32_t* __restrict__ counts,
                                                        int32_t* __restrict__ offsets,
                                                        int32_t* __restrict__ perm, int32_t* __restrict__ inv,
                                                        int32_t* __restrict__ tiles,
-                                                       int32_t* __restrict__ n_tiles) {
+                                                       int32_t* __restrict__ n_tiles,
+                                                       int32_t* __restrict__ tile_src) {
   __shared__ int32_t tot[kMaxExperts], pre[kMaxExperts], off_s[kMaxExperts + 1], tile_off[kMaxExperts + 1];
   __shared__ int32_t whist[kScatterWaves][kMaxExperts];
   const int tid = threadIdx.x;
@@ -455,18 +462,17 @@ __global__ void __launch_bounds__(1024) scatter_kernel(const int32_t* __restrict
       offsets[E] = off_s[E];
       n_tiles[0] = min(tile_off[E], max_tiles);
     }
+    // records past the last tile say "no rows" (the decode form reads every record up to max_tiles)
+    for (int ti = tile_off[E] + tid; ti < max_tiles; ti += 1024) *(int4*)(tiles + 4 * ti) = int4{0, 0, 0, 0};
     for (int e = wave; e < E; e += kScatterWaves) {
       const int c = tot[e];
       const int nt = (c + bm - 1) / bm;
-      for (int m = lane; m < nt; m += 64) {
+      for (int m = lane >> 4; m < nt; m += 4) {
         const int ti = tile_off[e] + m;
         if (ti < max_tiles) {
-          int4 rec;
-          rec.x = e;
-          rec.y = off_s[e] + m * bm;
-          rec.z = min(bm, c - m * bm);
-          rec.w = 0;
-          *(int4*)(tiles + 4 * ti) = rec;
+          const int rows = min(bm, c - m * bm);
+          if ((lane & 15) == 0) *(int4*)(tiles + 4 * ti) = int4{e, off_s[e] + m * bm, rows, 0};
+          if (tile_src && (lane & 15) >= rows) tile_src[ti * kTileSrcCols + (lane & 15)] = 0;
         }
       }
     }
@@ -491,7 +497,12 @@ __global__ void __launch_bounds__(1024) scatter_kernel(const int32_t* __restrict
       const int pos = whist[wave][e] + rank;
       perm[pos] = p;
       inv[p] = pos;
-      __builtin_amdgcn_s_waitcnt(0);
+      if (tile_src) {
+        const int rel = pos - off_s[e];
+        const int ti = tile_off[e] + rel / bm;
+        if (ti < max_tiles) tile_src[ti * kTileSrcCols + rel % bm] = p / k;
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): every lane has read its start
       if (rank == cnt - 1) whist[wave][e] += cnt;
     }
   }
@@ -501,15 +512,16 @@ int group_hist_blocks(int P) { return (P + kPairsPerBlock - 1) / kPairsPerBlock;
 
 hipError_t launch_group_multi(const int32_t* ids, int T, int k, int E, int bm, int max_tiles, int32_t* hist,
                               int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* tiles,
-                              int32_t* n_tiles, hipStream_t stream) {
+                              int32_t* n_tiles, int32_t* tile_src, hipStream_t stream) {
+  if (tile_src && bm != kTileSrcCols) return hipErrorInvalidValue;
   const int P = T * k;
   const int nb = group_hist_blocks(P);
   if (nb <= 0) return hipSuccess;
   hipLaunchKernelGGL(count_kernel, dim3(nb), dim3(1024), 0, stream, ids, P, E, hist);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(scatter_kernel, dim3(nb), dim3(1024), 0, stream, ids, P, E, bm, max_tiles, hist, counts,
-                     offsets, perm, inv, tiles, n_tiles);
+  hipLaunchKernelGGL(scatter_kernel, dim3(nb), dim3(1024), 0, stream, ids, P, k, E, bm, max_tiles, hist, counts,
+                     offsets, perm, inv, tiles, n_tiles, tile_src);
   return hipGetLastError();
 }
 
@@ -520,7 +532,7 @@ __global__ void __launch_bounds__(1024) route_group_kernel(
     const void* __restrict__ logits, int T, int E, int k, unsigned flags, int bm, int max_tiles,
     int32_t* __restrict__ ids_out, float* __restrict__ w_out, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ inv,
-    int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles) {
+    int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles, int32_t* __restrict__ tile_src) {
   __shared__ GroupLds L;
   __shared__ int32_t ids_s[kFusedRouteMaxPairs];
   __shared__ float sv[kGroupWaves][kMaxTopK];
@@ -538,7 +550,7 @@ __global__ void __launch_bounds__(1024) route_group_kernel(
     }
   }
   __syncthreads();
-  group_body(ids_s, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, L);
+  group_body(ids_s, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, tile_src, L);
 }
 
 #define NKT_VPL_SWITCH(E, CASE) \
@@ -574,20 +586,21 @@ bool route_group_fused(int T, int k) { return T <= kFusedRouteMaxTokens && T * k
 hipError_t launch_route_group(const void* logits, int act_bf16, int T, int E, int k,
                               unsigned flags, int bm, int max_tiles, int32_t* ids, float* w,
                               int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
-                              int32_t* tiles, int32_t* n_tiles, hipStream_t stream) {
+                              int32_t* tiles, int32_t* n_tiles, int32_t* tile_src, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
   if (!route_group_fused(T, k)) return hipErrorInvalidValue;
+  if (tile_src && bm != kTileSrcCols) return hipErrorInvalidValue;
   dim3 grid(1), block(64 * kGroupWaves);
 #define NKT_RG_CASE(V)                                                                          \
   case V:                                                                                       \
     if (act_bf16)                                                                               \
       hipLaunchKernelGGL((route_group_kernel<V, true>), grid, block, 0, stream, logits, T, E, k, \
                          flags, bm, max_tiles, ids, w, counts, offsets, perm, inv, tiles,       \
-                         n_tiles);                                                              \
+                         n_tiles, tile_src);                                                    \
     else                                                                                        \
       hipLaunchKernelGGL((route_group_kernel<V, false>), grid, block, 0, stream, logits, T, E,  \
                          k, flags, bm, max_tiles, ids, w, counts, offsets, perm, inv, tiles,    \
-                         n_tiles);                                                              \
+                         n_tiles, tile_src);                                                    \
     break;
   NKT_VPL_SWITCH(E, NKT_RG_CASE)
 #undef NKT_RG_CASE
