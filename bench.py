@@ -183,6 +183,50 @@ def time_stages(layers, xs, ls, outs, rounds):
     return {n: acc[n] / count for n in names}
 
 
+def time_kernel(layers, xs, ls, phase, passes=5):
+    """Average duration (us) of one expert-GEMM kernel (phase 0: gate_up + SwiGLU,
+    1: down).  Every layer copy is routed (and its gate_up run) first; then each
+    launch of the phase carries its own pair of HIP events, stamped by the
+    dispatch at the kernel's start and end (nkt_moe_experts_phase_timed), on the
+    stream the kernel runs on.  A sleep kernel keeps the host ahead so the
+    launches run back to back over the rotating weight copies."""
+    import torch
+
+    T = xs[0].shape[0]
+    for i, layer in enumerate(layers):
+        layer.route(ls[i % len(ls)])
+        layer.expert_phase(0, xs[i % len(xs)], T)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    pairs = []
+    for _ in range(passes * len(layers)):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)  # creates the events; the launch re-stamps them
+        b.record(stream)
+        pairs.append((a, b))
+    torch.cuda.synchronize()
+    try:
+        torch.cuda._sleep(20_000_000)
+    except Exception:
+        pass
+    n = 0
+    for _ in range(passes):
+        for i, layer in enumerate(layers):
+            a, b = pairs[n]
+            layer.expert_phase_timed(phase, xs[i % len(xs)] if phase == 0 else None, T, a, b)
+            n += 1
+    torch.cuda.synchronize()
+    times = [a.elapsed_time(b) * 1e3 for a, b in pairs]
+    return sum(times) / len(times)
+
+
+def kernel_form(w, T):
+    """Which K3 kernel the library runs for this shape (mirrors gemm_tile_m)."""
+    if T * w.k <= 12 * w.E:
+        return "gemv_kernel"
+    return "gemm2_kernel" if w.wfmt != "f32" else "gemm_kernel"
+
+
 def bench_workload(w, T, layers, router, steps, warmup, device):
     import torch
 
@@ -192,6 +236,8 @@ def bench_workload(w, T, layers, router, steps, warmup, device):
     mean_act = sum(n_act) / len(n_act)
     ms, timed = time_graph(layers, xs, ls, outs, steps, warmup)
     stages = time_stages(layers, xs, ls, outs, rounds=3)
+    gate_up_us = time_kernel(layers, xs, ls, 0)
+    down_us = time_kernel(layers, xs, ls, 1)
     P = T * w.k
     gate_up_bytes = mean_act * w.bytes_per_expert("gate_up") + T * w.H * 2 + P * w.I * 2
     down_bytes = mean_act * w.bytes_per_expert("down") + P * w.I * 2 + P * w.H * 4
@@ -199,27 +245,52 @@ def bench_workload(w, T, layers, router, steps, warmup, device):
                    + T * w.H * 2 * 2 + T * w.E * 2)
     gate_up_flops = 2.0 * P * 2 * w.I * w.H
     down_flops = 2.0 * P * w.H * w.I
-    return dict(workload=w.name, tokens=T, ms_per_step=ms, us_per_layer=ms * 1e3, steps=timed,
+    form = kernel_form(w, T)
+    return dict(workload=w.name, wfmt=w.wfmt, tokens=T, ms_per_step=ms, us_per_layer=ms * 1e3, steps=timed,
                 tokens_per_s=T / (ms * 1e-3), mean_active_experts=mean_act, breakdown_us=stages,
                 layer_bytes=layer_bytes, layer_hbm_frac=layer_bytes / (ms * 1e-3) / HBM_PEAK,
-                gate_up=dict(bytes=gate_up_bytes, flops=gate_up_flops, us=stages["gate_up"]),
-                down=dict(bytes=down_bytes, flops=down_flops, us=stages["down"]))
+                gate_up=dict(kernel=form, bytes=gate_up_bytes, flops=gate_up_flops, us=gate_up_us),
+                down=dict(kernel=form, bytes=down_bytes, flops=down_flops, us=down_us))
+
+
+def traffic_table():
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE, WRITE_SIZE),
+    calibrated on a copy kernel, from profiles/pmc_traffic_moe_layer.md (None if absent)."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic_moe_layer.md")
+    try:
+        text = open(path).read()
+    except OSError:
+        return {}
+    out = {}
+    for line in text.splitlines():
+        # | key | fetch bytes | write bytes | traffic bytes | ...
+        if line.startswith("| `traffic:"):
+            cells = [c.strip() for c in line.strip("|").split("|")]
+            try:
+                out[cells[0].strip("`")[len("traffic:"):]] = float(cells[3])
+            except (ValueError, IndexError):
+                pass
+    return out
 
 
 def roofline_for(res, bound):
-    """Roofline of the dominant kernel (the larger of the two expert GEMM launches)."""
+    """Roofline of the dominant kernel (the longer of the two expert-GEMM kernels),
+    its duration from the dispatch-stamped events of time_kernel."""
     k = "gate_up" if res["gate_up"]["us"] >= res["down"]["us"] else "down"
     d = res[k]
     sec = d["us"] * 1e-6
+    name = f"{d['kernel']} ({k}, {res['wfmt']}, T={res['tokens']})"
+    traffic = traffic_table().get(f"{d['kernel']}:{k}:{res['wfmt']}:{res['tokens']}")
     if bound == "hbm":
         achieved = d["bytes"] / sec / 1e9
-        return dict(kernel=f"gemm_kernel ({k})", bound="hbm", achieved=round(achieved, 1),
+        return dict(kernel=name, bound="hbm", achieved=round(achieved, 1),
                     peak=HBM_PEAK / 1e9, unit="GB/s", frac=round(achieved * 1e9 / HBM_PEAK, 4),
-                    traffic=None, algorithmic_bytes_per_launch=round(d["bytes"]))
+                    traffic=traffic, algorithmic_bytes_per_launch=round(d["bytes"]),
+                    us_per_launch=round(d["us"], 2))
     achieved = d["flops"] / sec / 1e12
-    return dict(kernel=f"gemm_kernel ({k})", bound="mfma", achieved=round(achieved, 1),
+    return dict(kernel=name, bound="mfma", achieved=round(achieved, 1),
                 peak=MFMA_BF16_PEAK / 1e12, unit="TFLOP/s", frac=round(achieved * 1e12 / MFMA_BF16_PEAK, 4),
-                traffic=None, algorithmic_flops_per_launch=d["flops"])
+                traffic=traffic, algorithmic_flops_per_launch=d["flops"], us_per_launch=round(d["us"], 2))
 
 
 # --------------------------------------------------------------------- CPU baseline
@@ -272,6 +343,112 @@ def cpu_baseline(w, T, budget_s=15.0):
                        f"{sec * 1e3:.0f} ms; numpy fp32 grouped-matvec loop, BLAS limited to 1 thread")
 
 
+# --------------------------------------------------------------------- HBM traffic (rocprofv3 --pmc)
+PMC_COPY_BYTES = 256 << 20   # the calibration kernel reads and writes this many bytes
+PMC_KERNELS = {  # kernel-name prefix -> traffic key (kernel:phase:weights:tokens) of the probe's launches
+    "nkt::gemv_kernel<3, 0,": "gemv_kernel:gate_up:int4_g128:16",
+    "nkt::gemv_kernel<3, 1,": "gemv_kernel:down:int4_g128:16",
+}
+
+
+def pmc_probe():
+    """Launches for a counter run (counters restricted to these kernels with
+    --kernel-include-regex): a calibration kernel of known traffic (fp32 negate,
+    PMC_COPY_BYTES in and out), then route + both expert GEMMs of the headline
+    decode (int4, T=16, 8 weight copies)."""
+    import torch
+
+    dev = torch.device("cuda", 0)
+    a = torch.ones(PMC_COPY_BYTES // 4, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        torch.neg(a, out=b)
+    torch.cuda.synchronize()
+    del a, b
+    for w, copies in ((Workload("decode", tokens=16, **QWEN3_INT4), 8),):
+        log(f"pmc probe: {w.wfmt} T={w.tokens}")
+        router, layers = make_layers(w, copies, dev, max_tokens=w.tokens)
+        xs, ls = make_inputs(w, router, w.tokens, 8, dev)
+        for _ in range(2):
+            for i, layer in enumerate(layers):
+                layer.route(ls[i % len(ls)])
+                layer.expert_phase(0, xs[i % len(xs)], w.tokens)
+                layer.expert_phase(1, None, w.tokens)
+        torch.cuda.synchronize()
+        del layers
+        torch.cuda.empty_cache()
+    log("pmc probe done")
+
+
+def _pmc_per_kernel(path, counter):
+    """Mean per-dispatch value of one counter for every kernel name in a rocprofv3 counter CSV."""
+    import collections
+    import csv
+
+    per_dispatch = collections.defaultdict(float)
+    for r in csv.DictReader(open(path)):
+        if r.get("Counter_Name") != counter:
+            continue
+        per_dispatch[(r["Kernel_Name"], r.get("Dispatch_Id", ""))] += float(r["Counter_Value"])
+    by_name = collections.defaultdict(list)
+    for (name, _), v in per_dispatch.items():
+        by_name[name].append(v)
+    return {name: sum(v) / len(v) for name, v in by_name.items()}
+
+
+def summarize_trace(trace_csv):
+    """Markdown table of the nkt kernels in a rocprofv3 kernel-trace CSV, grouped by
+    kernel and launch grid (workgroups in x, y): durations End - Start."""
+    import collections
+    import csv
+    import statistics
+
+    d = collections.defaultdict(list)
+    meta = {}
+    for r in csv.DictReader(open(trace_csv)):
+        n = r["Kernel_Name"]
+        if "nkt::" not in n:
+            continue
+        name = n.split("(")[0].replace("void ", "")
+        key = (name, int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"]), int(r["Grid_Size_Y"]))
+        d[key].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+        meta[key] = (r["VGPR_Count"], r["Accum_VGPR_Count"], r["LDS_Block_Size"], r["Scratch_Size"],
+                     r["Workgroup_Size_X"])
+    print("| kernel | grid (x, y) | wg | calls | avg us | median us | min us | vgpr/agpr | lds B | scratch |")
+    print("|---|---|---|---|---|---|---|---|---|---|")
+    for k, v in sorted(d.items()):
+        m = meta[k]
+        print(f"| `{k[0]}` | {k[1]}, {k[2]} | {m[4]} | {len(v)} | {statistics.mean(v) / 1e3:.2f} | "
+              f"{statistics.median(v) / 1e3:.2f} | {min(v) / 1e3:.2f} | {m[0]}/{m[1]} | {m[2]} | {m[3]} |")
+
+
+def summarize_pmc(fetch_csv, write_csv):
+    """Markdown rows of HBM bytes per launch: FETCH_SIZE and WRITE_SIZE (KiB per dispatch),
+    each scaled by the factor that makes the calibration kernel read / write PMC_COPY_BYTES."""
+    fetch = _pmc_per_kernel(fetch_csv, "FETCH_SIZE")
+    write = _pmc_per_kernel(write_csv, "WRITE_SIZE")
+
+    def calib(d, what):
+        cal = [v for n, v in d.items() if "neg_kernel" in n]
+        if not cal:
+            raise SystemExit(f"no calibration kernel in the {what} counters")
+        return PMC_COPY_BYTES / (cal[0] * 1024.0), cal[0]
+
+    ff, fraw = calib(fetch, "FETCH_SIZE")
+    wf, wraw = calib(write, "WRITE_SIZE")
+    print(f"calibration (fp32 negate, {PMC_COPY_BYTES} B in and out): FETCH_SIZE {fraw:.0f} KiB -> factor "
+          f"{ff:.4f}; WRITE_SIZE {wraw:.0f} KiB -> factor {wf:.4f}\n")
+    print("| key | HBM read B/launch | HBM write B/launch | traffic B/launch | FETCH_SIZE KiB | WRITE_SIZE KiB |")
+    print("|---|---|---|---|---|---|")
+    for prefix, key in PMC_KERNELS.items():
+        fk = [v for n, v in fetch.items() if prefix in n]
+        wk = [v for n, v in write.items() if prefix in n]
+        if not fk or not wk:
+            continue
+        rd, wr = fk[0] * 1024.0 * ff, wk[0] * 1024.0 * wf
+        print(f"| `traffic:{key}` | {rd:.0f} | {wr:.0f} | {rd + wr:.0f} | {fk[0]:.0f} | {wk[0]:.0f} |")
+
+
 # --------------------------------------------------------------------- main
 def main():
     ap = argparse.ArgumentParser()
@@ -282,7 +459,18 @@ def main():
     ap.add_argument("--layers", type=int, default=8, help="distinct weight copies rotated per step")
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-probe", action="store_true", help="only the launches of a rocprofv3 --pmc run")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print HBM traffic per launch from two rocprofv3 --pmc counter CSVs")
+    ap.add_argument("--summarize-trace", metavar="TRACE_CSV",
+                    help="print the nkt kernels of a rocprofv3 kernel-trace CSV as a markdown table")
     args = ap.parse_args()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace)
+        return
+    if args.summarize_pmc:
+        summarize_pmc(*args.summarize_pmc)
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (the MoE path here has no multi-GPU build); got --gpus {args.gpus}",
               file=sys.stderr)
@@ -292,6 +480,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs the MI355X GPU", file=sys.stderr)
         sys.exit(1)
+    if args.pmc_probe:
+        pmc_probe()
+        return
     dev = torch.device("cuda", 0)
     head = Workload("qwen3_30b_a3b_moe_layer_int4_g128_decode", tokens=args.tokens, **QWEN3_INT4)
     log(f"building {args.layers} copies of the int4 layer")

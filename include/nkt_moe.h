@@ -136,6 +136,15 @@ int nkt_moe_experts_phase(void* handle, int phase, const void* hidden_states, in
                           void* workspace, size_t workspace_bytes, void* stream, char* err,
                           size_t err_len);
 
+/* nkt_moe_experts_phase with the phase's expert-GEMM kernel stamped by two
+ * hipEvent_t (start_event, stop_event) at its own start and end
+ * (hipExtLaunchKernelGGL), so that hipEventElapsedTime gives that kernel's
+ * duration without launch gaps.  No counterpart in the reference: a
+ * measurement hook for benchmarks (bench.py's roofline). */
+int nkt_moe_experts_phase_timed(void* handle, int phase, const void* hidden_states, int num_tokens,
+                                void* workspace, size_t workspace_bytes, void* stream, void* start_event,
+                                void* stop_event, char* err, size_t err_len);
+
 /* K4 (+ K3 with one dense expert): shared expert and its sigmoid gate,
  * nano_ktrans/models/mixtral.py:170-179, 215-218.  Writes NKT_WS_SHARED_*. */
 int nkt_moe_shared(void* handle, const void* hidden_states, int num_tokens, void* workspace,

@@ -271,21 +271,21 @@ int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, 
 // The prefill form's gate_up first sums the activations per 128-wide group
 // (int formats; the down projection reads the sums gate_up writes).
 hipError_t launch_expert_gemm(const Handle* h, const GemmArgs& a, int phase, int bm, int tiles,
-                              hipStream_t st) {
-  if (bm == 16 && gemv_supported(h->wf, phase, a.N, a.K, a.I)) return launch_gemv(a, h->wf, phase, tiles, st);
+                              hipStream_t st, const KernelTimer* tm = nullptr) {
+  if (bm == 16 && gemv_supported(h->wf, phase, a.N, a.K, a.I)) return launch_gemv(a, h->wf, phase, tiles, st, tm);
   if (bm == kPrefillTileM && gemm2_supported(h->wf, phase, a.N, a.K, a.I)) {
     if (phase == PHASE_GATE_UP && (h->wf == WF_I4 || h->wf == WF_I8)) {
       const hipError_t e = launch_group_sums(a.in, (a.perm ? a.num_rows / a.topk : a.num_rows), a.K,
                                              const_cast<float*>(a.xsum), st);
       if (e != hipSuccess) return e;
     }
-    return launch_gemm2(a, h->wf, phase, tiles, st);
+    return launch_gemm2(a, h->wf, phase, tiles, st, tm);
   }
-  return launch_gemm(a, h->wf, phase, bm, tiles, st);
+  return launch_gemm(a, h->wf, phase, bm, tiles, st, tm);
 }
 
 int do_expert_phase(Handle* h, int phase, const void* x, int T, void* ws, const WsLayout& L,
-                    hipStream_t st, char* err, size_t len) {
+                    hipStream_t st, char* err, size_t len, const KernelTimer* tm = nullptr) {
   if (phase == PHASE_GATE_UP && !x) {
     set_err(err, len, "null hidden_states");
     return NKT_ERR;
@@ -293,11 +293,11 @@ int do_expert_phase(Handle* h, int phase, const void* x, int T, void* ws, const 
   if (!check_weights(h, false, err, len)) return NKT_ERR;
   if (phase == PHASE_GATE_UP) {
     GemmArgs a = expert_args(h, PHASE_GATE_UP, false, x, ws, L, T);
-    if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, L.bm, L.max_tiles, st), "gate_up gemm", err, len))
+    if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, L.bm, L.max_tiles, st, tm), "gate_up gemm", err, len))
       return NKT_ERR;
   } else {
     GemmArgs b = expert_args(h, PHASE_DOWN, false, ws_ptr<void>(ws, L, NKT_WS_H), ws, L, T);
-    if (!check_hip(launch_expert_gemm(h, b, PHASE_DOWN, L.bm, L.max_tiles, st), "down gemm", err, len))
+    if (!check_hip(launch_expert_gemm(h, b, PHASE_DOWN, L.bm, L.max_tiles, st, tm), "down gemm", err, len))
       return NKT_ERR;
   }
   return NKT_OK;
@@ -536,6 +536,26 @@ int nkt_moe_experts_phase(void* handle, int phase, const void* hidden_states, in
   const WsLayout L = ws_layout(h, num_tokens);
   return do_expert_phase(h, phase, hidden_states, num_tokens, workspace, L, (hipStream_t)stream, err,
                          err_len);
+}
+
+int nkt_moe_experts_phase_timed(void* handle, int phase, const void* hidden_states, int num_tokens,
+                                void* workspace, size_t workspace_bytes, void* stream, void* start_event,
+                                void* stop_event, char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!check_call(h, num_tokens, workspace, workspace_bytes, err, err_len)) return NKT_ERR;
+  if (phase != PHASE_GATE_UP && phase != PHASE_DOWN) {
+    set_err(err, err_len, "phase must be 0 (gate_up) or 1 (down), got %d", phase);
+    return NKT_ERR;
+  }
+  if (!start_event || !stop_event) {
+    set_err(err, err_len, "null timing event");
+    return NKT_ERR;
+  }
+  if (num_tokens == 0) return NKT_OK;
+  const WsLayout L = ws_layout(h, num_tokens);
+  const KernelTimer tm{(hipEvent_t)start_event, (hipEvent_t)stop_event};
+  return do_expert_phase(h, phase, hidden_states, num_tokens, workspace, L, (hipStream_t)stream, err,
+                         err_len, &tm);
 }
 
 int nkt_moe_shared(void* handle, const void* hidden_states, int num_tokens, void* workspace,

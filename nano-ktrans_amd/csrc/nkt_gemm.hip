@@ -366,7 +366,8 @@ int gemm_rows_per_block(int wf, int phase, int bm) {
 }
 
 template <int WF, int BM, int PHASE>
-static hipError_t launch_gemm_t(const GemmArgs& a, int grid_tiles, hipStream_t stream) {
+static hipError_t launch_gemm_t(const GemmArgs& a, int grid_tiles, hipStream_t stream,
+                                const KernelTimer* tm) {
   constexpr int NW = (BM == 16) ? 8 : 4;
   constexpr int RT = (BM == 16) ? 2 : 4;
   // LDS stage: BM x KC activations (~33 KiB); fp32 activations take half the K
@@ -377,38 +378,37 @@ static hipError_t launch_gemm_t(const GemmArgs& a, int grid_tiles, hipStream_t s
   const int out_dim = (PHASE == PHASE_GATE_UP) ? a.I : a.N;
   const int rows_per_block = NW * ((PHASE == PHASE_GATE_UP) ? RT / 2 : RT) * 16;
   dim3 grid(grid_tiles, (out_dim + rows_per_block - 1) / rows_per_block);
-  hipLaunchKernelGGL((gemm_kernel<WF, BM, NW, RT, PHASE, KC, PF>), grid, dim3(NW * 64), 0, stream,
-                     a);
+  launch_timed(gemm_kernel<WF, BM, NW, RT, PHASE, KC, PF>, grid, dim3(NW * 64), 0, stream, tm, a);
   return hipGetLastError();
 }
 
 template <int WF>
 static hipError_t launch_gemm_wf(const GemmArgs& a, int phase, int bm, int grid_tiles,
-                                 hipStream_t stream) {
+                                 hipStream_t stream, const KernelTimer* tm) {
   if (phase == PHASE_GATE_UP) {
-    if (bm == 16) return launch_gemm_t<WF, 16, PHASE_GATE_UP>(a, grid_tiles, stream);
-    if (bm == 32) return launch_gemm_t<WF, 32, PHASE_GATE_UP>(a, grid_tiles, stream);
-    if (bm == 64) return launch_gemm_t<WF, 64, PHASE_GATE_UP>(a, grid_tiles, stream);
+    if (bm == 16) return launch_gemm_t<WF, 16, PHASE_GATE_UP>(a, grid_tiles, stream, tm);
+    if (bm == 32) return launch_gemm_t<WF, 32, PHASE_GATE_UP>(a, grid_tiles, stream, tm);
+    if (bm == 64) return launch_gemm_t<WF, 64, PHASE_GATE_UP>(a, grid_tiles, stream, tm);
   } else {
-    if (bm == 16) return launch_gemm_t<WF, 16, PHASE_DOWN>(a, grid_tiles, stream);
-    if (bm == 32) return launch_gemm_t<WF, 32, PHASE_DOWN>(a, grid_tiles, stream);
-    if (bm == 64) return launch_gemm_t<WF, 64, PHASE_DOWN>(a, grid_tiles, stream);
+    if (bm == 16) return launch_gemm_t<WF, 16, PHASE_DOWN>(a, grid_tiles, stream, tm);
+    if (bm == 32) return launch_gemm_t<WF, 32, PHASE_DOWN>(a, grid_tiles, stream, tm);
+    if (bm == 64) return launch_gemm_t<WF, 64, PHASE_DOWN>(a, grid_tiles, stream, tm);
   }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemm(const GemmArgs& a, int wf, int phase, int bm, int grid_tiles,
-                       hipStream_t stream) {
+                       hipStream_t stream, const KernelTimer* tm) {
   if (grid_tiles <= 0) return hipSuccess;
   switch (wf) {
     case WF_F32:
-      return launch_gemm_wf<WF_F32>(a, phase, bm, grid_tiles, stream);
+      return launch_gemm_wf<WF_F32>(a, phase, bm, grid_tiles, stream, tm);
     case WF_BF16:
-      return launch_gemm_wf<WF_BF16>(a, phase, bm, grid_tiles, stream);
+      return launch_gemm_wf<WF_BF16>(a, phase, bm, grid_tiles, stream, tm);
     case WF_I8:
-      return launch_gemm_wf<WF_I8>(a, phase, bm, grid_tiles, stream);
+      return launch_gemm_wf<WF_I8>(a, phase, bm, grid_tiles, stream, tm);
     case WF_I4:
-      return launch_gemm_wf<WF_I4>(a, phase, bm, grid_tiles, stream);
+      return launch_gemm_wf<WF_I4>(a, phase, bm, grid_tiles, stream, tm);
     default:
       return hipErrorInvalidValue;
   }

@@ -363,7 +363,8 @@ hipError_t launch_group_sums(const void* x, int rows, int K, float* out, hipStre
   return hipGetLastError();
 }
 
-hipError_t launch_gemm2(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream) {
+hipError_t launch_gemm2(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream,
+                        const KernelTimer* tm) {
   if (max_tiles <= 0) return hipSuccess;
   const int n_slabs = phase == PHASE_GATE_UP ? a.I / 128 : a.N / 256;
   const int64_t items = (int64_t)n_slabs * max_tiles;
@@ -371,9 +372,9 @@ hipError_t launch_gemm2(const GemmArgs& a, int wf, int phase, int max_tiles, hip
 #define NKT_G2(W)                                                                                  \
   case W:                                                                                          \
     if (phase == PHASE_GATE_UP)                                                                    \
-      hipLaunchKernelGGL((gemm2_kernel<W, PHASE_GATE_UP>), grid, block, 0, stream, a, n_slabs);    \
+      launch_timed(gemm2_kernel<W, PHASE_GATE_UP>, grid, block, 0, stream, tm, a, n_slabs);        \
     else                                                                                           \
-      hipLaunchKernelGGL((gemm2_kernel<W, PHASE_DOWN>), grid, block, 0, stream, a, n_slabs);       \
+      launch_timed(gemm2_kernel<W, PHASE_DOWN>, grid, block, 0, stream, tm, a, n_slabs);           \
     break;
   switch (wf) {
     NKT_G2(WF_BF16)

@@ -337,11 +337,12 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
 namespace {
 
 template <int WF, int PHASE, int RT, int S, int NG>
-hipError_t launch_gemv_s(const GemmArgs& a, int max_tiles, int n_rowsets, hipStream_t stream) {
+hipError_t launch_gemv_s(const GemmArgs& a, int max_tiles, int n_rowsets, hipStream_t stream,
+                         const KernelTimer* tm) {
   constexpr int P = gemv_rowsets_per_wg(S);
   constexpr int D = (WF == WF_BF16) ? 2 : 3;
   dim3 grid((n_rowsets + P - 1) / P, max_tiles);
-  hipLaunchKernelGGL((gemv_kernel<WF, PHASE, RT, S, NG, D>), grid, dim3(S * P * 64), 0, stream, a, n_rowsets);
+  launch_timed(gemv_kernel<WF, PHASE, RT, S, NG, D>, grid, dim3(S * P * 64), 0, stream, tm, a, n_rowsets);
   return hipGetLastError();
 }
 
@@ -351,26 +352,27 @@ hipError_t launch_gemv_s(const GemmArgs& a, int max_tiles, int n_rowsets, hipStr
 constexpr int kGemvGroupsPerWave = 2;
 
 template <int WF, int PHASE, int RT>
-hipError_t launch_gemv_rt(const GemmArgs& a, int max_tiles, hipStream_t stream) {
+hipError_t launch_gemv_rt(const GemmArgs& a, int max_tiles, hipStream_t stream, const KernelTimer* tm) {
   const int out_dim = (PHASE == PHASE_GATE_UP) ? a.I : a.N;
   const int n_rowsets = out_dim / (RT * 16);
   const int G = a.K / 128;
   constexpr int NG = kGemvGroupsPerWave;
   const int need = (G + NG - 1) / NG;
-  if (need <= 1) return launch_gemv_s<WF, PHASE, RT, 1, NG>(a, max_tiles, n_rowsets, stream);
-  if (need <= 2) return launch_gemv_s<WF, PHASE, RT, 2, NG>(a, max_tiles, n_rowsets, stream);
-  if (need <= 3) return launch_gemv_s<WF, PHASE, RT, 3, NG>(a, max_tiles, n_rowsets, stream);
-  if (need <= 4) return launch_gemv_s<WF, PHASE, RT, 4, NG>(a, max_tiles, n_rowsets, stream);
-  if (need <= 6) return launch_gemv_s<WF, PHASE, RT, 6, NG>(a, max_tiles, n_rowsets, stream);
-  if (need <= 8) return launch_gemv_s<WF, PHASE, RT, 8, NG>(a, max_tiles, n_rowsets, stream);
-  if (need <= 16) return launch_gemv_s<WF, PHASE, RT, 8, 2 * NG>(a, max_tiles, n_rowsets, stream);
-  return launch_gemv_s<WF, PHASE, RT, 8, 0>(a, max_tiles, n_rowsets, stream);
+  if (need <= 1) return launch_gemv_s<WF, PHASE, RT, 1, NG>(a, max_tiles, n_rowsets, stream, tm);
+  if (need <= 2) return launch_gemv_s<WF, PHASE, RT, 2, NG>(a, max_tiles, n_rowsets, stream, tm);
+  if (need <= 3) return launch_gemv_s<WF, PHASE, RT, 3, NG>(a, max_tiles, n_rowsets, stream, tm);
+  if (need <= 4) return launch_gemv_s<WF, PHASE, RT, 4, NG>(a, max_tiles, n_rowsets, stream, tm);
+  if (need <= 6) return launch_gemv_s<WF, PHASE, RT, 6, NG>(a, max_tiles, n_rowsets, stream, tm);
+  if (need <= 8) return launch_gemv_s<WF, PHASE, RT, 8, NG>(a, max_tiles, n_rowsets, stream, tm);
+  if (need <= 16) return launch_gemv_s<WF, PHASE, RT, 8, 2 * NG>(a, max_tiles, n_rowsets, stream, tm);
+  return launch_gemv_s<WF, PHASE, RT, 8, 0>(a, max_tiles, n_rowsets, stream, tm);
 }
 
 template <int WF>
-hipError_t launch_gemv_wf(const GemmArgs& a, int phase, int max_tiles, hipStream_t stream) {
-  if (phase == PHASE_GATE_UP) return launch_gemv_rt<WF, PHASE_GATE_UP, kGemvRtGateUp>(a, max_tiles, stream);
-  return launch_gemv_rt<WF, PHASE_DOWN, kGemvRtDown>(a, max_tiles, stream);
+hipError_t launch_gemv_wf(const GemmArgs& a, int phase, int max_tiles, hipStream_t stream,
+                          const KernelTimer* tm) {
+  if (phase == PHASE_GATE_UP) return launch_gemv_rt<WF, PHASE_GATE_UP, kGemvRtGateUp>(a, max_tiles, stream, tm);
+  return launch_gemv_rt<WF, PHASE_DOWN, kGemvRtDown>(a, max_tiles, stream, tm);
 }
 
 }  // namespace
@@ -383,16 +385,17 @@ bool gemv_supported(int wf, int phase, int N, int K, int I) {
   return out_dim % rows_per_set == 0;
 }
 
-hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream) {
+hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream,
+                       const KernelTimer* tm) {
   if (max_tiles <= 0) return hipSuccess;
   if (a.perm && !a.tile_src) return hipErrorInvalidValue;  // gathered rows come from tile_src
   switch (wf) {
     case WF_BF16:
-      return launch_gemv_wf<WF_BF16>(a, phase, max_tiles, stream);
+      return launch_gemv_wf<WF_BF16>(a, phase, max_tiles, stream, tm);
     case WF_I8:
-      return launch_gemv_wf<WF_I8>(a, phase, max_tiles, stream);
+      return launch_gemv_wf<WF_I8>(a, phase, max_tiles, stream, tm);
     case WF_I4:
-      return launch_gemv_wf<WF_I4>(a, phase, max_tiles, stream);
+      return launch_gemv_wf<WF_I4>(a, phase, max_tiles, stream, tm);
     default:
       return hipErrorInvalidValue;
   }

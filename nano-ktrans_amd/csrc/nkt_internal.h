@@ -1,6 +1,7 @@
 // Launch wrappers shared between the kernel files and the C ABI.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -48,6 +49,21 @@ struct GemmArgs {
 
 enum GemmPhase : int { PHASE_GATE_UP = 0, PHASE_DOWN = 1 };
 
+// Optional pair of events stamped by the dispatch itself at a kernel's start
+// and end (hipExtLaunchKernelGGL): the kernel's own duration, no launch gap.
+struct KernelTimer {
+  hipEvent_t start, stop;
+};
+
+template <typename Kernel, typename... Args>
+inline void launch_timed(Kernel kernel, dim3 grid, dim3 block, uint32_t lds, hipStream_t stream,
+                         const KernelTimer* tm, Args... args) {
+  if (tm)
+    hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, tm->start, tm->stop, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+}
+
 // positions per tile of the prefill form of K3
 constexpr int kPrefillTileM = 64;
 // positions per tile of the decode form; K2 then also writes, per tile, the
@@ -80,15 +96,17 @@ int gemm_tile_m(int num_tokens, int topk, int num_experts, int wf, bool prefill_
 int gemm_rows_per_block(int wf, int phase, int bm);
 
 hipError_t launch_gemm(const GemmArgs& a, int wf, int phase, int bm, int grid_tiles,
-                       hipStream_t stream);
+                       hipStream_t stream, const KernelTimer* tm = nullptr);
 
 // Decode form of K3 (tiles of at most 16 positions, split-K in a workgroup).
 bool gemv_supported(int wf, int phase, int N, int K, int I);
-hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream);
+hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream,
+                       const KernelTimer* tm = nullptr);
 
 // Prefill form of K3 (tiles of 128 positions, bf16 / int8 / int4 weights).
 bool gemm2_supported(int wf, int phase, int N, int K, int I);
-hipError_t launch_gemm2(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream);
+hipError_t launch_gemm2(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream,
+                        const KernelTimer* tm = nullptr);
 // fp32 sums of every 128-wide K group of the rows of a bf16 matrix [rows, K]
 hipError_t launch_group_sums(const void* x, int rows, int K, float* out, hipStream_t stream);
 

@@ -62,6 +62,7 @@ EXPORTED_SYMBOLS = (
     "nkt_moe_route",
     "nkt_moe_experts",
     "nkt_moe_experts_phase",
+    "nkt_moe_experts_phase_timed",
     "nkt_moe_shared",
     "nkt_moe_combine",
     "nkt_moe_forward",
@@ -108,6 +109,8 @@ def lib() -> ctypes.CDLL:
     L.nkt_moe_experts.restype = i
     L.nkt_moe_experts_phase.argtypes = [vp, i, vp, i, vp, sz, vp, cp, sz]
     L.nkt_moe_experts_phase.restype = i
+    L.nkt_moe_experts_phase_timed.argtypes = [vp, i, vp, i, vp, sz, vp, vp, vp, cp, sz]
+    L.nkt_moe_experts_phase_timed.restype = i
     L.nkt_moe_shared.argtypes = [vp, vp, i, vp, sz, vp, cp, sz]
     L.nkt_moe_shared.restype = i
     L.nkt_moe_combine.argtypes = [vp, i, vp, vp, sz, vp, cp, sz]

@@ -249,6 +249,20 @@ class NativeMoE:
                                                           ws.numel(), self._stream(), self.err.buf,
                                                           self.err.size), "nkt_moe_experts_phase")
 
+    def expert_phase_timed(self, phase: int, hidden_states: Optional[torch.Tensor], num_tokens: int,
+                           start: "torch.cuda.Event", stop: "torch.cuda.Event") -> None:
+        """``expert_phase`` with its expert-GEMM kernel stamped by ``start``/``stop``
+        (events created with enable_timing=True) at the kernel's own start and end."""
+        xp = None
+        if phase == 0:
+            xp = self._check_input(hidden_states, self.hidden_size, "hidden_states").data_ptr()
+        ws = self.workspace(num_tokens)
+        with torch.cuda.device(self.device):
+            self.err.check(self.lib.nkt_moe_experts_phase_timed(
+                self.handle, phase, xp, num_tokens, ws.data_ptr(), ws.numel(), self._stream(),
+                ctypes.c_void_p(start.cuda_event), ctypes.c_void_p(stop.cuda_event),
+                self.err.buf, self.err.size), "nkt_moe_experts_phase_timed")
+
     def shared(self, hidden_states: torch.Tensor):
         """K4 + K3 on the shared expert: returns (gate fp32 [T], y_shared fp32 [T, H])."""
         x = self._check_input(hidden_states, self.hidden_size, "hidden_states")

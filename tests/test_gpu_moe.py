@@ -155,3 +155,27 @@ def test_stages_match_forward(gpu_device):
     # K4 alone: sigmoid(x . g)
     ref_gate = torch.sigmoid(x.float().cpu() @ layer.shared_gate.cpu())
     assert torch.allclose(gate.cpu(), ref_gate, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("name,T", [("qwen3_int4", 16), ("qwen3_int8", 512)])
+def test_timed_phases_match_untimed(gpu_device, name, T):
+    """The measurement entry point runs the same kernels: bitwise-equal h and y, and
+    its dispatch-stamped events give a positive duration."""
+    announce(f"timed phases {name} T={T}")
+    layer, native = _layer(name, E=32)
+    x, logits = build_inputs(layer, T, seed=11, device="cuda")
+    native.route(logits)
+    h0, y0 = (t.clone() for t in native.experts(x))
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    for e in ev:
+        e.record()
+    native.expert_phase_timed(0, x, T, ev[0], ev[1])
+    native.expert_phase_timed(1, None, T, ev[2], ev[3])
+    torch.cuda.synchronize()
+    P = T * layer.cfg.k
+    from nano_ktrans_amd import _native as N
+    h1 = native.region(T, N.WS_H, torch.bfloat16, (P, layer.cfg.I))
+    y1 = native.region(T, N.WS_Y, torch.float32, (P, layer.cfg.H))
+    assert torch.equal(h0, h1)
+    assert torch.equal(y0, y1)
+    assert ev[0].elapsed_time(ev[1]) > 0 and ev[2].elapsed_time(ev[3]) > 0
