@@ -222,7 +222,8 @@ def time_kernel(layers, xs, ls, phase, passes=5):
 
 def kernel_form(w, T):
     """Which K3 kernel the library runs for this shape (mirrors gemm_tile_m)."""
-    if T * w.k <= 12 * w.E:
+    avg = T * w.k / w.E
+    if avg <= 12:
         return "gemv_kernel"
     return "gemm2_kernel" if w.wfmt != "f32" else "gemm_kernel"
 

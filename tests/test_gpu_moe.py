@@ -81,6 +81,18 @@ def test_qwen3_int8_cut_experts(gpu_device, T):
     _check(layer, native, T)
 
 
+@pytest.mark.parametrize("T", [16, 100, 256])
+def test_qwen3_shape_bf16_weights(gpu_device, T):
+    """Dense bf16 experts at the Qwen3 shape (E cut to 16): T=16 decode form,
+    T=100 the 64-position prefill form, T=256 the 128-position form."""
+    announce(f"forward qwen3 shape bf16 weights E=16 T={T}")
+    from dataclasses import replace
+    cfg = replace(CONFIGS["qwen3_int4"], name="qwen3_bf16", wfmt="bf16")
+    _LAYERS.clear()
+    layer = build_layer(cfg, device="cuda", num_experts=16)
+    _check(layer, native_layer(layer, torch.device("cuda")), T)
+
+
 def test_qwen3_int8_full_prefill(gpu_device):
     announce("forward qwen3_int8 full T=2048")
     layer, native = _layer("qwen3_int8")
