@@ -147,6 +147,36 @@ def time_graph(layers, xs, ls, outs, steps, warmup):
     return ms / (reps * L), reps * L
 
 
+def time_graph_hidden(layers, xs, outs, steps, warmup):
+    """time_graph for the layer from hidden states alone (router GEMV fused):
+    ms per layer step."""
+    import torch
+
+    L = len(layers)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i, layer in enumerate(layers):
+            layer.forward_hidden(xs[i % len(xs)], out=outs[i])
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i, layer in enumerate(layers):
+            layer.forward_hidden(xs[i % len(xs)], out=outs[i])
+    for _ in range(max(1, (warmup + L - 1) // L)):
+        graph.replay()
+    torch.cuda.synchronize()
+    reps = max(1, (steps + L - 1) // L)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        graph.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / (reps * L)
+
+
 def time_stages(layers, xs, ls, outs, rounds):
     """Per-stage device time with HIP events; a sleep kernel keeps the host ahead."""
     import torch
@@ -499,6 +529,19 @@ def main():
             r["roofline"] = roofline_for(r, "hbm")
             log(json.dumps(r))
             secondary.append(r)
+    if not args.no_secondary:
+        # the layer from hidden states: router GEMV [E, H] fused into the routing launch
+        gate = router.to(torch.bfloat16)
+        for layer in layers:
+            layer.load_router(gate)
+        T = args.tokens
+        xs, _ = make_inputs(head, router, T, 8, dev)
+        outs = [torch.empty(T, head.H, dtype=torch.bfloat16, device=dev) for _ in layers]
+        ms = time_graph_hidden(layers, xs, outs, args.steps, args.warmup)
+        r = dict(workload=head.name + "_fused_router", tokens=T, us_per_layer=ms * 1e3,
+                 tokens_per_s=T / (ms * 1e-3))
+        log(json.dumps(r))
+        secondary.append(r)
     del layers
     torch.cuda.empty_cache()
     if not args.no_secondary:

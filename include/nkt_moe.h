@@ -64,7 +64,8 @@ extern "C" {
 #define NKT_SLOT_SHARED_DOWN 6
 #define NKT_SLOT_SHARED_DOWN_SCALES 7
 #define NKT_SLOT_SHARED_GATE 8 /* shared_expert_gate.weight [1, H], act dtype */
-#define NKT_NUM_SLOTS 9
+#define NKT_SLOT_ROUTER 9      /* router gate weight [E, H] (bf16 act only), packed */
+#define NKT_NUM_SLOTS 10
 
 /* workspace regions for nkt_moe_workspace_region */
 #define NKT_WS_TOPK_IDS 0     /* int32 [T, k]            */
@@ -78,7 +79,8 @@ extern "C" {
 #define NKT_WS_SHARED_GATE 8  /* fp32 [T] sigmoid(x . g)                              */
 #define NKT_WS_SHARED_H 9     /* act dtype [T, I_s]                                    */
 #define NKT_WS_SHARED_Y 10    /* fp32 [T, H]                                           */
-#define NKT_WS_NUM_REGIONS 11
+#define NKT_WS_ROUTER_LOGITS 11 /* bf16 [T, E] router logits of the *_hidden entry points */
+#define NKT_WS_NUM_REGIONS 12
 
 /* Create a handle for one layer shape.
  * Replaces the construction of HybridMoE's expert state
@@ -98,8 +100,10 @@ int nkt_moe_weight_bytes(void* handle, int slot, size_t* bytes, char* err, size_
  * layout inside dst (a buffer of nkt_moe_weight_bytes(slot) bytes; dst_scales
  * likewise for the matching *_SCALES slot, NULL for dense formats).
  * slot: NKT_SLOT_GATE_UP / NKT_SLOT_DOWN (expert in [0, E)) or
- * NKT_SLOT_SHARED_GATE_UP / NKT_SLOT_SHARED_DOWN (expert 0).  Replaces the
- * per-expert weight load of nano_ktrans/layers/expert_mlp.py:56-85 and
+ * NKT_SLOT_SHARED_GATE_UP / NKT_SLOT_SHARED_DOWN (expert 0), or
+ * NKT_SLOT_ROUTER (expert 0; src = the gate weight [E, H] in bf16, rows
+ * padded to a multiple of 32 with zeros).  Replaces the per-expert weight
+ * load of nano_ktrans/layers/expert_mlp.py:56-85 and
  * nano_ktrans/kernels/weight_loader.py:278-325, 355-392. */
 int nkt_moe_pack_weight(void* handle, int slot, int expert, const void* src, const void* src_scales,
                         void* dst, void* dst_scales, void* stream, char* err, size_t err_len);
@@ -163,6 +167,22 @@ int nkt_moe_combine(void* handle, int num_tokens, void* out, void* workspace,
 int nkt_moe_forward(void* handle, const void* hidden_states, const void* router_logits,
                     int num_tokens, void* out, void* workspace, size_t workspace_bytes,
                     void* stream, char* err, size_t err_len);
+
+/* Router GEMV + K1 + K2: router_logits = hidden_states . gate^T (fp32
+ * accumulation, rounded to bf16 as nn.Linear(H, E, bias=False) does in bf16),
+ * written to NKT_WS_ROUTER_LOGITS, then routed as by nkt_moe_route.  Fuses the
+ * decoder layer's gate (nano_ktrans/models/mixtral.py:127, 212) into the
+ * expert path; needs bf16 activations and a packed NKT_SLOT_ROUTER. */
+int nkt_moe_route_hidden(void* handle, const void* hidden_states, int num_tokens, void* workspace,
+                         size_t workspace_bytes, void* stream, char* err, size_t err_len);
+
+/* The whole layer from hidden states alone: nkt_moe_route_hidden, then the
+ * experts, shared expert and combine of nkt_moe_forward.  Replaces
+ * router_logits = self.gate(x); HybridMoE.forward(x, router_logits)
+ * (nano_ktrans/models/mixtral.py:212-218). */
+int nkt_moe_forward_hidden(void* handle, const void* hidden_states, int num_tokens, void* out,
+                           void* workspace, size_t workspace_bytes, void* stream, char* err,
+                           size_t err_len);
 
 /* Library version string (static storage). */
 const char* nkt_moe_version(void);

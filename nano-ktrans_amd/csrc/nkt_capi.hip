@@ -80,8 +80,12 @@ int64_t scale_elems(const Handle* h, int N, int K) {
   return 0;
 }
 
+// router gate rows, padded for the decode GEMM's 32-row sets
+int router_rows(const Handle* h) { return (h->E + 31) / 32 * 32; }
+
 size_t slot_bytes(const Handle* h, int slot) {
   if (slot == NKT_SLOT_SHARED_GATE) return h->Is > 0 ? (size_t)h->H * (h->act_bf16 ? 2 : 4) : 0;
+  if (slot == NKT_SLOT_ROUTER) return h->act_bf16 ? (size_t)router_rows(h) * h->H * 2 : 0;
   int N, K, ne;
   if (!slot_shape(h, slot, &N, &K, &ne)) return 0;
   if (is_scale_slot(slot)) return (size_t)ne * scale_elems(h, N, K) * 2;
@@ -124,6 +128,7 @@ WsLayout ws_layout(const Handle* h, int T) {
   sz[NKT_WS_SHARED_GATE] = h->Is > 0 ? (size_t)T * 4 : 0;
   sz[NKT_WS_SHARED_H] = h->Is > 0 ? (size_t)T * h->Is * es : 0;
   sz[NKT_WS_SHARED_Y] = h->Is > 0 ? (size_t)T * h->H * 4 : 0;
+  sz[NKT_WS_ROUTER_LOGITS] = h->act_bf16 ? (size_t)T * h->E * 2 : 0;
   sz[kWsTiles] = (size_t)L.max_tiles * 16;
   sz[kWsNTiles] = 4;
   sz[kWsXsum] = (size_t)T * (h->H / 128) * 4;
@@ -264,6 +269,42 @@ int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, 
                  "group kernels", err, len))
     return NKT_ERR;
   return NKT_OK;
+}
+
+// Router GEMV (decode-form GEMM over dense 16-token tiles, bf16 gate rows)
+// into the bf16 logits region, then K1 + K2 on those logits.
+int do_route_hidden(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipStream_t st, char* err,
+                    size_t len) {
+  if (!x) {
+    set_err(err, len, "null hidden_states");
+    return NKT_ERR;
+  }
+  if (!h->act_bf16) {
+    set_err(err, len, "the fused router needs bf16 activations");
+    return NKT_ERR;
+  }
+  if (!h->w[NKT_SLOT_ROUTER]) {
+    set_err(err, len, "router weight not bound (NKT_SLOT_ROUTER)");
+    return NKT_ERR;
+  }
+  const int Ep = router_rows(h);
+  if (!gemv_supported(WF_BF16, PHASE_DOWN, Ep, h->H, 0)) {
+    set_err(err, len, "hidden size %d unsupported by the router GEMM", h->H);
+    return NKT_ERR;
+  }
+  GemmArgs r;
+  memset(&r, 0, sizeof(r));
+  r.w = (const uint8_t*)h->w[NKT_SLOT_ROUTER];
+  r.N = Ep;
+  r.K = h->H;
+  r.in = x;
+  r.topk = 1;
+  r.out = ws_ptr<void>(ws, L, NKT_WS_ROUTER_LOGITS);
+  r.num_rows = T;
+  r.act_bf16 = 1;
+  r.out_cols = h->E;
+  if (!check_hip(launch_gemv(r, WF_BF16, PHASE_DOWN, (T + 15) / 16, st), "router gemm", err, len)) return NKT_ERR;
+  return do_route(h, ws_ptr<void>(ws, L, NKT_WS_ROUTER_LOGITS), T, ws, L, st, err, len);
 }
 
 // K3 launch for one projection: the decode form for tiles of at most 16
@@ -446,6 +487,21 @@ int nkt_moe_pack_weight(void* handle, int slot, int expert, const void* src, con
     set_err(err, err_len, "null handle");
     return NKT_ERR;
   }
+  if (slot == NKT_SLOT_ROUTER) {
+    if (!h->act_bf16) {
+      set_err(err, err_len, "the fused router needs bf16 activations");
+      return NKT_ERR;
+    }
+    if (expert != 0 || !src || !dst) {
+      set_err(err, err_len, "router: expert must be 0 and src/dst non-null");
+      return NKT_ERR;
+    }
+    if (!check_hip(launch_pack(WF_BF16, src, nullptr, router_rows(h), h->H, (uint8_t*)dst, nullptr,
+                               (hipStream_t)stream, h->E),
+                   "router pack kernel", err, err_len))
+      return NKT_ERR;
+    return NKT_OK;
+  }
   if (slot != NKT_SLOT_GATE_UP && slot != NKT_SLOT_DOWN && slot != NKT_SLOT_SHARED_GATE_UP &&
       slot != NKT_SLOT_SHARED_DOWN) {
     set_err(err, err_len, "slot %d is not a packable projection", slot);
@@ -591,6 +647,29 @@ int nkt_moe_forward(void* handle, const void* hidden_states, const void* router_
   return do_combine(h, num_tokens, out, workspace, L, st, err, err_len);
 }
 
-const char* nkt_moe_version(void) { return "nkt_moe 0.1.0 gfx950"; }
+int nkt_moe_route_hidden(void* handle, const void* hidden_states, int num_tokens, void* workspace,
+                         size_t workspace_bytes, void* stream, char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!check_call(h, num_tokens, workspace, workspace_bytes, err, err_len)) return NKT_ERR;
+  if (num_tokens == 0) return NKT_OK;
+  const WsLayout L = ws_layout(h, num_tokens);
+  return do_route_hidden(h, hidden_states, num_tokens, workspace, L, (hipStream_t)stream, err, err_len);
+}
+
+int nkt_moe_forward_hidden(void* handle, const void* hidden_states, int num_tokens, void* out, void* workspace,
+                           size_t workspace_bytes, void* stream, char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!check_call(h, num_tokens, workspace, workspace_bytes, err, err_len)) return NKT_ERR;
+  if (num_tokens == 0) return NKT_OK;
+  const WsLayout L = ws_layout(h, num_tokens);
+  hipStream_t st = (hipStream_t)stream;
+  if (do_route_hidden(h, hidden_states, num_tokens, workspace, L, st, err, err_len) != NKT_OK) return NKT_ERR;
+  if (do_experts(h, hidden_states, num_tokens, workspace, L, st, err, err_len) != NKT_OK) return NKT_ERR;
+  if (h->Is > 0 && do_shared(h, hidden_states, num_tokens, workspace, L, st, err, err_len) != NKT_OK)
+    return NKT_ERR;
+  return do_combine(h, num_tokens, out, workspace, L, st, err, err_len);
+}
+
+const char* nkt_moe_version(void) { return "nkt_moe 0.2.0 gfx950"; }
 
 }  // extern "C"

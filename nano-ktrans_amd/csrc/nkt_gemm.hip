@@ -421,7 +421,7 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int phase, int bm, int grid_ti
 template <int WF>
 __global__ void __launch_bounds__(256) pack_kernel(const void* __restrict__ src,
                                                    const uint16_t* __restrict__ src_scales, int N,
-                                                   int K, uint8_t* __restrict__ dst,
+                                                   int K, int n_valid, uint8_t* __restrict__ dst,
                                                    uint16_t* __restrict__ dst_scales) {
   const int KB = block_k(WF);
   const int NKB = K / KB;
@@ -457,9 +457,10 @@ __global__ void __launch_bounds__(256) pack_kernel(const void* __restrict__ src,
         out[2 * st + 1] = (uint32_t)p[4] | ((uint32_t)p[5] << 8) | ((uint32_t)p[6] << 16) | ((uint32_t)p[7] << 24);
       }
     } else if (WF == WF_BF16) {
-      const uint16_t* s = (const uint16_t*)src + (int64_t)row * K + kb * 32 + 8 * kq;
+      const uint16_t* s = (const uint16_t*)src + (int64_t)(row < n_valid ? row : 0) * K + kb * 32 + 8 * kq;
 #pragma unroll
-      for (int h = 0; h < 4; ++h) out[h] = (uint32_t)s[2 * h] | ((uint32_t)s[2 * h + 1] << 16);
+      for (int h = 0; h < 4; ++h)
+        out[h] = row < n_valid ? (uint32_t)s[2 * h] | ((uint32_t)s[2 * h + 1] << 16) : 0u;
     } else {
       const float* s = (const float*)src + (int64_t)row * K + kb * 16 + kq;
 #pragma unroll
@@ -482,7 +483,9 @@ __global__ void __launch_bounds__(256) pack_kernel(const void* __restrict__ src,
 }
 
 hipError_t launch_pack(int wf, const void* src, const void* src_scales, int N, int K, uint8_t* dst,
-                       uint16_t* dst_scales, hipStream_t stream) {
+                       uint16_t* dst_scales, hipStream_t stream, int n_valid) {
+  if (n_valid < 0) n_valid = N;
+  if (n_valid != N && wf != WF_BF16) return hipErrorInvalidValue;  // row padding: bf16 only
   const int64_t nthreads = (int64_t)(N / 16) * (K / block_k(wf)) * 64;
   const int64_t nscale = (wf == WF_I4) ? (int64_t)N * (K / 128) : N;
   const int64_t total = nthreads > nscale ? nthreads : nscale;
@@ -490,19 +493,19 @@ hipError_t launch_pack(int wf, const void* src, const void* src_scales, int N, i
   switch (wf) {
     case WF_F32:
       hipLaunchKernelGGL(pack_kernel<WF_F32>, grid, block, 0, stream, src,
-                         (const uint16_t*)src_scales, N, K, dst, dst_scales);
+                         (const uint16_t*)src_scales, N, K, n_valid, dst, dst_scales);
       break;
     case WF_BF16:
       hipLaunchKernelGGL(pack_kernel<WF_BF16>, grid, block, 0, stream, src,
-                         (const uint16_t*)src_scales, N, K, dst, dst_scales);
+                         (const uint16_t*)src_scales, N, K, n_valid, dst, dst_scales);
       break;
     case WF_I8:
       hipLaunchKernelGGL(pack_kernel<WF_I8>, grid, block, 0, stream, src,
-                         (const uint16_t*)src_scales, N, K, dst, dst_scales);
+                         (const uint16_t*)src_scales, N, K, n_valid, dst, dst_scales);
       break;
     case WF_I4:
       hipLaunchKernelGGL(pack_kernel<WF_I4>, grid, block, 0, stream, src,
-                         (const uint16_t*)src_scales, N, K, dst, dst_scales);
+                         (const uint16_t*)src_scales, N, K, n_valid, dst, dst_scales);
       break;
     default:
       return hipErrorInvalidValue;

@@ -326,7 +326,15 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
       *(u32x2*)((uint16_t*)a.out + pos * a.I + orow) = pk;
     } else {
       if (WF == WF_I8) s0 *= bf16x4_to_f32(*(const u32x2*)(sexp + orow));
-      *(f32x4*)((float*)a.out + pos * a.N + orow) = s0;
+      if (a.out_cols > 0) {
+        // bf16 [rows, out_cols] (router logits): columns past out_cols are padding
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (orow + v < a.out_cols)
+            ((uint16_t*)a.out)[pos * a.out_cols + orow + v] = (uint16_t)f32_to_bf16_bits(s0[v]);
+      } else {
+        *(f32x4*)((float*)a.out + pos * a.N + orow) = s0;
+      }
     }
   }
 }

@@ -45,6 +45,7 @@ struct GemmArgs {
   const float* xsum;       // prefill, int formats: group sums of the input rows [rows, K/128]
   float* hsum;             // prefill gate_up: group sums of the stored h [positions, I/128]
   const int32_t* tile_src; // decode gate_up: [max_tiles][kTileSrcCols] input row of each tile column
+  int out_cols;            // decode down, > 0: store bf16 [rows, out_cols] (columns < out_cols)
 };
 
 enum GemmPhase : int { PHASE_GATE_UP = 0, PHASE_DOWN = 1 };
@@ -110,8 +111,10 @@ hipError_t launch_gemm2(const GemmArgs& a, int wf, int phase, int max_tiles, hip
 // fp32 sums of every 128-wide K group of the rows of a bf16 matrix [rows, K]
 hipError_t launch_group_sums(const void* x, int rows, int K, float* out, hipStream_t stream);
 
+// Repack [N, K] into the block layout; rows >= n_valid (bf16 only) are zero
+// and not read (n_valid < 0: all N rows).
 hipError_t launch_pack(int wf, const void* src, const void* src_scales, int N, int K,
-                       uint8_t* dst, uint16_t* dst_scales, hipStream_t stream);
+                       uint8_t* dst, uint16_t* dst_scales, hipStream_t stream, int n_valid = -1);
 
 hipError_t launch_shared_gate(const void* x, const void* gate_w, int act_bf16, int T, int H,
                               float* gate_out, hipStream_t stream);

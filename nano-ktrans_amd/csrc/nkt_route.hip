@@ -98,15 +98,20 @@ __device__ __forceinline__ void route_token(const void* __restrict__ logits, int
   uint32_t key[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) key[j] = valid[j] ? ordered_bits(v[j]) : 0u;  // valid keys > 0
+  // a bf16 value fixes the low 16 key bits (0 for values >= 0, ones below):
+  // only the high 16 need rounds
+  const int low_bit = BF16 ? 16 : 0;
   uint32_t tau = 0;
 #pragma unroll 4
-  for (int b = 31; b >= 0; --b) {
+  for (int b = 31; b >= low_bit; --b) {
     const uint32_t cand = tau | (1u << b);
     int cnt = 0;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) cnt += __popcll(ballot64(key[j] >= cand));
     tau = (cnt >= k) ? cand : tau;
   }
+  // the skipped low bits of a bf16 key: 0 for values >= 0, all ones below 0
+  if (BF16 && !(tau & 0x80000000u)) tau |= 0xffffu;
   int above = 0;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) above += __popcll(ballot64(key[j] > tau));

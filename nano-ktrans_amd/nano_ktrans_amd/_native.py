@@ -37,7 +37,8 @@ SLOT_SHARED_GATE_UP_SCALES = 5
 SLOT_SHARED_DOWN = 6
 SLOT_SHARED_DOWN_SCALES = 7
 SLOT_SHARED_GATE = 8
-NUM_SLOTS = 9
+SLOT_ROUTER = 9
+NUM_SLOTS = 10
 
 WS_TOPK_IDS = 0
 WS_TOPK_WEIGHTS = 1
@@ -50,6 +51,7 @@ WS_Y = 7
 WS_SHARED_GATE = 8
 WS_SHARED_H = 9
 WS_SHARED_Y = 10
+WS_ROUTER_LOGITS = 11
 
 EXPORTED_SYMBOLS = (
     "nkt_moe_create",
@@ -66,6 +68,8 @@ EXPORTED_SYMBOLS = (
     "nkt_moe_shared",
     "nkt_moe_combine",
     "nkt_moe_forward",
+    "nkt_moe_route_hidden",
+    "nkt_moe_forward_hidden",
     "nkt_moe_version",
 )
 
@@ -117,6 +121,10 @@ def lib() -> ctypes.CDLL:
     L.nkt_moe_combine.restype = i
     L.nkt_moe_forward.argtypes = [vp, vp, vp, i, vp, vp, sz, vp, cp, sz]
     L.nkt_moe_forward.restype = i
+    L.nkt_moe_route_hidden.argtypes = [vp, vp, i, vp, sz, vp, cp, sz]
+    L.nkt_moe_route_hidden.restype = i
+    L.nkt_moe_forward_hidden.argtypes = [vp, vp, i, vp, vp, sz, vp, cp, sz]
+    L.nkt_moe_forward_hidden.restype = i
     L.nkt_moe_version.argtypes = []
     L.nkt_moe_version.restype = ctypes.c_char_p
     _lib = L

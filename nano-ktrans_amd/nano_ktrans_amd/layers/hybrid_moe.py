@@ -90,6 +90,7 @@ class HybridMoE(nn.Module):
         quantized_experts: Optional[Dict[int, Dict[str, GPTQLinearWeight]]] = None,
         shared_expert: Optional[nn.Module] = None,
         shared_expert_gate: Optional[nn.Module] = None,
+        gate: Optional[nn.Module] = None,
         max_tokens: int = 65536,
     ):
         super().__init__()
@@ -121,6 +122,10 @@ class HybridMoE(nn.Module):
         self.quantized_experts = quantized_experts or {}
         self.shared_expert = shared_expert
         self.shared_expert_gate = shared_expert_gate
+        # optional router nn.Linear(H, E, bias=False) (the decoder layer's self.gate,
+        # nano_ktrans/models/mixtral.py:127): with it, forward(x) without
+        # router_logits runs the router GEMV fused into the routing launch
+        self.gate = gate
         self.max_tokens = max_tokens
         self.offload_backend = None  # every expert is HBM-resident
         self._native: Optional[NativeMoE] = None
@@ -179,6 +184,8 @@ class HybridMoE(nn.Module):
             if shared_src is not None:
                 native.load_shared_expert(shared_src["gate"], shared_src["up"], shared_src["down"],
                                           self.shared_expert_gate.weight.detach())
+            if self.gate is not None and act_dtype == torch.bfloat16:
+                native.load_router(self.gate.weight.detach())
         self._native = native
 
     def reload_weights(self) -> None:
@@ -200,13 +207,22 @@ class HybridMoE(nn.Module):
         ids, w, *_ = native.route(router_logits.reshape(-1, self.num_experts))
         return w.to(router_logits.dtype), ids.to(torch.int64)
 
-    def forward(self, hidden_states: torch.Tensor, router_logits: torch.Tensor) -> torch.Tensor:
+    def forward(self, hidden_states: torch.Tensor, router_logits: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The reference forward (hidden_states, router_logits).  router_logits=None
+        (with gate= given at construction, bf16 activations) computes the logits
+        inside the expert path: the router GEMV fused with routing."""
         self.forward_calls += 1
         self.last_phase = "prefill" if get_context().is_prefill else "decode"
         native = self._ensure(hidden_states)
         shape = hidden_states.shape
-        out = native.forward(hidden_states.reshape(-1, self.hidden_size),
-                             router_logits.reshape(-1, self.num_experts))
+        x = hidden_states.reshape(-1, self.hidden_size)
+        if router_logits is None:
+            if self.gate is None:
+                raise ValueError("router_logits is required unless HybridMoE was built with gate=")
+            if hidden_states.dtype != torch.bfloat16:
+                raise ValueError("the fused router needs bf16 activations; pass router_logits")
+            return native.forward_hidden(x).view(shape)
+        out = native.forward(x, router_logits.reshape(-1, self.num_experts))
         return out.view(shape)
 
     def diagnostics(self) -> dict:

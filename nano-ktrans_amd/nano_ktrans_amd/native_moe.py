@@ -91,11 +91,11 @@ class NativeMoE:
         self.handle = ctypes.c_void_p(h)
         self.slots: Dict[int, torch.Tensor] = {}
         for slot in range(N.NUM_SLOTS):
-            nbytes = ctypes.c_size_t(0)
-            self.err.check(self.lib.nkt_moe_weight_bytes(self.handle, slot, ctypes.byref(nbytes),
-                                                         self.err.buf, self.err.size), "nkt_moe_weight_bytes")
-            if nbytes.value:
-                self.slots[slot] = torch.empty(nbytes.value, dtype=torch.uint8, device=self.device)
+            if slot == N.SLOT_ROUTER:
+                continue  # allocated and bound by load_router (the fused router is optional)
+            nbytes = self._slot_bytes(slot)
+            if nbytes:
+                self.slots[slot] = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         self._bind()
         self._ws: Optional[torch.Tensor] = None
 
@@ -108,6 +108,12 @@ class NativeMoE:
                 pass
 
     # ------------------------------------------------------------------ weights
+    def _slot_bytes(self, slot: int) -> int:
+        nbytes = ctypes.c_size_t(0)
+        self.err.check(self.lib.nkt_moe_weight_bytes(self.handle, slot, ctypes.byref(nbytes),
+                                                     self.err.buf, self.err.size), "nkt_moe_weight_bytes")
+        return nbytes.value
+
     def _bind(self) -> None:
         arr = (ctypes.c_void_p * N.NUM_SLOTS)()
         for slot in range(N.NUM_SLOTS):
@@ -173,6 +179,23 @@ class NativeMoE:
             raise ValueError(f"shared_expert_gate weight must have {H} elements")
         self.slots[N.SLOT_SHARED_GATE].view(self.act_dtype).copy_(g)
 
+    def load_router(self, gate_weight: torch.Tensor) -> None:
+        """Ingest the router gate weight [E, H] (nn.Linear(H, E, bias=False).weight) for
+        the fused router GEMV of ``route_hidden`` / ``forward_hidden`` (bf16 layers)."""
+        if self.act_dtype != torch.bfloat16:
+            raise ValueError("the fused router needs bf16 activations")
+        w = gate_weight.to(torch.bfloat16).to(self.device).contiguous()
+        if tuple(w.shape) != (self.num_experts, self.hidden_size):
+            raise ValueError(f"router weight must be [{self.num_experts}, {self.hidden_size}], got {tuple(w.shape)}")
+        if N.SLOT_ROUTER not in self.slots:
+            self.slots[N.SLOT_ROUTER] = torch.empty(self._slot_bytes(N.SLOT_ROUTER), dtype=torch.uint8,
+                                                    device=self.device)
+        with torch.cuda.device(self.device):
+            self.err.check(self.lib.nkt_moe_pack_weight(
+                self.handle, N.SLOT_ROUTER, 0, w.data_ptr(), None, self.slots[N.SLOT_ROUTER].data_ptr(), None,
+                self._stream(), self.err.buf, self.err.size), "nkt_moe_pack_weight(router)")
+        self._bind()
+
     # ---------------------------------------------------------------- workspace
     def workspace_bytes(self, num_tokens: int) -> int:
         nbytes = ctypes.c_size_t(0)
@@ -220,6 +243,25 @@ class NativeMoE:
                                                   self._stream(), self.err.buf, self.err.size), "nkt_moe_route")
         k, E = self.top_k, self.num_experts
         return (self.region(T, N.WS_TOPK_IDS, torch.int32, (T, k)),
+                self.region(T, N.WS_TOPK_WEIGHTS, torch.float32, (T, k)),
+                self.region(T, N.WS_COUNTS, torch.int32, (E,)),
+                self.region(T, N.WS_OFFSETS, torch.int32, (E + 1,)),
+                self.region(T, N.WS_PERM, torch.int32, (T * k,)),
+                self.region(T, N.WS_INV, torch.int32, (T * k,)))
+
+    def route_hidden(self, hidden_states: torch.Tensor):
+        """Router GEMV + K1 + K2 from hidden states (after ``load_router``).  Returns
+        (router_logits bf16 [T, E], ids, weights, counts, offsets, perm, inv) as views."""
+        x = self._check_input(hidden_states, self.hidden_size, "hidden_states")
+        T = x.shape[0]
+        ws = self.workspace(T)
+        with torch.cuda.device(self.device):
+            self.err.check(self.lib.nkt_moe_route_hidden(self.handle, x.data_ptr(), T, ws.data_ptr(), ws.numel(),
+                                                         self._stream(), self.err.buf, self.err.size),
+                           "nkt_moe_route_hidden")
+        k, E = self.top_k, self.num_experts
+        return (self.region(T, N.WS_ROUTER_LOGITS, torch.bfloat16, (T, E)),
+                self.region(T, N.WS_TOPK_IDS, torch.int32, (T, k)),
                 self.region(T, N.WS_TOPK_WEIGHTS, torch.float32, (T, k)),
                 self.region(T, N.WS_COUNTS, torch.int32, (E,)),
                 self.region(T, N.WS_OFFSETS, torch.int32, (E + 1,)),
@@ -283,6 +325,21 @@ class NativeMoE:
         with torch.cuda.device(self.device):
             self.err.check(self.lib.nkt_moe_combine(self.handle, T, out.data_ptr(), ws.data_ptr(), ws.numel(),
                                                     self._stream(), self.err.buf, self.err.size), "nkt_moe_combine")
+        return out
+
+    def forward_hidden(self, hidden_states: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The whole layer from hidden states (router GEMV fused; after ``load_router``)."""
+        x = self._check_input(hidden_states, self.hidden_size, "hidden_states")
+        T = x.shape[0]
+        if out is None:
+            out = torch.empty(T, self.hidden_size, dtype=self.act_dtype, device=self.device)
+        if T == 0:
+            return out
+        ws = self.workspace(T)
+        with torch.cuda.device(self.device):
+            self.err.check(self.lib.nkt_moe_forward_hidden(self.handle, x.data_ptr(), T, out.data_ptr(),
+                                                           ws.data_ptr(), ws.numel(), self._stream(),
+                                                           self.err.buf, self.err.size), "nkt_moe_forward_hidden")
         return out
 
     def forward(self, hidden_states: torch.Tensor, router_logits: torch.Tensor,

@@ -19,6 +19,9 @@ nano-ktrans tree):
 * ``matvec_grouped``          nano_ktrans/kernels/quantized_ops.py:86-124
 * ``expert_dense``            nano_ktrans/layers/expert_mlp.py:20-23, 37-41
 * ``expert_quant``            nano_ktrans/kernels/cpu_moe.py:419-450
+* ``router_logits``           nano_ktrans/models/mixtral.py:127, 212 (the gate
+                              nn.Linear(H, E, bias=False) in bf16: exact dot
+                              products rounded once to bf16)
 * ``route``                   nano_ktrans/layers/hybrid_moe.py:3321-3329 (C restatement)
 * ``group``                   nano_ktrans/layers/hybrid_moe.py:3512-3526,
                               nano_ktrans/kernels/cpu_moe.py:515-523 (C restatement)
@@ -114,6 +117,29 @@ def softmax_row(x: np.ndarray) -> np.ndarray:
     p = np.empty_like(x)
     lib().orc_softmax_row(_fptr(x), x.size, _fptr(p))
     return p
+
+
+def router_logits(x: np.ndarray, gate: np.ndarray) -> np.ndarray:
+    """router_logits = gate(x) for bf16 x [T, H] and gate weight [E, H]
+    (nano_ktrans/models/mixtral.py:127, 212, nn.Linear(H, E, bias=False) in
+    bf16): dot products accumulated in float64 (rounding errors far below
+    bf16 resolution), then rounded once to bf16 (ties to even); float32 out."""
+    acc = np.asarray(x, dtype=np.float64) @ np.asarray(gate, dtype=np.float64).T
+    return round64_to_bf16(acc)
+
+
+def round64_to_bf16(a: np.ndarray) -> np.ndarray:
+    """float64 -> nearest bf16 (ties to even) in a single rounding, as float32:
+    round to float32 with round-to-odd (truncate, set the last bit when
+    inexact), then to bf16 with ties-to-even -- float32 carries more than two
+    extra bits, so the two steps equal one correct rounding."""
+    a = np.asarray(a, dtype=np.float64)
+    f = a.astype(np.float32)
+    f64 = f.astype(np.float64)
+    exact = f64 == a
+    toward_zero = np.where(np.abs(f64) > np.abs(a), np.nextafter(f, np.float32(0)), f).astype(np.float32)
+    odd = (toward_zero.view(np.uint32) | np.uint32(1)).view(np.float32)
+    return bf16_round(np.where(exact, f, odd).astype(np.float32))
 
 
 def route(logits: np.ndarray, top_k: int, use_softmax: bool, renorm: bool, bf16: bool):

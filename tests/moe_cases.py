@@ -167,6 +167,30 @@ def bf16_ulp(x: np.ndarray) -> np.ndarray:
     return np.ldexp(1.0, ex - 8)
 
 
+def bf16_steps(a, b) -> np.ndarray:
+    """Elementwise distance in bf16 steps between two arrays of bf16 values (float32)."""
+    ia = (np.ascontiguousarray(a, np.float32).view(np.int32) >> 16).astype(np.int64)
+    ib = (np.ascontiguousarray(b, np.float32).view(np.int32) >> 16).astype(np.int64)
+    # sign-magnitude -> a monotone integer line (+0 and -0 both map to 0)
+    ia = np.where(ia < 0, -(ia & 0x7FFF), ia)
+    ib = np.where(ib < 0, -(ib & 0x7FFF), ib)
+    return np.abs(ia - ib)
+
+
+def check_router_logits(got: np.ndarray, x: np.ndarray, gate: np.ndarray) -> None:
+    """GPU bf16 logits against the oracle's single rounding of the exact dot
+    products: each within one bf16 step, or, where cancellation leaves a value
+    near zero, within fp32 summation error (2^-20 x sum |x_i w_i|, a bound far
+    above a 2048-term fp32 sum's typical error); nearly all bit-equal."""
+    ref = O.router_logits(x, gate)
+    steps = bf16_steps(got, ref)
+    absterm = np.abs(np.asarray(x, np.float64)) @ np.abs(np.asarray(gate, np.float64)).T
+    near = np.abs(np.asarray(got, np.float64) - ref) <= 2.0 ** -20 * absterm
+    bad = ~((steps <= 1) | near)
+    assert not bad.any(), f"{bad.sum()} logits off: got {got[bad][:4]} want {ref[bad][:4]}"
+    assert (steps == 0).mean() > 0.99
+
+
 def compare(got: np.ndarray, ref: np.ndarray, cfg: MoEConfig):
     """Check a GPU output against the oracle's fp32 result.
 

@@ -95,6 +95,38 @@ def test_qwen3_packed_modules_quantized_int4(gpu_device):
     _check(out, oracle_forward(layer, x, logits))
 
 
+def test_qwen3_fused_router_gate_module(gpu_device):
+    """HybridMoE(gate=nn.Linear): forward(x) without router_logits runs the router
+    GEMV inside the path and equals forward(x, gate(x)) computed by the library's
+    own logits; the logits match the oracle's gate(x)."""
+    from moe_cases import check_router_logits
+    from nano_ktrans_amd import _native as N
+    announce("HybridMoE qwen3 fused router gate module")
+    E, k, H, I, T = 16, 8, 2048, 768, 12
+    experts = nn.ModuleDict({str(e): _init(PackedSparseExpertMLP(H, I), 300 + e).to(gpu_device, torch.bfloat16)
+                             for e in range(E)})
+    gate = nn.Linear(H, E, bias=False)
+    with torch.no_grad():
+        gate.weight.copy_(torch.randn(E, H, generator=torch.Generator().manual_seed(9)) * 0.02)
+    gate = gate.to(gpu_device, torch.bfloat16)
+    moe = HybridMoE(E, k, H, I, experts, torch.ones(E, dtype=torch.bool), 0, "",
+                    router_use_softmax=True, normalize_topk_prob=True, experts_are_packed=True,
+                    expert_key_template=QWEN3_MOE_SPEC.expert_key_template,
+                    expert_proj_names=QWEN3_MOE_SPEC.expert_proj_names, quantization="int4_g128", gate=gate)
+    x, _ = _inputs(T, H, E, seed=3)
+    x = x.to(gpu_device)
+    out = moe(x).clone()
+    torch.cuda.synchronize()
+    logits = moe._native.region(T, N.WS_ROUTER_LOGITS, torch.bfloat16, (T, E)).clone()
+    check_router_logits(logits.float().cpu().numpy(), x.float().cpu().numpy(),
+                        gate.weight.detach().float().cpu().numpy())
+    assert torch.equal(out, moe(x, logits))
+    with pytest.raises(ValueError, match="router_logits is required"):
+        HybridMoE(E, k, H, I, experts, torch.ones(E, dtype=torch.bool), 0, "", router_use_softmax=True,
+                  experts_are_packed=True, expert_key_template=QWEN3_MOE_SPEC.expert_key_template,
+                  expert_proj_names=QWEN3_MOE_SPEC.expert_proj_names, quantization="int4_g128")(x)
+
+
 def test_safetensors_dense_and_gptq_checkpoints(gpu_device, tmp_path):
     from safetensors.torch import save_file
 

@@ -191,3 +191,29 @@ def test_timed_phases_match_untimed(gpu_device, name, T):
     assert torch.equal(h0, h1)
     assert torch.equal(y0, y1)
     assert ev[0].elapsed_time(ev[1]) > 0 and ev[2].elapsed_time(ev[3]) > 0
+
+
+@pytest.mark.parametrize("name,E,T", [("qwen3_int4", 32, 16), ("qwen3_int8", 32, 512), ("mixtral_int4", None, 1),
+                                      ("qwen15_int8_shared", None, 16)])
+def test_forward_hidden_fused_router(gpu_device, name, E, T):
+    """The layer from hidden states alone (router GEMV fused): logits checked
+    against the oracle's (check_router_logits), the output equal to the
+    oracle's forward on the GPU's logits within the bf16 tolerance, and to
+    nkt_moe_forward on them bit for bit."""
+    from nano_ktrans_amd import _native as N
+    from moe_cases import check_router_logits
+    announce(f"forward_hidden {name} E={E} T={T}")
+    layer, native = _layer(name, E=E)
+    gate = layer.router.to(torch.bfloat16)
+    native.load_router(gate)
+    x, _ = build_inputs(layer, T, seed=21, device="cuda")
+    out = native.forward_hidden(x).clone()
+    torch.cuda.synchronize()
+    g_logits = native.region(T, N.WS_ROUTER_LOGITS, torch.bfloat16, (T, layer.cfg.E)).clone()
+    check_router_logits(g_logits.float().cpu().numpy(), x.float().cpu().numpy(), gate.float().cpu().numpy())
+    ref = oracle_forward(layer, x, g_logits)
+    err_abs, err_rel = compare(out.float().cpu().numpy(), ref, layer.cfg)
+    announce(f"  {name} T={T}: max_abs={err_abs:.3e} rel_l2={err_rel:.3e}")
+    again = native.forward(x, g_logits)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again)

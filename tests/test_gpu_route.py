@@ -7,7 +7,7 @@ import pytest
 import torch
 
 import oracle as O
-from moe_cases import CONFIGS, build_inputs, build_layer
+from moe_cases import CONFIGS, build_inputs, build_layer, check_router_logits
 
 pytestmark = pytest.mark.gpu
 
@@ -17,13 +17,14 @@ def announce(msg):
     sys.__stderr__.flush()
 
 
-def _router_only(E, k, softmax, renorm, act_dtype, device, max_tokens=8192):
+def _router_only(E, k, softmax, renorm, act_dtype, device, max_tokens=8192, hidden=128):
     from nano_ktrans_amd.native_moe import NativeMoE
 
     wfmt = "f32" if act_dtype == torch.float32 else "bf16"
-    return NativeMoE(num_experts=E, top_k=k, hidden_size=128, intermediate_size=128, weight_format=wfmt,
+    return NativeMoE(num_experts=E, top_k=k, hidden_size=hidden, intermediate_size=128, weight_format=wfmt,
                      act_dtype=act_dtype, use_softmax=softmax, renorm=renorm, max_tokens=max_tokens,
                      device=device)
+
 
 
 def _check_route(native, logits, k, softmax, renorm, bf16):
@@ -103,3 +104,44 @@ def test_route_repeatable(gpu_device):
         again = native.route(logits)
         for a, b in zip(first, again):
             assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("name,T", [
+    ("qwen3_int4", 1), ("qwen3_int4", 16), ("qwen3_int4", 100), ("qwen3_int8", 1024),
+    ("mixtral_int4", 16), ("qwen15_int8_shared", 1), ("qwen15_int8_shared", 300),
+])
+def test_route_hidden_matches_oracle(gpu_device, name, T):
+    """Router GEMV fused with K1 + K2: bf16 logits against the oracle's single
+    rounding of the exact dot products (check_router_logits), and routing /
+    grouping of those logits bit-exact."""
+    cfg = CONFIGS[name]
+    announce(f"route_hidden {name} T={T}")
+    g = torch.Generator().manual_seed(cfg.seed + 50)
+    gate = (torch.randn(cfg.E, cfg.H, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(T, cfg.H, generator=g).to(torch.bfloat16)
+    native = _router_only(cfg.E, cfg.k, cfg.softmax, cfg.renorm, torch.bfloat16, gpu_device, hidden=cfg.H)
+    native.load_router(gate)
+    logits, ids, w, counts, offsets, perm, inv = native.route_hidden(x.to(gpu_device))
+    torch.cuda.synchronize()
+    g_logits = logits.float().cpu().numpy()
+    check_router_logits(g_logits, x.float().numpy(), gate.float().numpy())
+    oids, ow = O.route(g_logits, cfg.k, cfg.softmax, cfg.renorm, True)
+    ocounts, ooffsets, operm, oinv = O.group(oids, cfg.E)
+    assert np.array_equal(ids.cpu().numpy(), oids)
+    assert np.array_equal(w.cpu().numpy().view(np.uint32), ow.view(np.uint32))
+    assert np.array_equal(counts.cpu().numpy(), ocounts)
+    assert np.array_equal(offsets.cpu().numpy(), ooffsets)
+    assert np.array_equal(perm.cpu().numpy(), operm)
+    assert np.array_equal(inv.cpu().numpy(), oinv)
+
+
+def test_route_hidden_rejects_missing_router_and_fp32(gpu_device):
+    from nano_ktrans_amd._native import NativeError
+
+    native = _router_only(8, 2, True, True, torch.bfloat16, gpu_device, hidden=256)
+    x = torch.zeros(4, 256, dtype=torch.bfloat16, device=gpu_device)
+    with pytest.raises(NativeError, match="router weight not bound"):
+        native.route_hidden(x)
+    f32 = _router_only(8, 2, True, True, torch.float32, gpu_device, hidden=256)
+    with pytest.raises(ValueError, match="bf16 activations"):
+        f32.load_router(torch.zeros(8, 256))

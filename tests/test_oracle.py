@@ -52,6 +52,61 @@ def test_bf16_round_matches_torch():
     assert O.bf16_round(np.array([1.0 + 3 * 2.0 ** -8], np.float32))[0] == 1.0 + 2.0 ** -6
 
 
+# ---------------------------------------------------------------- router logits
+def _nearest_bf16_brute(a: float) -> float:
+    """Nearest bf16 to a float64 value by enumerating the bf16 neighbours."""
+    f = np.float32(a)
+    base = int(np.array([f], np.float32).view(np.uint32)[0]) & 0xFFFF0000
+    cands = []
+    for d in (-0x10000, 0, 0x10000):
+        b = (base + d) & 0xFFFFFFFF
+        cands.append((float(np.array([b], np.uint32).view(np.float32)[0]), b))
+    best = min(abs(c - a) for c, _ in cands)
+    ties = [(c, b) for c, b in cands if abs(c - a) == best]
+    if len(ties) == 1:
+        return ties[0][0]
+    return [c for c, b in ties if ((b >> 16) & 1) == 0][0]  # ties to even
+
+
+def test_round64_to_bf16_matches_brute_force():
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal(3000) * 10.0 ** rng.integers(-6, 6, 3000)
+    # exact halfway points and values a hair either side of them
+    mids = np.array([1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, -(2.0 + 2.0 ** -7), 96.0 + 0.25])
+    a = np.concatenate([a, mids, mids + 1e-12, mids - 1e-12])
+    ours = O.round64_to_bf16(a)
+    ref = np.array([_nearest_bf16_brute(v) for v in a], np.float32)
+    assert np.array_equal(ours.view(np.uint32), ref.view(np.uint32))
+
+
+def test_router_logits_one_hot_rows_pick_gate_columns():
+    rng = np.random.default_rng(4)
+    E, H = 12, 256
+    gate = O.bf16_round(rng.standard_normal((E, H)).astype(np.float32))
+    x = np.zeros((H, H), np.float32)
+    x[np.arange(H), np.arange(H)] = 1.0
+    assert np.array_equal(O.router_logits(x, gate), gate.T)
+    # scaling an input row by a power of two scales its logits exactly
+    x2 = O.bf16_round(rng.standard_normal((5, H)).astype(np.float32))
+    assert np.array_equal(O.router_logits(4.0 * x2, gate), 4.0 * O.router_logits(x2, gate))
+
+
+def test_router_logits_agree_with_torch_bf16_linear():
+    """torch's CPU bf16 nn.Linear (fp32 accumulation, one rounding) lands on the
+    same bf16 logit or one ulp away."""
+    g = torch.Generator().manual_seed(5)
+    E, H, T = 60, 2048, 64
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    w = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16)
+    ref = torch.nn.functional.linear(x, w).float().numpy()
+    ours = O.router_logits(x.float().numpy(), w.float().numpy())
+    # distance in bf16 steps (both are bf16 values; the sign never differs here)
+    assert np.array_equal(np.sign(ref), np.sign(ours))
+    ulp = np.abs((ref.view(np.int32) >> 16).astype(np.int64) - (ours.view(np.int32) >> 16).astype(np.int64))
+    assert ulp.max() <= 1
+    assert (ulp == 0).mean() > 0.98
+
+
 # ---------------------------------------------------------------- softmax
 @pytest.mark.parametrize("E", [8, 60, 64, 100, 128, 256])
 def test_softmax_row_close_to_float64(E):
