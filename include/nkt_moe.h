@@ -161,6 +161,21 @@ int nkt_moe_shared(void* handle, const void* hidden_states, int num_tokens, void
 int nkt_moe_combine(void* handle, int num_tokens, void* out, void* workspace,
                     size_t workspace_bytes, void* stream, char* err, size_t err_len);
 
+/* Mixed residency (nano_ktrans/layers/hybrid_moe.py:264-290, 3373-3378,
+ * 3563-3570: experts whose gpu_experts_mask entry is False run in an offload
+ * backend).  resident: device bytes [E], 0 = the expert's weights are not in
+ * HBM; NULL (the default) = every expert resident.  Later route / experts
+ * calls give non-resident experts no GEMM tiles (counts, offsets and the
+ * permutation still cover every pair), and the combine skips their slots. */
+int nkt_moe_bind_residency(void* handle, const void* resident, char* err, size_t err_len);
+
+/* nkt_moe_combine plus extra [T, H] (act dtype, NULL for none): the sum the
+ * offload backend's sync_forward returned for the non-resident experts
+ * (nano_ktrans/kernels/offload_backend.py:40-52), added after the resident
+ * experts and before the shared expert, in the same fp32 sum. */
+int nkt_moe_combine_extra(void* handle, int num_tokens, const void* extra, void* out, void* workspace,
+                          size_t workspace_bytes, void* stream, char* err, size_t err_len);
+
 /* The whole layer: route, experts, shared expert, combine.  Replaces
  * HybridMoE.forward (nano_ktrans/layers/hybrid_moe.py:3310-3570) plus the
  * shared-expert add of nano_ktrans/models/mixtral.py:215-218. */

@@ -18,6 +18,7 @@ struct Handle {
   unsigned flags;
   int max_tokens;
   const void* w[NKT_NUM_SLOTS];
+  const uint8_t* resident;  // [E] device bytes, 0 = expert not in HBM; nullptr = all resident
 };
 
 constexpr int kWsTiles = NKT_WS_NUM_REGIONS;       // int32 [max_tiles][4]
@@ -256,7 +257,8 @@ int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, 
   int32_t* tile_src = L.bm == kTileSrcCols ? ws_ptr<int32_t>(ws, L, kWsTileSrc) : nullptr;
   if (route_group_fused(T, h->k)) {
     if (!check_hip(launch_route_group(logits, h->act_bf16, T, h->E, h->k, h->flags, L.bm, L.max_tiles,
-                                      ids, wts, counts, offsets, perm, inv, tiles, n_tiles, tile_src, st),
+                                      ids, wts, counts, offsets, perm, inv, tiles, n_tiles, tile_src,
+                                      h->resident, st),
                    "route+group kernel", err, len))
       return NKT_ERR;
     return NKT_OK;
@@ -265,7 +267,7 @@ int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, 
                  "route kernel", err, len))
     return NKT_ERR;
   if (!check_hip(launch_group_multi(ids, T, h->k, h->E, L.bm, L.max_tiles, ws_ptr<int32_t>(ws, L, kWsHist), counts,
-                                    offsets, perm, inv, tiles, n_tiles, tile_src, st),
+                                    offsets, perm, inv, tiles, n_tiles, tile_src, h->resident, st),
                  "group kernels", err, len))
     return NKT_ERR;
   return NKT_OK;
@@ -377,7 +379,7 @@ int do_shared(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipS
 }
 
 int do_combine(Handle* h, int T, void* out, void* ws, const WsLayout& L, hipStream_t st, char* err,
-               size_t len) {
+               size_t len, const void* extra = nullptr) {
   if (!out) {
     set_err(err, len, "null output");
     return NKT_ERR;
@@ -387,8 +389,8 @@ int do_combine(Handle* h, int T, void* out, void* ws, const WsLayout& L, hipStre
                                 ws_ptr<float>(ws, L, NKT_WS_TOPK_WEIGHTS),
                                 ws_ptr<int32_t>(ws, L, NKT_WS_INV),
                                 sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_Y) : nullptr,
-                                sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE) : nullptr, T, h->k,
-                                h->H, out, h->act_bf16, st),
+                                sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE) : nullptr, h->resident,
+                                extra, T, h->k, h->H, out, h->act_bf16, st),
                  "combine kernel", err, len))
     return NKT_ERR;
   return NKT_OK;
@@ -630,6 +632,25 @@ int nkt_moe_combine(void* handle, int num_tokens, void* out, void* workspace, si
   if (num_tokens == 0) return NKT_OK;
   const WsLayout L = ws_layout(h, num_tokens);
   return do_combine(h, num_tokens, out, workspace, L, (hipStream_t)stream, err, err_len);
+}
+
+int nkt_moe_combine_extra(void* handle, int num_tokens, const void* extra, void* out, void* workspace,
+                          size_t workspace_bytes, void* stream, char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!check_call(h, num_tokens, workspace, workspace_bytes, err, err_len)) return NKT_ERR;
+  if (num_tokens == 0) return NKT_OK;
+  const WsLayout L = ws_layout(h, num_tokens);
+  return do_combine(h, num_tokens, out, workspace, L, (hipStream_t)stream, err, err_len, extra);
+}
+
+int nkt_moe_bind_residency(void* handle, const void* resident, char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!h) {
+    set_err(err, err_len, "null handle");
+    return NKT_ERR;
+  }
+  h->resident = (const uint8_t*)resident;
+  return NKT_OK;
 }
 
 int nkt_moe_forward(void* handle, const void* hidden_states, const void* router_logits,

@@ -3,8 +3,10 @@
 // K5: un-permute and weighted combine.  For every token the k expert outputs
 //     are added in ascending expert id (the visiting order of
 //     nano_ktrans/layers/hybrid_moe.py:3512-3533 and cpu_moe.py:515-536),
-//     in fp32, then the gated shared expert, then one rounding to the output
-//     dtype.  No atomics: each output element is owned by one thread.
+//     in fp32, then the sum an offload backend returned for the experts that
+//     are not HBM-resident (hybrid_moe.py:3563-3570; their slots are skipped),
+//     then the gated shared expert, then one rounding to the output dtype.
+//     No atomics: each output element is owned by one thread.
 #include "nkt_common.h"
 #include "nkt_internal.h"
 
@@ -36,17 +38,19 @@ template <int K>
 __global__ void __launch_bounds__(256) combine_kernel(
     const float* __restrict__ y, const int32_t* __restrict__ ids, const float* __restrict__ w,
     const int32_t* __restrict__ inv, const float* __restrict__ y_shared,
-    const float* __restrict__ shared_gate, int num_tokens, int H, void* __restrict__ out,
-    int out_bf16) {
+    const float* __restrict__ shared_gate, const uint8_t* __restrict__ resident,
+    const void* __restrict__ extra, int num_tokens, int H, void* __restrict__ out, int out_bf16) {
   const int t = blockIdx.x;
   const int c = blockIdx.y * blockDim.x + threadIdx.x;  // float4 column index
   // order the token's slots by expert id: rank[j] = #{i : id_i < id_j}
   // (ids of one token are distinct), then gather by rank with static indices
   int sid[K], spos[K], rank[K];
   float sw[K];
+  bool sres[K];
 #pragma unroll
   for (int j = 0; j < K; ++j) {
     sid[j] = ids[(int64_t)t * K + j];
+    sres[j] = resident ? resident[sid[j]] != 0 : true;
     // positions index y [T*K, H]; keep a corrupt entry from reading outside it
     spos[j] = min(max(inv[(int64_t)t * K + j], 0), num_tokens * K - 1);
     sw[j] = w[(int64_t)t * K + j];
@@ -60,19 +64,23 @@ __global__ void __launch_bounds__(256) combine_kernel(
   }
   int order_pos[K];
   float order_w[K];
+  bool order_res[K];
 #pragma unroll
   for (int r = 0; r < K; ++r) {
     int p = 0;
     float wt = 0.f;
+    bool rs = true;
 #pragma unroll
     for (int j = 0; j < K; ++j) {
       if (rank[j] == r) {
         p = spos[j];
         wt = sw[j];
+        rs = sres[j];
       }
     }
     order_pos[r] = p;
     order_w[r] = wt;
+    order_res[r] = rs;
   }
   if (4 * c >= H) return;
   // every load first, then the fixed-order sum
@@ -85,9 +93,20 @@ __global__ void __launch_bounds__(256) combine_kernel(
     vs = *(const f32x4*)(y_shared + (int64_t)t * H + 4 * c);
     sg = shared_gate[t];
   }
-  f32x4 acc = order_w[0] * v[0];
+  // slots of experts that are not resident have no y row this call: their
+  // (stale) values are selected away, never multiplied
+  const f32x4 zero = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 acc = order_res[0] ? order_w[0] * v[0] : zero;
 #pragma unroll
-  for (int j = 1; j < K; ++j) acc += order_w[j] * v[j];
+  for (int j = 1; j < K; ++j) acc += order_res[j] ? order_w[j] * v[j] : zero;
+  if (extra) {
+    if (out_bf16) {
+      const u32x2 e = *(const u32x2*)((const uint16_t*)extra + (int64_t)t * H + 4 * c);
+      acc += bf16x4_to_f32(e);
+    } else {
+      acc += *(const f32x4*)((const float*)extra + (int64_t)t * H + 4 * c);
+    }
+  }
   if (y_shared) acc += sg * vs;
   if (out_bf16) {
     u32x2 pk;
@@ -108,14 +127,15 @@ hipError_t launch_shared_gate(const void* x, const void* gate_w, int act_bf16, i
 }
 
 hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, const int32_t* inv,
-                          const float* y_shared, const float* shared_gate, int T, int k, int H,
-                          void* out, int out_bf16, hipStream_t stream) {
+                          const float* y_shared, const float* shared_gate, const uint8_t* resident,
+                          const void* extra, int T, int k, int H, void* out, int out_bf16,
+                          hipStream_t stream) {
   if (T <= 0) return hipSuccess;
   dim3 grid(T, (H / 4 + 255) / 256), block(256);
 #define NKT_COMBINE_CASE(KK)                                                                   \
   case KK:                                                                                     \
     hipLaunchKernelGGL(combine_kernel<KK>, grid, block, 0, stream, y, ids, w, inv, y_shared,   \
-                       shared_gate, T, H, out, out_bf16);                                      \
+                       shared_gate, resident, extra, T, H, out, out_bf16);                     \
     break;
   switch (k) {
     NKT_COMBINE_CASE(1)

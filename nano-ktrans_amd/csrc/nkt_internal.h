@@ -74,18 +74,21 @@ constexpr int kTileSrcCols = 16;
 hipError_t launch_route(const void* logits, int act_bf16, int T, int E, int k, unsigned flags,
                         int32_t* ids, float* w, hipStream_t stream);
 
-// K1 + K2 in one workgroup when route_group_fused(T, k).
+// K1 + K2 in one workgroup when route_group_fused(T, k).  resident (nullable,
+// [E] device bytes): experts with 0 are grouped but get no GEMM tiles.
 bool route_group_fused(int T, int k);
 hipError_t launch_route_group(const void* logits, int act_bf16, int T, int E, int k,
                               unsigned flags, int bm, int max_tiles, int32_t* ids, float* w,
                               int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
-                              int32_t* tiles, int32_t* n_tiles, int32_t* tile_src, hipStream_t stream);
+                              int32_t* tiles, int32_t* n_tiles, int32_t* tile_src,
+                              const uint8_t* resident, hipStream_t stream);
 
 // K2 over many workgroups (large batches): hist holds group_hist_blocks(T*k) x E int32.
 int group_hist_blocks(int P);
 hipError_t launch_group_multi(const int32_t* ids, int T, int k, int E, int bm, int max_tiles, int32_t* hist,
                               int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* tiles,
-                              int32_t* n_tiles, int32_t* tile_src, hipStream_t stream);
+                              int32_t* n_tiles, int32_t* tile_src, const uint8_t* resident,
+                              hipStream_t stream);
 
 // Tile shapes: returns the token-tile height (BM) used for num_tokens:
 // 16 for decode-sized expert groups (gemv form), else kPrefillTileM when
@@ -120,7 +123,8 @@ hipError_t launch_shared_gate(const void* x, const void* gate_w, int act_bf16, i
                               float* gate_out, hipStream_t stream);
 
 hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, const int32_t* inv,
-                          const float* y_shared, const float* shared_gate, int T, int k, int H,
-                          void* out, int out_bf16, hipStream_t stream);
+                          const float* y_shared, const float* shared_gate, const uint8_t* resident,
+                          const void* extra, int T, int k, int H, void* out, int out_bf16,
+                          hipStream_t stream);
 
 }  // namespace nkt

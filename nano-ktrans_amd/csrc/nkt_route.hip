@@ -236,7 +236,8 @@ __device__ __forceinline__ void group_body(const int32_t* ids, int T, int k, int
                                            int32_t* __restrict__ perm, int32_t* __restrict__ inv,
                                            int32_t* __restrict__ tiles,
                                            int32_t* __restrict__ n_tiles,
-                                           int32_t* __restrict__ tile_src, GroupLds& L) {
+                                           int32_t* __restrict__ tile_src,
+                                           const uint8_t* __restrict__ resident, GroupLds& L) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -267,7 +268,8 @@ __device__ __forceinline__ void group_body(const int32_t* ids, int T, int k, int
   }
   __syncthreads();
 
-  // exclusive scans over experts (wave 0, 4 experts per lane): positions and tiles
+  // exclusive scans over experts (wave 0, 4 experts per lane): positions and
+  // tiles (experts that are not HBM-resident get no tiles)
   if (wave == 0) {
     int local[4], tl[4];
     int sum = 0, tsum = 0;
@@ -275,7 +277,7 @@ __device__ __forceinline__ void group_body(const int32_t* ids, int T, int k, int
     for (int i = 0; i < 4; ++i) {
       const int e = lane * 4 + i;
       local[i] = (e < E) ? L.tot[e] : 0;
-      tl[i] = (local[i] + bm - 1) / bm;
+      tl[i] = (e < E && (!resident || resident[e])) ? (local[i] + bm - 1) / bm : 0;
       sum += local[i];
       tsum += tl[i];
     }
@@ -326,7 +328,7 @@ __device__ __forceinline__ void group_body(const int32_t* ids, int T, int k, int
       const int pos = L.hist[wave][e] + rank;
       perm[pos] = p;
       inv[p] = pos;
-      if (tile_src) {
+      if (tile_src && (!resident || resident[e])) {
         const int rel = pos - L.off_s[e];
         const int ti = L.tile_off[e] + rel / bm;
         if (ti < max_tiles) tile_src[ti * kTileSrcCols + rel % bm] = p / k;
@@ -340,7 +342,7 @@ __device__ __forceinline__ void group_body(const int32_t* ids, int T, int k, int
   // group lane/16 takes a tile, its 16 lanes the tile's source-row padding
   for (int e = wave; e < E; e += kGroupWaves) {
     const int c = L.tot[e];
-    const int nt = (c + bm - 1) / bm;
+    const int nt = (!resident || resident[e]) ? (c + bm - 1) / bm : 0;
     for (int m = lane >> 4; m < nt; m += 4) {
       const int ti = L.tile_off[e] + m;
       if (ti < max_tiles) {
@@ -388,7 +390,8 @@ __global__ void __launch_bounds__(1024) scatter_kernel(const int32_t* __restrict
                                                        int32_t* __restrict__ perm, int32_t* __restrict__ inv,
                                                        int32_t* __restrict__ tiles,
                                                        int32_t* __restrict__ n_tiles,
-                                                       int32_t* __restrict__ tile_src) {
+                                                       int32_t* __restrict__ tile_src,
+                                                       const uint8_t* __restrict__ resident) {
   __shared__ int32_t tot[kMaxExperts], pre[kMaxExperts], off_s[kMaxExperts + 1], tile_off[kMaxExperts + 1];
   __shared__ int32_t whist[kScatterWaves][kMaxExperts];
   const int tid = threadIdx.x;
@@ -410,7 +413,8 @@ __global__ void __launch_bounds__(1024) scatter_kernel(const int32_t* __restrict
   }
   for (int i = tid; i < kScatterWaves * kMaxExperts; i += 1024) (&whist[0][0])[i] = 0;
   __syncthreads();
-  // exclusive scans over experts (wave 0, 4 experts per lane): positions and tiles
+  // exclusive scans over experts (wave 0, 4 experts per lane): positions and
+  // tiles (experts that are not HBM-resident get no tiles)
   if (wave == 0) {
     int local[4], tl[4];
     int sum = 0, tsum = 0;
@@ -418,7 +422,7 @@ __global__ void __launch_bounds__(1024) scatter_kernel(const int32_t* __restrict
     for (int i = 0; i < 4; ++i) {
       const int e = lane * 4 + i;
       local[i] = (e < E) ? tot[e] : 0;
-      tl[i] = (local[i] + bm - 1) / bm;
+      tl[i] = (e < E && (!resident || resident[e])) ? (local[i] + bm - 1) / bm : 0;
       sum += local[i];
       tsum += tl[i];
     }
@@ -471,7 +475,7 @@ __global__ void __launch_bounds__(1024) scatter_kernel(const int32_t* __restrict
     for (int ti = tile_off[E] + tid; ti < max_tiles; ti += 1024) *(int4*)(tiles + 4 * ti) = int4{0, 0, 0, 0};
     for (int e = wave; e < E; e += kScatterWaves) {
       const int c = tot[e];
-      const int nt = (c + bm - 1) / bm;
+      const int nt = (!resident || resident[e]) ? (c + bm - 1) / bm : 0;
       for (int m = lane >> 4; m < nt; m += 4) {
         const int ti = tile_off[e] + m;
         if (ti < max_tiles) {
@@ -502,7 +506,7 @@ __global__ void __launch_bounds__(1024) scatter_kernel(const int32_t* __restrict
       const int pos = whist[wave][e] + rank;
       perm[pos] = p;
       inv[p] = pos;
-      if (tile_src) {
+      if (tile_src && (!resident || resident[e])) {
         const int rel = pos - off_s[e];
         const int ti = tile_off[e] + rel / bm;
         if (ti < max_tiles) tile_src[ti * kTileSrcCols + rel % bm] = p / k;
@@ -517,7 +521,8 @@ int group_hist_blocks(int P) { return (P + kPairsPerBlock - 1) / kPairsPerBlock;
 
 hipError_t launch_group_multi(const int32_t* ids, int T, int k, int E, int bm, int max_tiles, int32_t* hist,
                               int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* tiles,
-                              int32_t* n_tiles, int32_t* tile_src, hipStream_t stream) {
+                              int32_t* n_tiles, int32_t* tile_src, const uint8_t* resident,
+                              hipStream_t stream) {
   if (tile_src && bm != kTileSrcCols) return hipErrorInvalidValue;
   const int P = T * k;
   const int nb = group_hist_blocks(P);
@@ -526,7 +531,7 @@ hipError_t launch_group_multi(const int32_t* ids, int T, int k, int E, int bm, i
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(scatter_kernel, dim3(nb), dim3(1024), 0, stream, ids, P, k, E, bm, max_tiles, hist, counts,
-                     offsets, perm, inv, tiles, n_tiles, tile_src);
+                     offsets, perm, inv, tiles, n_tiles, tile_src, resident);
   return hipGetLastError();
 }
 
@@ -537,7 +542,8 @@ __global__ void __launch_bounds__(1024) route_group_kernel(
     const void* __restrict__ logits, int T, int E, int k, unsigned flags, int bm, int max_tiles,
     int32_t* __restrict__ ids_out, float* __restrict__ w_out, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ inv,
-    int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles, int32_t* __restrict__ tile_src) {
+    int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles, int32_t* __restrict__ tile_src,
+    const uint8_t* __restrict__ resident) {
   __shared__ GroupLds L;
   __shared__ int32_t ids_s[kFusedRouteMaxPairs];
   __shared__ float sv[kGroupWaves][kMaxTopK];
@@ -555,7 +561,7 @@ __global__ void __launch_bounds__(1024) route_group_kernel(
     }
   }
   __syncthreads();
-  group_body(ids_s, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, tile_src, L);
+  group_body(ids_s, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, tile_src, resident, L);
 }
 
 #define NKT_VPL_SWITCH(E, CASE) \
@@ -591,7 +597,8 @@ bool route_group_fused(int T, int k) { return T <= kFusedRouteMaxTokens && T * k
 hipError_t launch_route_group(const void* logits, int act_bf16, int T, int E, int k,
                               unsigned flags, int bm, int max_tiles, int32_t* ids, float* w,
                               int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
-                              int32_t* tiles, int32_t* n_tiles, int32_t* tile_src, hipStream_t stream) {
+                              int32_t* tiles, int32_t* n_tiles, int32_t* tile_src,
+                              const uint8_t* resident, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
   if (!route_group_fused(T, k)) return hipErrorInvalidValue;
   if (tile_src && bm != kTileSrcCols) return hipErrorInvalidValue;
@@ -601,11 +608,11 @@ hipError_t launch_route_group(const void* logits, int act_bf16, int T, int E, in
     if (act_bf16)                                                                               \
       hipLaunchKernelGGL((route_group_kernel<V, true>), grid, block, 0, stream, logits, T, E, k, \
                          flags, bm, max_tiles, ids, w, counts, offsets, perm, inv, tiles,       \
-                         n_tiles, tile_src);                                                    \
+                         n_tiles, tile_src, resident);                                          \
     else                                                                                        \
       hipLaunchKernelGGL((route_group_kernel<V, false>), grid, block, 0, stream, logits, T, E,  \
                          k, flags, bm, max_tiles, ids, w, counts, offsets, perm, inv, tiles,    \
-                         n_tiles, tile_src);                                                    \
+                         n_tiles, tile_src, resident);                                          \
     break;
   NKT_VPL_SWITCH(E, NKT_RG_CASE)
 #undef NKT_RG_CASE

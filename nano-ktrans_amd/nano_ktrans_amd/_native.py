@@ -67,6 +67,8 @@ EXPORTED_SYMBOLS = (
     "nkt_moe_experts_phase_timed",
     "nkt_moe_shared",
     "nkt_moe_combine",
+    "nkt_moe_combine_extra",
+    "nkt_moe_bind_residency",
     "nkt_moe_forward",
     "nkt_moe_route_hidden",
     "nkt_moe_forward_hidden",
@@ -121,6 +123,10 @@ def lib() -> ctypes.CDLL:
     L.nkt_moe_combine.restype = i
     L.nkt_moe_forward.argtypes = [vp, vp, vp, i, vp, vp, sz, vp, cp, sz]
     L.nkt_moe_forward.restype = i
+    L.nkt_moe_combine_extra.argtypes = [vp, i, vp, vp, vp, sz, vp, cp, sz]
+    L.nkt_moe_combine_extra.restype = i
+    L.nkt_moe_bind_residency.argtypes = [vp, vp, cp, sz]
+    L.nkt_moe_bind_residency.restype = i
     L.nkt_moe_route_hidden.argtypes = [vp, vp, i, vp, sz, vp, cp, sz]
     L.nkt_moe_route_hidden.restype = i
     L.nkt_moe_forward_hidden.argtypes = [vp, vp, i, vp, vp, sz, vp, cp, sz]

@@ -1,12 +1,13 @@
 """HybridMoE: drop-in MoE layer whose expert path runs as HIP kernels on MI355X.
 
 Same constructor keywords and ``forward(hidden_states, router_logits)`` as
-nano_ktrans/layers/hybrid_moe.py:55-86, 3310-3570.  Every expert lives in
-HBM (an MI355X holds the experts of a whole Qwen3-30B-A3B or Mixtral-8x7B
-model), so the CPU/PIM offload split of the reference collapses to one device
-path: experts whose ``gpu_experts_mask`` entry is False are read from
-``weight_path`` (dense ``.weight`` or GPTQ ``.qweight``/``.scales``) into HBM
-instead of being served by an offload backend.  The residency control plane
+nano_ktrans/layers/hybrid_moe.py:55-86, 3310-3570.  By default every expert
+lives in HBM (an MI355X holds the experts of a whole Qwen3-30B-A3B or
+Mixtral-8x7B model), so the CPU/PIM offload split of the reference collapses
+to one device path: experts whose ``gpu_experts_mask`` entry is False are read
+from ``weight_path`` (dense ``.weight`` or GPTQ ``.qweight``/``.scales``) into
+HBM instead of being served by an offload backend (pass
+``offload_backend_impl`` to keep them out of HBM).  The residency control plane
 (migration, prefetch caches, scheduler, expert-map store) has nothing to do in
 that arrangement; its keywords are accepted and ignored, and an enabled
 dynamic scheduler is rejected.
@@ -20,6 +21,18 @@ Additions, keyword-only and off by default:
                      nn.Linear(H, 1) gate; forward then adds
                      sigmoid(gate(x)) * shared_expert(x) as
                      nano_ktrans/models/mixtral.py:215-218 does.
+  gate               the router nn.Linear(H, E, bias=False); forward(x) without
+                     router_logits then runs the router GEMV inside the path.
+  offload_backend_impl
+                     an object with the reference's offload contract
+                     (submit_forward(hidden_states, topk_ids, topk_weights,
+                     cuda_stream), sync_forward(hidden_states, cuda_stream),
+                     nano_ktrans/kernels/offload_backend.py:40-52).  With it,
+                     experts whose gpu_experts_mask entry is False stay out of
+                     HBM and the backend serves them: the routing goes to
+                     submit_forward, the resident experts run on the GPU, and
+                     sync_forward's sum joins the combine
+                     (nano_ktrans/layers/hybrid_moe.py:3373-3378, 3563-3570).
   max_tokens         largest token count per call (default 65536).
 """
 from __future__ import annotations
@@ -91,6 +104,7 @@ class HybridMoE(nn.Module):
         shared_expert: Optional[nn.Module] = None,
         shared_expert_gate: Optional[nn.Module] = None,
         gate: Optional[nn.Module] = None,
+        offload_backend_impl: Optional[object] = None,
         max_tokens: int = 65536,
     ):
         super().__init__()
@@ -127,7 +141,15 @@ class HybridMoE(nn.Module):
         # router_logits runs the router GEMV fused into the routing launch
         self.gate = gate
         self.max_tokens = max_tokens
-        self.offload_backend = None  # every expert is HBM-resident
+        mask = [bool(m) for m in gpu_experts_mask.reshape(-1).tolist()] if gpu_experts_mask is not None \
+            else [True] * num_experts
+        if offload_backend_impl is not None and not all(mask):
+            # the mask decides residency; the backend serves the other experts
+            self.offload_backend = offload_backend_impl
+            self.resident = mask
+        else:
+            self.offload_backend = None  # every expert is HBM-resident
+            self.resident = [True] * num_experts
         self._native: Optional[NativeMoE] = None
         self.forward_calls = 0
         self.last_phase = ""
@@ -154,7 +176,7 @@ class HybridMoE(nn.Module):
 
     def _materialize(self, device: torch.device, act_dtype: torch.dtype) -> None:
         loader = ExpertWeightLoader(self.weight_path) if self.weight_path else None
-        sources = {e: self._expert_sources(e, loader) for e in range(self.num_experts)}
+        sources = {e: self._expert_sources(e, loader) for e in range(self.num_experts) if self.resident[e]}
         if self.quantization is not None:
             quant = _QUANTIZERS[self.quantization]
             for e, src in sources.items():
@@ -186,6 +208,8 @@ class HybridMoE(nn.Module):
                                           self.shared_expert_gate.weight.detach())
             if self.gate is not None and act_dtype == torch.bfloat16:
                 native.load_router(self.gate.weight.detach())
+        if self.offload_backend is not None:
+            native.set_residency(torch.tensor(self.resident, dtype=torch.bool))
         self._native = native
 
     def reload_weights(self) -> None:
@@ -216,6 +240,8 @@ class HybridMoE(nn.Module):
         native = self._ensure(hidden_states)
         shape = hidden_states.shape
         x = hidden_states.reshape(-1, self.hidden_size)
+        if self.offload_backend is not None:
+            return self._forward_mixed(native, x, router_logits).view(shape)
         if router_logits is None:
             if self.gate is None:
                 raise ValueError("router_logits is required unless HybridMoE was built with gate=")
@@ -225,6 +251,25 @@ class HybridMoE(nn.Module):
         out = native.forward(x, router_logits.reshape(-1, self.num_experts))
         return out.view(shape)
 
+    def _forward_mixed(self, native: NativeMoE, x: torch.Tensor, router_logits: Optional[torch.Tensor]):
+        """Routing -> backend submit -> resident experts on the GPU -> backend sync ->
+        combine with the backend's sum (hybrid_moe.py:3373-3378, 3563-3570)."""
+        T = x.shape[0]
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        if router_logits is None:
+            if self.gate is None:
+                raise ValueError("router_logits is required unless HybridMoE was built with gate=")
+            logits, ids, w, *_ = native.route_hidden(x)
+        else:
+            logits = router_logits.reshape(-1, self.num_experts)
+            ids, w, *_ = native.route(logits)
+        self.offload_backend.submit_forward(x, ids.to(torch.int64), w.to(logits.dtype), stream)
+        native.experts(x)
+        if self.shared_expert is not None:
+            native.shared(x)
+        extra = self.offload_backend.sync_forward(x, stream)
+        return native.combine(T, extra=extra.reshape(T, self.hidden_size).to(x.dtype))
+
     def diagnostics(self) -> dict:
         n = self._native
         return {
@@ -232,6 +277,6 @@ class HybridMoE(nn.Module):
             "forward_calls": self.forward_calls,
             "last_phase": self.last_phase,
             "weight_format": None if n is None else n.weight_format,
-            "experts_resident": self.num_experts,
-            "offload_backend": None,
+            "experts_resident": sum(self.resident),
+            "offload_backend": None if self.offload_backend is None else type(self.offload_backend).__name__,
         }

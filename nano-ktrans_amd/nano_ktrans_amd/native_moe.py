@@ -316,16 +316,44 @@ class NativeMoE:
         return (self.region(T, N.WS_SHARED_GATE, torch.float32, (T,)),
                 self.region(T, N.WS_SHARED_Y, torch.float32, (T, self.hidden_size)))
 
-    def combine(self, num_tokens: int, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """K5 after ``route``/``experts`` (and ``shared`` when the layer has one)."""
+    def combine(self, num_tokens: int, out: Optional[torch.Tensor] = None,
+                extra: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """K5 after ``route``/``experts`` (and ``shared`` when the layer has one).
+        extra [T, H] (act dtype): an offload backend's sum for the non-resident
+        experts, added inside the same fixed-order fp32 sum."""
         T = num_tokens
         if out is None:
             out = torch.empty(T, self.hidden_size, dtype=self.act_dtype, device=self.device)
         ws = self.workspace(T)
         with torch.cuda.device(self.device):
-            self.err.check(self.lib.nkt_moe_combine(self.handle, T, out.data_ptr(), ws.data_ptr(), ws.numel(),
-                                                    self._stream(), self.err.buf, self.err.size), "nkt_moe_combine")
+            if extra is None:
+                self.err.check(self.lib.nkt_moe_combine(self.handle, T, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                                        self._stream(), self.err.buf, self.err.size),
+                               "nkt_moe_combine")
+            else:
+                e = self._check_input(extra, self.hidden_size, "extra")
+                if e.shape[0] != T:
+                    raise ValueError(f"extra has {e.shape[0]} rows, expected {T}")
+                self._extra = e  # kept alive until the next call (the kernel reads it asynchronously)
+                self.err.check(self.lib.nkt_moe_combine_extra(self.handle, T, e.data_ptr(), out.data_ptr(),
+                                                              ws.data_ptr(), ws.numel(), self._stream(),
+                                                              self.err.buf, self.err.size), "nkt_moe_combine_extra")
         return out
+
+    def set_residency(self, resident: Optional[torch.Tensor]) -> None:
+        """Which experts have their weights in HBM (bool [E]); None = all.  Non-resident
+        experts get no GEMM work; their sum comes in through ``combine(extra=...)``."""
+        if resident is None:
+            self._resident = None
+            ptr = None
+        else:
+            r = torch.as_tensor(resident).reshape(-1)
+            if r.numel() != self.num_experts:
+                raise ValueError(f"residency mask needs {self.num_experts} entries")
+            self._resident = r.to(torch.uint8).to(self.device).contiguous()
+            ptr = self._resident.data_ptr()
+        self.err.check(self.lib.nkt_moe_bind_residency(self.handle, ptr, self.err.buf, self.err.size),
+                       "nkt_moe_bind_residency")
 
     def forward_hidden(self, hidden_states: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """The whole layer from hidden states (router GEMV fused; after ``load_router``)."""

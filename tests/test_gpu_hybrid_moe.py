@@ -199,3 +199,57 @@ def test_shared_expert_int8(gpu_device):
         shared={"gate": q(shared.w1.weight), "up": q(shared.w3.weight), "down": q(shared.w2.weight)},
         shared_gate=gate.weight.detach().float().reshape(-1).cpu())
     _check(out, oracle_forward(layer, x, logits))
+
+
+class _OracleOffload:
+    """A stand-in offload backend with the reference's contract
+    (nano_ktrans/kernels/offload_backend.py:40-52): the weighted sum of the
+    non-resident experts' outputs, computed on the CPU by the oracle."""
+
+    def __init__(self, experts, resident):
+        self.experts, self.resident = experts, resident
+        self.pending = None
+        self.calls = 0
+
+    def submit_forward(self, hidden_states, topk_ids, topk_weights, cuda_stream):
+        assert topk_ids.dtype == torch.int64
+        self.pending = (topk_ids.cpu().numpy(), topk_weights.float().cpu().numpy())
+
+    def sync_forward(self, hidden_states, cuda_stream):
+        ids, w = self.pending
+        x = hidden_states.float().cpu().numpy()
+        out = np.zeros_like(x)
+        for t in range(x.shape[0]):
+            for j in np.argsort(ids[t], kind="stable"):  # ascending expert id
+                e = int(ids[t, j])
+                if not self.resident[e]:
+                    out[t] += w[t, j] * O.expert_forward(x[t:t + 1], self.experts[e])[0]
+        self.calls += 1
+        return torch.from_numpy(out).to(hidden_states.device, hidden_states.dtype)
+
+
+@pytest.mark.parametrize("T", [5, 300])
+def test_mixed_residency_with_offload_backend(gpu_device, T):
+    """gpu_experts_mask False + an offload backend: non-resident experts get no GPU
+    work, the backend's sum joins the combine, and the result matches the oracle's
+    all-expert forward (decode and prefill forms)."""
+    announce(f"HybridMoE mixed residency T={T}")
+    E, k, H, I = 16, 4, 2048, 768
+    experts = nn.ModuleDict({str(e): _init(SparseExpertMLP(H, I), 500 + e).to(gpu_device, torch.bfloat16)
+                             for e in range(E)})
+    mask = torch.tensor([e % 3 != 1 for e in range(E)])
+    oracle_experts = [O.Expert(_bf16(experts[str(e)].w1.weight).numpy(), _bf16(experts[str(e)].w3.weight).numpy(),
+                               _bf16(experts[str(e)].w2.weight).numpy()) for e in range(E)]
+    backend = _OracleOffload(oracle_experts, mask.tolist())
+    moe = HybridMoE(E, k, H, I, experts, mask, 0, "", router_use_softmax=True, normalize_topk_prob=True,
+                    expert_key_template=MIXTRAL_SPEC.expert_key_template,
+                    expert_proj_names=MIXTRAL_SPEC.expert_proj_names, offload_backend_impl=backend)
+    x, logits = _inputs(T, H, E, seed=7)
+    out = moe(x.to(gpu_device), logits.to(gpu_device))
+    torch.cuda.synchronize()
+    assert backend.calls == 1 and moe.diagnostics()["experts_resident"] == int(mask.sum())
+    cfg = MoEConfig("m", H, E, k, I, 0, True, True, "bf16", "bf16")
+    layer = Layer(cfg, torch.zeros(E, H), [
+        {"gate": _bf16(experts[str(e)].w1.weight), "up": _bf16(experts[str(e)].w3.weight),
+         "down": _bf16(experts[str(e)].w2.weight)} for e in range(E)])
+    _check(out, oracle_forward(layer, x, logits))
