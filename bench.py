@@ -147,23 +147,25 @@ def time_graph(layers, xs, ls, outs, steps, warmup):
     return ms / (reps * L), reps * L
 
 
-def time_graph_hidden(layers, xs, outs, steps, warmup):
-    """time_graph for the layer from hidden states alone (router GEMV fused):
-    ms per layer step."""
+def time_graph_hidden(layers, xs, outs, steps, warmup, call=None):
+    """time_graph for the layer from hidden states alone (router GEMV fused; or
+    call(layer, x, out)): ms per layer step."""
     import torch
 
+    if call is None:
+        call = lambda layer, x, out: layer.forward_hidden(x, out=out)
     L = len(layers)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         for i, layer in enumerate(layers):
-            layer.forward_hidden(xs[i % len(xs)], out=outs[i])
+            call(layer, xs[i % len(xs)], outs[i])
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for i, layer in enumerate(layers):
-            layer.forward_hidden(xs[i % len(xs)], out=outs[i])
+            call(layer, xs[i % len(xs)], outs[i])
     for _ in range(max(1, (warmup + L - 1) // L)):
         graph.replay()
     torch.cuda.synchronize()
@@ -539,6 +541,14 @@ def main():
         outs = [torch.empty(T, head.H, dtype=torch.bfloat16, device=dev) for _ in layers]
         ms = time_graph_hidden(layers, xs, outs, args.steps, args.warmup)
         r = dict(workload=head.name + "_fused_router", tokens=T, us_per_layer=ms * 1e3,
+                 tokens_per_s=T / (ms * 1e-3))
+        log(json.dumps(r))
+        secondary.append(r)
+        # the decoder layer's MoE half: residual + MoE(RMSNorm(hidden)), router fused
+        norm_w = (1.0 + 0.1 * torch.randn(head.H, generator=torch.Generator().manual_seed(3))).to(dev)
+        fwd = lambda layer, x, out: layer.forward_block(x, norm_w, 1e-6, out=out)
+        ms = time_graph_hidden(layers, xs, outs, args.steps, args.warmup, call=fwd)
+        r = dict(workload=head.name + "_decoder_block", tokens=T, us_per_layer=ms * 1e3,
                  tokens_per_s=T / (ms * 1e-3))
         log(json.dumps(r))
         secondary.append(r)

@@ -80,7 +80,8 @@ extern "C" {
 #define NKT_WS_SHARED_H 9     /* act dtype [T, I_s]                                    */
 #define NKT_WS_SHARED_Y 10    /* fp32 [T, H]                                           */
 #define NKT_WS_ROUTER_LOGITS 11 /* bf16 [T, E] router logits of the *_hidden entry points */
-#define NKT_WS_NUM_REGIONS 12
+#define NKT_WS_NORMED 12        /* bf16 [T, H] RMSNorm output of nkt_moe_forward_block    */
+#define NKT_WS_NUM_REGIONS 13
 
 /* Create a handle for one layer shape.
  * Replaces the construction of HybridMoE's expert state
@@ -198,6 +199,15 @@ int nkt_moe_route_hidden(void* handle, const void* hidden_states, int num_tokens
 int nkt_moe_forward_hidden(void* handle, const void* hidden_states, int num_tokens, void* out,
                            void* workspace, size_t workspace_bytes, void* stream, char* err,
                            size_t err_len);
+
+/* The decoder layer's MoE half (nano_ktrans/models/mixtral.py:206-223):
+ * x = RMSNorm(hidden_states) with norm_weight [H] (bf16, device) and eps as
+ * nano_ktrans/layers/norm.py:11-17 computes it (written to NKT_WS_NORMED),
+ * then the layer from x as nkt_moe_forward_hidden, and out = hidden_states +
+ * that output (the residual add inside the combine's fp32 sum).  bf16 only. */
+int nkt_moe_forward_block(void* handle, const void* hidden_states, const void* norm_weight, float eps,
+                          int num_tokens, void* out, void* workspace, size_t workspace_bytes, void* stream,
+                          char* err, size_t err_len);
 
 /* Library version string (static storage). */
 const char* nkt_moe_version(void);

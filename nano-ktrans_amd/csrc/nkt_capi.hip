@@ -130,6 +130,7 @@ WsLayout ws_layout(const Handle* h, int T) {
   sz[NKT_WS_SHARED_H] = h->Is > 0 ? (size_t)T * h->Is * es : 0;
   sz[NKT_WS_SHARED_Y] = h->Is > 0 ? (size_t)T * h->H * 4 : 0;
   sz[NKT_WS_ROUTER_LOGITS] = h->act_bf16 ? (size_t)T * h->E * 2 : 0;
+  sz[NKT_WS_NORMED] = h->act_bf16 ? (size_t)T * h->H * 2 : 0;
   sz[kWsTiles] = (size_t)L.max_tiles * 16;
   sz[kWsNTiles] = 4;
   sz[kWsXsum] = (size_t)T * (h->H / 128) * 4;
@@ -379,7 +380,7 @@ int do_shared(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipS
 }
 
 int do_combine(Handle* h, int T, void* out, void* ws, const WsLayout& L, hipStream_t st, char* err,
-               size_t len, const void* extra = nullptr) {
+               size_t len, const void* extra = nullptr, const void* residual = nullptr) {
   if (!out) {
     set_err(err, len, "null output");
     return NKT_ERR;
@@ -390,7 +391,7 @@ int do_combine(Handle* h, int T, void* out, void* ws, const WsLayout& L, hipStre
                                 ws_ptr<int32_t>(ws, L, NKT_WS_INV),
                                 sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_Y) : nullptr,
                                 sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE) : nullptr, h->resident,
-                                extra, T, h->k, h->H, out, h->act_bf16, st),
+                                extra, residual, T, h->k, h->H, out, h->act_bf16, st),
                  "combine kernel", err, len))
     return NKT_ERR;
   return NKT_OK;
@@ -691,6 +692,36 @@ int nkt_moe_forward_hidden(void* handle, const void* hidden_states, int num_toke
   return do_combine(h, num_tokens, out, workspace, L, st, err, err_len);
 }
 
-const char* nkt_moe_version(void) { return "nkt_moe 0.2.0 gfx950"; }
+int nkt_moe_forward_block(void* handle, const void* hidden_states, const void* norm_weight, float eps,
+                          int num_tokens, void* out, void* workspace, size_t workspace_bytes, void* stream,
+                          char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!check_call(h, num_tokens, workspace, workspace_bytes, err, err_len)) return NKT_ERR;
+  if (num_tokens == 0) return NKT_OK;
+  if (!h->act_bf16) {
+    set_err(err, err_len, "the decoder-block form needs bf16 activations");
+    return NKT_ERR;
+  }
+  if (!hidden_states || !norm_weight || !out) {
+    set_err(err, err_len, "null hidden_states, norm_weight or output");
+    return NKT_ERR;
+  }
+  if (!(eps >= 0.f)) {
+    set_err(err, err_len, "eps must be >= 0");
+    return NKT_ERR;
+  }
+  const WsLayout L = ws_layout(h, num_tokens);
+  hipStream_t st = (hipStream_t)stream;
+  void* x = ws_ptr<void>(workspace, L, NKT_WS_NORMED);
+  if (!check_hip(launch_rmsnorm(hidden_states, norm_weight, eps, num_tokens, h->H, x, st), "rmsnorm kernel", err,
+                 err_len))
+    return NKT_ERR;
+  if (do_route_hidden(h, x, num_tokens, workspace, L, st, err, err_len) != NKT_OK) return NKT_ERR;
+  if (do_experts(h, x, num_tokens, workspace, L, st, err, err_len) != NKT_OK) return NKT_ERR;
+  if (h->Is > 0 && do_shared(h, x, num_tokens, workspace, L, st, err, err_len) != NKT_OK) return NKT_ERR;
+  return do_combine(h, num_tokens, out, workspace, L, st, err, err_len, nullptr, hidden_states);
+}
+
+const char* nkt_moe_version(void) { return "nkt_moe 0.3.0 gfx950"; }
 
 }  // extern "C"

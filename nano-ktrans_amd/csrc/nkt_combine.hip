@@ -5,8 +5,11 @@
 //     nano_ktrans/layers/hybrid_moe.py:3512-3533 and cpu_moe.py:515-536),
 //     in fp32, then the sum an offload backend returned for the experts that
 //     are not HBM-resident (hybrid_moe.py:3563-3570; their slots are skipped),
-//     then the gated shared expert, then one rounding to the output dtype.
-//     No atomics: each output element is owned by one thread.
+//     then the gated shared expert, then (decoder-block form) the residual
+//     stream, then one rounding to the output dtype.  No atomics: each output
+//     element is owned by one thread.
+// Decoder-block form: RMSNorm of the residual stream before the path
+//     (nano_ktrans/layers/norm.py:11-17), one wave per token.
 #include "nkt_common.h"
 #include "nkt_internal.h"
 
@@ -39,7 +42,8 @@ __global__ void __launch_bounds__(256) combine_kernel(
     const float* __restrict__ y, const int32_t* __restrict__ ids, const float* __restrict__ w,
     const int32_t* __restrict__ inv, const float* __restrict__ y_shared,
     const float* __restrict__ shared_gate, const uint8_t* __restrict__ resident,
-    const void* __restrict__ extra, int num_tokens, int H, void* __restrict__ out, int out_bf16) {
+    const void* __restrict__ extra, const void* __restrict__ residual, int num_tokens, int H,
+    void* __restrict__ out, int out_bf16) {
   const int t = blockIdx.x;
   const int c = blockIdx.y * blockDim.x + threadIdx.x;  // float4 column index
   // order the token's slots by expert id: rank[j] = #{i : id_i < id_j}
@@ -108,6 +112,12 @@ __global__ void __launch_bounds__(256) combine_kernel(
     }
   }
   if (y_shared) acc += sg * vs;
+  if (residual) {
+    if (out_bf16)
+      acc += bf16x4_to_f32(*(const u32x2*)((const uint16_t*)residual + (int64_t)t * H + 4 * c));
+    else
+      acc += *(const f32x4*)((const float*)residual + (int64_t)t * H + 4 * c);
+  }
   if (out_bf16) {
     u32x2 pk;
     pk[0] = pack_bf16x2(acc[0], acc[1]);
@@ -116,6 +126,51 @@ __global__ void __launch_bounds__(256) combine_kernel(
   } else {
     *(f32x4*)((float*)out + (int64_t)t * H + 4 * c) = acc;
   }
+}
+
+// RMSNorm as nano_ktrans/layers/norm.py:11-17 computes it: in fp32,
+// x * rsqrt(mean(x^2) + eps), rounded to bf16, then times the bf16 weight,
+// rounded again.  Lane l holds the 8-column chunks l, l + 64, ...; the sum of
+// squares adds a lane's chunks in order, then a fixed butterfly.
+__global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* __restrict__ x,
+                                                      const uint16_t* __restrict__ w, float eps, int T,
+                                                      int H, uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const uint16_t* xr = x + (int64_t)t * H;
+  float ss = 0.f;
+  for (int c = lane * 8; c < H; c += 512) {
+    const u32x4 v = *(const u32x4*)(xr + c);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const float a = __uint_as_float(v[h] << 16), b = __uint_as_float(v[h] & 0xffff0000u);
+      ss += a * a;
+      ss += b * b;
+    }
+  }
+  ss = wave_sum_butterfly(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)H + eps);
+  for (int c = lane * 8; c < H; c += 512) {
+    const u32x4 v = *(const u32x4*)(xr + c);
+    const u32x4 g = *(const u32x4*)(w + c);
+    u32x4 o;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const float a = bf16_round(__uint_as_float(v[h] << 16) * inv);
+      const float b = bf16_round(__uint_as_float(v[h] & 0xffff0000u) * inv);
+      o[h] = pack_bf16x2(a * __uint_as_float(g[h] << 16), b * __uint_as_float(g[h] & 0xffff0000u));
+    }
+    *(u32x4*)(out + (int64_t)t * H + c) = o;
+  }
+}
+
+hipError_t launch_rmsnorm(const void* x, const void* w, float eps, int T, int H, void* out, hipStream_t stream) {
+  if (T <= 0) return hipSuccess;
+  if (H % 8 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((T + 3) / 4), dim3(256), 0, stream, (const uint16_t*)x,
+                     (const uint16_t*)w, eps, T, H, (uint16_t*)out);
+  return hipGetLastError();
 }
 
 hipError_t launch_shared_gate(const void* x, const void* gate_w, int act_bf16, int T, int H,
@@ -128,14 +183,14 @@ hipError_t launch_shared_gate(const void* x, const void* gate_w, int act_bf16, i
 
 hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, const int32_t* inv,
                           const float* y_shared, const float* shared_gate, const uint8_t* resident,
-                          const void* extra, int T, int k, int H, void* out, int out_bf16,
-                          hipStream_t stream) {
+                          const void* extra, const void* residual, int T, int k, int H, void* out,
+                          int out_bf16, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
   dim3 grid(T, (H / 4 + 255) / 256), block(256);
 #define NKT_COMBINE_CASE(KK)                                                                   \
   case KK:                                                                                     \
     hipLaunchKernelGGL(combine_kernel<KK>, grid, block, 0, stream, y, ids, w, inv, y_shared,   \
-                       shared_gate, resident, extra, T, H, out, out_bf16);                     \
+                       shared_gate, resident, extra, residual, T, H, out, out_bf16);           \
     break;
   switch (k) {
     NKT_COMBINE_CASE(1)

@@ -124,7 +124,10 @@ hipError_t launch_shared_gate(const void* x, const void* gate_w, int act_bf16, i
 
 hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, const int32_t* inv,
                           const float* y_shared, const float* shared_gate, const uint8_t* resident,
-                          const void* extra, int T, int k, int H, void* out, int out_bf16,
-                          hipStream_t stream);
+                          const void* extra, const void* residual, int T, int k, int H, void* out,
+                          int out_bf16, hipStream_t stream);
+
+// bf16 RMSNorm rows of x [T, H] with weight w [H] (decoder-block form)
+hipError_t launch_rmsnorm(const void* x, const void* w, float eps, int T, int H, void* out, hipStream_t stream);
 
 }  // namespace nkt

@@ -52,6 +52,7 @@ WS_SHARED_GATE = 8
 WS_SHARED_H = 9
 WS_SHARED_Y = 10
 WS_ROUTER_LOGITS = 11
+WS_NORMED = 12
 
 EXPORTED_SYMBOLS = (
     "nkt_moe_create",
@@ -72,6 +73,7 @@ EXPORTED_SYMBOLS = (
     "nkt_moe_forward",
     "nkt_moe_route_hidden",
     "nkt_moe_forward_hidden",
+    "nkt_moe_forward_block",
     "nkt_moe_version",
 )
 
@@ -131,6 +133,8 @@ def lib() -> ctypes.CDLL:
     L.nkt_moe_route_hidden.restype = i
     L.nkt_moe_forward_hidden.argtypes = [vp, vp, i, vp, vp, sz, vp, cp, sz]
     L.nkt_moe_forward_hidden.restype = i
+    L.nkt_moe_forward_block.argtypes = [vp, vp, vp, ctypes.c_float, i, vp, vp, sz, vp, cp, sz]
+    L.nkt_moe_forward_block.restype = i
     L.nkt_moe_version.argtypes = []
     L.nkt_moe_version.restype = ctypes.c_char_p
     _lib = L

@@ -370,6 +370,27 @@ class NativeMoE:
                                                            self.err.buf, self.err.size), "nkt_moe_forward_hidden")
         return out
 
+    def forward_block(self, hidden_states: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The decoder layer's MoE half: hidden + MoE(RMSNorm(hidden)) with the fused
+        router (after ``load_router``); the RMSNorm output stays in NKT_WS_NORMED."""
+        x = self._check_input(hidden_states, self.hidden_size, "hidden_states")
+        T = x.shape[0]
+        w = norm_weight.to(self.act_dtype).to(self.device).reshape(-1).contiguous()
+        if w.numel() != self.hidden_size:
+            raise ValueError(f"norm weight must have {self.hidden_size} entries")
+        if out is None:
+            out = torch.empty(T, self.hidden_size, dtype=self.act_dtype, device=self.device)
+        if T == 0:
+            return out
+        self._norm_w = w  # kept alive while the kernels run
+        ws = self.workspace(T)
+        with torch.cuda.device(self.device):
+            self.err.check(self.lib.nkt_moe_forward_block(self.handle, x.data_ptr(), w.data_ptr(), float(eps), T,
+                                                          out.data_ptr(), ws.data_ptr(), ws.numel(), self._stream(),
+                                                          self.err.buf, self.err.size), "nkt_moe_forward_block")
+        return out
+
     def forward(self, hidden_states: torch.Tensor, router_logits: torch.Tensor,
                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
         """The whole layer; returns [T, H] in the activation dtype."""

@@ -22,6 +22,8 @@ nano-ktrans tree):
 * ``router_logits``           nano_ktrans/models/mixtral.py:127, 212 (the gate
                               nn.Linear(H, E, bias=False) in bf16: exact dot
                               products rounded once to bf16)
+* ``rms_norm``                nano_ktrans/layers/norm.py:11-17 (the post-attention
+                              RMSNorm of the decoder-block form)
 * ``route``                   nano_ktrans/layers/hybrid_moe.py:3321-3329 (C restatement)
 * ``group``                   nano_ktrans/layers/hybrid_moe.py:3512-3526,
                               nano_ktrans/kernels/cpu_moe.py:515-523 (C restatement)
@@ -140,6 +142,17 @@ def round64_to_bf16(a: np.ndarray) -> np.ndarray:
     toward_zero = np.where(np.abs(f64) > np.abs(a), np.nextafter(f, np.float32(0)), f).astype(np.float32)
     odd = (toward_zero.view(np.uint32) | np.uint32(1)).view(np.float32)
     return bf16_round(np.where(exact, f, odd).astype(np.float32))
+
+
+def rms_norm(x: np.ndarray, weight: np.ndarray, eps: float) -> np.ndarray:
+    """RMSNorm of bf16 rows x [T, H] with bf16 weight [H]
+    (nano_ktrans/layers/norm.py:11-17): t = x * rsqrt(mean(x^2) + eps) cast to
+    bf16, then t * weight cast to bf16.  The mean and the scaling in float64,
+    each bf16 cast one rounding; float32 out."""
+    x64 = np.asarray(x, dtype=np.float64)
+    inv = 1.0 / np.sqrt(np.mean(x64 * x64, axis=-1, keepdims=True) + eps)
+    t = round64_to_bf16(x64 * inv)
+    return round64_to_bf16(t.astype(np.float64) * np.asarray(weight, dtype=np.float64))
 
 
 def route(logits: np.ndarray, top_k: int, use_softmax: bool, renorm: bool, bf16: bool):

@@ -253,3 +253,52 @@ def test_mixed_residency_with_offload_backend(gpu_device, T):
         {"gate": _bf16(experts[str(e)].w1.weight), "up": _bf16(experts[str(e)].w3.weight),
          "down": _bf16(experts[str(e)].w2.weight)} for e in range(E)])
     _check(out, oracle_forward(layer, x, logits))
+
+
+class _RMSNorm(nn.Module):
+    """The reference's RMSNorm parameters (nano_ktrans/layers/norm.py:5-9)."""
+
+    def __init__(self, H, eps):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(H))
+
+
+@pytest.mark.parametrize("T", [16, 300])
+def test_fused_decoder_block(gpu_device, T):
+    """FusedMoEBlock: hidden + MoE(RMSNorm(hidden)) with the fused router.  The
+    RMSNorm output matches the oracle's within one bf16 step, the logits pass
+    check_router_logits, and the block output matches hidden + the oracle's MoE
+    forward on the GPU's normalised input and logits."""
+    from moe_cases import bf16_steps, check_router_logits
+    from nano_ktrans_amd import _native as N
+    from nano_ktrans_amd.layers.moe_block import FusedMoEBlock
+    announce(f"fused decoder block T={T}")
+    E, k, H, I = 16, 4, 2048, 768
+    experts = nn.ModuleDict({str(e): _init(SparseExpertMLP(H, I), 700 + e).to(gpu_device, torch.bfloat16)
+                             for e in range(E)})
+    gate = _init(nn.Linear(H, E, bias=False), 42).to(gpu_device, torch.bfloat16)
+    norm = _RMSNorm(H, 1e-6)
+    with torch.no_grad():
+        norm.weight.copy_(1.0 + 0.1 * torch.randn(H, generator=torch.Generator().manual_seed(8)))
+    norm = norm.to(gpu_device, torch.bfloat16)
+    moe = HybridMoE(E, k, H, I, experts, torch.ones(E, dtype=torch.bool), 0, "", router_use_softmax=True,
+                    normalize_topk_prob=True, expert_key_template=MIXTRAL_SPEC.expert_key_template,
+                    expert_proj_names=MIXTRAL_SPEC.expert_proj_names, gate=gate)
+    block = FusedMoEBlock(norm, moe)
+    h = (torch.randn(T, H, generator=torch.Generator().manual_seed(T)) * 3.0).to(torch.bfloat16).to(gpu_device)
+    out = block(h).clone()
+    torch.cuda.synchronize()
+    native = moe._native
+    xg = native.region(T, N.WS_NORMED, torch.bfloat16, (T, H)).float().cpu().numpy()
+    xo = O.rms_norm(h.float().cpu().numpy(), norm.weight.detach().float().cpu().numpy(), 1e-6)
+    steps = bf16_steps(xg, xo)
+    assert steps.max() <= 1 and (steps == 0).mean() > 0.99
+    logits = native.region(T, N.WS_ROUTER_LOGITS, torch.bfloat16, (T, E)).clone()
+    check_router_logits(logits.float().cpu().numpy(), xg, gate.weight.detach().float().cpu().numpy())
+    cfg = MoEConfig("b", H, E, k, I, 0, True, True, "bf16", "bf16")
+    layer = Layer(cfg, torch.zeros(E, H), [
+        {"gate": _bf16(experts[str(e)].w1.weight), "up": _bf16(experts[str(e)].w3.weight),
+         "down": _bf16(experts[str(e)].w2.weight)} for e in range(E)])
+    moe_ref = oracle_forward(layer, torch.from_numpy(xg), logits.cpu())
+    _check(out, h.float().cpu().numpy() + moe_ref)

@@ -107,6 +107,26 @@ def test_router_logits_agree_with_torch_bf16_linear():
     assert (ulp == 0).mean() > 0.98
 
 
+def test_rms_norm_closed_forms():
+    rng = np.random.default_rng(6)
+    H = 512
+    w = O.bf16_round(rng.standard_normal(H).astype(np.float32))
+    # constant rows, eps 0: x / rms(x) = sign(x) exactly, so the output is +-w
+    x = np.array([[3.0] * H, [-0.125] * H], np.float32)
+    out = O.rms_norm(x, w, 0.0)
+    assert np.array_equal(out[0], w) and np.array_equal(out[1], -w)
+    # eps 0: scaling a row by a power of two leaves the output unchanged
+    r = O.bf16_round(rng.standard_normal((4, H)).astype(np.float32))
+    assert np.array_equal(O.rms_norm(r, w, 0.0), O.rms_norm(8.0 * r, w, 0.0))
+    # unit weight: the rows have unit root-mean-square up to bf16 rounding
+    n = O.rms_norm(r, np.ones(H, np.float32), 1e-6)
+    assert np.allclose(np.sqrt(np.mean(n.astype(np.float64) ** 2, axis=1)), 1.0, atol=2e-3)
+    # eps dominates a tiny row: x / sqrt(eps)
+    tiny = np.full((1, H), 2.0 ** -20, np.float32)
+    assert np.allclose(O.rms_norm(tiny, np.ones(H, np.float32), 1e-2), 2.0 ** -20 / np.sqrt(1e-2 + 2.0 ** -40),
+                       rtol=2 ** -8)
+
+
 # ---------------------------------------------------------------- softmax
 @pytest.mark.parametrize("E", [8, 60, 64, 100, 128, 256])
 def test_softmax_row_close_to_float64(E):
