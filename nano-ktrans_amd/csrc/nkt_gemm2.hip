@@ -6,17 +6,17 @@
 // PackedSparseExpertMLP.forward, nano_ktrans/layers/expert_mlp.py:20-41) and
 // the quantized loop of nano_ktrans/kernels/cpu_moe.py:419-450.
 //
-// Workgroup = 4 waves, tile = 64 positions x 256 weight rows, two
-// workgroups per CU.  gate_up: the
-// 256 rows are 128 gate rows and the 128 matching up rows (wave w holds gate
-// and up rows for the same 32 h columns, so SwiGLU is wave-local); down: 256
-// output rows, 64 per wave.  K advances one 128-wide group per step:
+// Workgroup = 4 or 8 waves, tile = 64 positions x 256 weight rows, two
+// workgroups per CU.  gate_up: the 256 rows are 128 gate rows and the 128
+// matching up rows (a wave holds gate and up rows for the same h columns, so
+// SwiGLU is wave-local); down: 256 output rows split over the waves.  K
+// advances one 128-wide group per step:
 //   * the token tile (64 positions x 128 K, bf16, gathered through the
 //     permutation for gate_up) is staged in LDS, double-buffered: the next
 //     group's rows load into registers while this group computes;
 //   * each wave streams its own weight blocks from HBM into registers (one
 //     16-byte load per lane per 1 KiB block), one group ahead;
-//   * per group a wave runs 4 row tiles x 4 column tiles x 4 K steps of
+//   * per group a wave runs 4 (or 2) row tiles x 4 column tiles x 4 K steps of
 //     v_mfma_f32_16x16x32_bf16, dequantising each weight fragment once.
 // Codes enter the matrix core as exact bf16 integers with an offset (int4:
 // 136 + q, int8: 128 + q); the offset times the group's activation sum
@@ -34,10 +34,10 @@ namespace {
 
 constexpr int kBM = 64;           // positions per tile
 constexpr int kCT = kBM / 16;     // 16-position MFMA column tiles
-constexpr int kRT = 4;            // 16-row weight tiles per wave
+
 constexpr int kXcds = 8;          // MI355X: accelerator complex dies, each with its own L2
 
-template <int WF>
+template <int WF, int kRT>
 struct ARegs {
   static constexpr int NBLK = 128 / block_k(WF);
   u32x4 w[kRT][NBLK];
@@ -47,8 +47,9 @@ struct ARegs {
 
 }  // namespace
 
-template <int WF, int PHASE>
-__global__ void __launch_bounds__(256, 2) gemm2_kernel(GemmArgs a, int n_slabs) {
+template <int WF, int PHASE, int kWaves>
+__global__ void __launch_bounds__(64 * kWaves, 2) gemm2_kernel(GemmArgs a, int n_slabs) {
+  constexpr int kRT = 16 / kWaves;  // 16-row weight tiles per wave
   constexpr int NBLK = 128 / block_k(WF);
   // two separate LDS objects (not one array) so the compiler can tell a
   // direct-to-LDS load into one buffer from reads of the other
@@ -57,7 +58,7 @@ __global__ void __launch_bounds__(256, 2) gemm2_kernel(GemmArgs a, int n_slabs) 
   __shared__ float xsl0[256];  // int4: group sums of the tile rows (each wave loads all; [0, kBM) used)
   __shared__ float xsl1[256];
   __shared__ int srcl[kBM];
-  __shared__ float hpart[4][kBM];
+  __shared__ float hpart[kWaves][kBM];
   __shared__ float xtot_l[kBM];
 
   // XCD-aware work order: workgroup b runs on XCD b % 8, so XCD x takes the
@@ -108,24 +109,25 @@ __global__ void __launch_bounds__(256, 2) gemm2_kernel(GemmArgs a, int n_slabs) 
 #pragma unroll
   for (int r = 0; r < kRT; ++r) {
     if (PHASE == PHASE_GATE_UP)
-      wrow[r] = (r < 2 ? 0 : a.I) + slab * 128 + wave * 32 + (r & 1) * 16;
+      wrow[r] = (r < kRT / 2 ? 0 : a.I) + slab * 128 + wave * (128 / kWaves) + (r % (kRT / 2)) * 16;
     else
-      wrow[r] = slab * 256 + wave * 64 + r * 16;
+      wrow[r] = slab * 256 + wave * (256 / kWaves) + r * 16;
     const uint32_t rb = (uint32_t)(wrow[r] >> 4);
     woff[r] = rb * (uint32_t)NKB * 1024u + (uint32_t)lane * 16u;
     soff[r] = rb * (uint32_t)G * 16u + 4u * (uint32_t)(lane >> 4);
   }
 
-  // ---- token-tile staging: 4 x 16 B per thread per group ------------------
+  // ---- token-tile staging: 16 / kWaves x 16 B per thread per group --------
   // A group's tile (kBM rows x 256 B) is stored in LDS unpadded with the
   // 16-byte chunks of row r XOR-swizzled by (r & 15), so the MFMA operand
   // reads below hit 16 distinct bank quads.  Pass i of thread t covers row
-  // r = 16 i + t / 16, chunk t % 16.
+  // r = 4 kWaves i + t / 16, chunk t % 16 (so r & 15 = (t / 16) & 15).
   const uint8_t* inb = (const uint8_t*)a.in;
-  constexpr int NST = kBM / 16;
+  constexpr int NST = kBM / (4 * kWaves);
   uint32_t boff[NST];
 #pragma unroll
-  for (int i = 0; i < NST; ++i) boff[i] = (uint32_t)srcl[i * 16 + (tid >> 4)] * (uint32_t)a.K * 2u + (tid & 15) * 16u;
+  for (int i = 0; i < NST; ++i)
+    boff[i] = (uint32_t)srcl[i * 4 * kWaves + (tid >> 4)] * (uint32_t)a.K * 2u + (tid & 15) * 16u;
   const int xs_src = tid < kBM ? srcl[tid] : 0;
   auto load_b = [&](u32x4(&st)[NST], float& xsv, int g) {
 #pragma unroll
@@ -135,12 +137,12 @@ __global__ void __launch_bounds__(256, 2) gemm2_kernel(GemmArgs a, int n_slabs) 
   auto store_b = [&](const u32x4(&st)[NST], float xsv, uint8_t* bt, float* xsl) {
 #pragma unroll
     for (int i = 0; i < NST; ++i) {
-      const int r = i * 16 + (tid >> 4);
+      const int r = i * 4 * kWaves + (tid >> 4);
       *(u32x4*)(bt + r * 256 + (((tid & 15) ^ (r & 15)) * 16)) = st[i];
     }
     if (WF == WF_I4 && tid < kBM) xsl[tid] = xsv;
   };
-  auto load_a = [&](ARegs<WF>& A, int g) {
+  auto load_a = [&](ARegs<WF, kRT>& A, int g) {
 #pragma unroll
     for (int r = 0; r < kRT; ++r) {
 #pragma unroll
@@ -155,7 +157,7 @@ __global__ void __launch_bounds__(256, 2) gemm2_kernel(GemmArgs a, int n_slabs) 
 #pragma unroll
     for (int c = 0; c < kCT; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](const ARegs<WF>& A, const uint8_t* bb, const float* xsl) {
+  auto compute = [&](const ARegs<WF, kRT>& A, const uint8_t* bb, const float* xsl) {
     if (WF == WF_I4) {
       // per-group scale: each (row tile, column tile) sums its 4 steps in a
       // temporary that starts at the offset correction, then is scaled in
@@ -219,7 +221,7 @@ __global__ void __launch_bounds__(256, 2) gemm2_kernel(GemmArgs a, int n_slabs) 
   // flight).  The loads are pinned above the MFMAs (the scheduler would sink
   // them to their use); past the last group they repeat it (no load behind a
   // branch).  The second workgroup on the CU computes while this one waits.
-  ARegs<WF> A0, A1;
+  ARegs<WF, kRT> A0, A1;
   u32x4 st[NST];
   float xsv = 0.f;
   load_b(st, xsv, 0);
@@ -263,13 +265,14 @@ __global__ void __launch_bounds__(256, 2) gemm2_kernel(GemmArgs a, int n_slabs) 
     }
   }
   if (PHASE == PHASE_GATE_UP) {
-    const int hcol0 = slab * 128 + wave * 32;
-    f32x4 sg[2], su[2];
+    const int hcol0 = slab * 128 + wave * (128 / kWaves);
+    constexpr int HR = kRT / 2;
+    f32x4 sg[HR], su[HR];
     if (WF == WF_I8) {
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
+      for (int r = 0; r < HR; ++r) {
         sg[r] = bf16x4_to_f32(*(const u32x2*)(sexp + wrow[r] + rq));
-        su[r] = bf16x4_to_f32(*(const u32x2*)(sexp + wrow[r + 2] + rq));
+        su[r] = bf16x4_to_f32(*(const u32x2*)(sexp + wrow[r + HR] + rq));
       }
     }
 #pragma unroll
@@ -277,8 +280,8 @@ __global__ void __launch_bounds__(256, 2) gemm2_kernel(GemmArgs a, int n_slabs) 
       const int pl = c * 16 + (lane & 15);
       float part = 0.f;
 #pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        f32x4 gv = acc[r][c], uv = acc[r + 2][c];
+      for (int r = 0; r < HR; ++r) {
+        f32x4 gv = acc[r][c], uv = acc[r + HR][c];
         if (WF == WF_I8) {
           gv *= sg[r];
           uv *= su[r];
@@ -301,7 +304,9 @@ __global__ void __launch_bounds__(256, 2) gemm2_kernel(GemmArgs a, int n_slabs) 
     if (a.hsum) {
       __syncthreads();
       if (tid < kBM && tid < rows) {
-        const float s = ((hpart[0][tid] + hpart[1][tid]) + hpart[2][tid]) + hpart[3][tid];
+        float s = hpart[0][tid];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) s += hpart[w][tid];
         a.hsum[(int64_t)(row0 + tid) * (a.I / 128) + slab] = s;
       }
     }
@@ -363,18 +368,25 @@ hipError_t launch_group_sums(const void* x, int rows, int K, float* out, hipStre
   return hipGetLastError();
 }
 
+// Waves per workgroup: int8 keeps 4 waves of 4 row tiles (its dequantised
+// fragments feed 4 column tiles each and its loop fits two workgroups per CU
+// without spills); bf16 and int4 take 8 waves of 2 row tiles, which halves
+// the weight registers a wave double-buffers (bf16 blocks hold 32 columns,
+// int4 adds per-group scale temporaries) and removes their spills.
+constexpr int gemm2_waves(int wf) { return wf == WF_I8 ? 4 : 8; }
+
 hipError_t launch_gemm2(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream,
                         const KernelTimer* tm) {
   if (max_tiles <= 0) return hipSuccess;
   const int n_slabs = phase == PHASE_GATE_UP ? a.I / 128 : a.N / 256;
   const int64_t items = (int64_t)n_slabs * max_tiles;
-  dim3 grid((unsigned)((items + kXcds - 1) / kXcds * kXcds)), block(256);
-#define NKT_G2(W)                                                                                  \
-  case W:                                                                                          \
-    if (phase == PHASE_GATE_UP)                                                                    \
-      launch_timed(gemm2_kernel<W, PHASE_GATE_UP>, grid, block, 0, stream, tm, a, n_slabs);        \
-    else                                                                                           \
-      launch_timed(gemm2_kernel<W, PHASE_DOWN>, grid, block, 0, stream, tm, a, n_slabs);           \
+  dim3 grid((unsigned)((items + kXcds - 1) / kXcds * kXcds)), block(64 * gemm2_waves(wf));
+#define NKT_G2(W)                                                                                          \
+  case W:                                                                                                  \
+    if (phase == PHASE_GATE_UP)                                                                            \
+      launch_timed(gemm2_kernel<W, PHASE_GATE_UP, gemm2_waves(W)>, grid, block, 0, stream, tm, a, n_slabs); \
+    else                                                                                                   \
+      launch_timed(gemm2_kernel<W, PHASE_DOWN, gemm2_waves(W)>, grid, block, 0, stream, tm, a, n_slabs);    \
     break;
   switch (wf) {
     NKT_G2(WF_BF16)
