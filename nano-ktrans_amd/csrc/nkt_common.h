@@ -100,14 +100,72 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return v;
 }
 
-// Inclusive prefix sum over the 64 lanes (Hillis-Steele).
-__device__ __forceinline__ int wave_inclusive_scan(int v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    int o = __shfl_up(v, off);
-    if (lane >= off) v += o;
+// ---------------------------------------------------------------------------
+// Lane moves without the LDS crossbar: DPP within 16-lane rows and the
+// gfx950 half / row swaps (a few cycles each instead of a ds_bpermute).
+// DPP controls used: row_shl:n = 0x100 + n (lane i reads lane i + n of its
+// row), row_shr:n = 0x110 + n (reads i - n), row_bcast:15 = 0x142 (lane 15
+// of each row to the next row), row_bcast:31 = 0x143 (lane 31 to rows 2, 3).
+// Lanes with no source lane, or in rows outside ROW_MASK, read 0.
+// ---------------------------------------------------------------------------
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, false);
+}
+
+// v(l) + v(l ^ 32) and v(l) + v(l ^ 16) in every lane (a swap of the wave's
+// halves / of neighbouring rows puts each lane's partner beside it).
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sum of the 64 lanes by the halving tree: level off = 32, 16, ..., 1 adds
+// lane l + off into lane l (l < off); the total of lane 0, as a uniform
+// value.  (The same order as wave_sum_butterfly's lane 0.)
+__device__ __forceinline__ float wave_sum_tree(float v) {
+  v = add_xor32(v);
+  v = add_xor16(v);
+  v = v + __uint_as_float(dpp_u32<0x108>(__float_as_uint(v)));
+  v = v + __uint_as_float(dpp_u32<0x104>(__float_as_uint(v)));
+  v = v + __uint_as_float(dpp_u32<0x102>(__float_as_uint(v)));
+  v = v + __uint_as_float(dpp_u32<0x101>(__float_as_uint(v)));
+  return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
+}
+
+// Maximum over the 64 lanes (fmaxf: NaN inputs are ignored unless all are
+// NaN), as a uniform value.
+__device__ __forceinline__ float wave_max_tree(float v) {
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
   }
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  }
+  // within the row: lanes past the row's end read 0, which only reaches
+  // lanes whose result is not used (lane 0 always reads real lanes)
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x108>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x104>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x102>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<0x101>(__float_as_uint(v))));
+  return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
+}
+
+// Inclusive prefix sum over the 64 lanes: shifted adds inside each row, then
+// the row totals carried across rows (row_bcast).
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  v += (int)dpp_u32<0x111>((uint32_t)v);
+  v += (int)dpp_u32<0x112>((uint32_t)v);
+  v += (int)dpp_u32<0x114>((uint32_t)v);
+  v += (int)dpp_u32<0x118>((uint32_t)v);
+  v += (int)dpp_u32<0x142, 0xa>((uint32_t)v);
+  v += (int)dpp_u32<0x143, 0xc>((uint32_t)v);
   return v;
 }
 

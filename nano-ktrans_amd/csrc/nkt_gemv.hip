@@ -161,6 +161,46 @@ __device__ __forceinline__ void mma_group(const WSlot<WF, NT>& r, const u32x4 (&
   }
 }
 
+// Output rows orow0 .. orow0 + 16 RT of the tile's positions: SwiGLU into h
+// (gate_up) or y / bf16 logits (down); int8 row scales applied here.
+template <int WF, int PHASE, int RT>
+__device__ __forceinline__ void gemv_epilogue(const GemmArgs& a, const f32x4 (&acc)[PHASE == PHASE_GATE_UP ? 2 * RT : RT],
+                                              int rows, int row0, int orow0, const uint16_t* sexp, uint32_t lane) {
+  const int t_out = lane & 15;
+  if (t_out >= rows) return;
+  const int64_t pos = row0 + t_out;
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    const int orow = orow0 + 16 * r + 4 * (lane >> 4);
+    f32x4 s0 = acc[r];
+    if (PHASE == PHASE_GATE_UP) {
+      f32x4 s1 = acc[RT + r];
+      if (WF == WF_I8) {
+        s0 *= bf16x4_to_f32(*(const u32x2*)(sexp + orow));
+        s1 *= bf16x4_to_f32(*(const u32x2*)(sexp + a.I + orow));
+      }
+      float h[4];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) h[v] = silu_f32(s0[v]) * s1[v];
+      u32x2 pk;
+      pk[0] = pack_bf16x2(h[0], h[1]);
+      pk[1] = pack_bf16x2(h[2], h[3]);
+      *(u32x2*)((uint16_t*)a.out + pos * a.I + orow) = pk;
+    } else {
+      if (WF == WF_I8) s0 *= bf16x4_to_f32(*(const u32x2*)(sexp + orow));
+      if (a.out_cols > 0) {
+        // bf16 [rows, out_cols] (router logits): columns past out_cols are padding
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (orow + v < a.out_cols)
+            ((uint16_t*)a.out)[pos * a.out_cols + orow + v] = (uint16_t)f32_to_bf16_bits(s0[v]);
+      } else {
+        *(f32x4*)((float*)a.out + pos * a.N + orow) = s0;
+      }
+    }
+  }
+}
+
 }  // namespace
 
 // Waves per workgroup: S K-parts of P row sets.
@@ -303,40 +343,7 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
     }
   }
   if (!rs_ok) return;
-
-  const int t_out = lane & 15;
-  if (t_out >= rows) return;
-  const int64_t pos = row0 + t_out;
-#pragma unroll
-  for (int r = 0; r < RT; ++r) {
-    const int orow = orow0 + 16 * r + 4 * (lane >> 4);
-    f32x4 s0 = acc[r];
-    if (PHASE == PHASE_GATE_UP) {
-      f32x4 s1 = acc[RT + r];
-      if (WF == WF_I8) {
-        s0 *= bf16x4_to_f32(*(const u32x2*)(sexp + orow));
-        s1 *= bf16x4_to_f32(*(const u32x2*)(sexp + a.I + orow));
-      }
-      float h[4];
-#pragma unroll
-      for (int v = 0; v < 4; ++v) h[v] = silu_f32(s0[v]) * s1[v];
-      u32x2 pk;
-      pk[0] = pack_bf16x2(h[0], h[1]);
-      pk[1] = pack_bf16x2(h[2], h[3]);
-      *(u32x2*)((uint16_t*)a.out + pos * a.I + orow) = pk;
-    } else {
-      if (WF == WF_I8) s0 *= bf16x4_to_f32(*(const u32x2*)(sexp + orow));
-      if (a.out_cols > 0) {
-        // bf16 [rows, out_cols] (router logits): columns past out_cols are padding
-#pragma unroll
-        for (int v = 0; v < 4; ++v)
-          if (orow + v < a.out_cols)
-            ((uint16_t*)a.out)[pos * a.out_cols + orow + v] = (uint16_t)f32_to_bf16_bits(s0[v]);
-      } else {
-        *(f32x4*)((float*)a.out + pos * a.N + orow) = s0;
-      }
-    }
-  }
+  gemv_epilogue<WF, PHASE, RT>(a, acc, rows, row0, orow0, sexp, lane);
 }
 
 // ---------------------------------------------------------------------------

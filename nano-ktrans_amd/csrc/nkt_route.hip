@@ -46,6 +46,13 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
 
 __device__ __forceinline__ uint64_t ballot64(bool p) { return __ballot(p); }
 
+// LDS writes of this wave visible to its other lanes (no workgroup barrier)
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Route one token with the whole wavefront.  sv/si: this wave's 16-entry LDS
 // scratch (selected values / ids in slot order).  Returns, in lanes < k, the
 // slot's expert id and weight; lanes >= k return id -1.
@@ -77,7 +84,7 @@ __device__ __forceinline__ void route_token(const void* __restrict__ logits, int
     float m = v[0];
 #pragma unroll
     for (int j = 1; j < VPL; ++j) m = (v[j] > m) ? v[j] : m;
-    m = wave_max(m);
+    m = wave_max_tree(m);
     float ex[VPL];
     float part = 0.0f;
 #pragma unroll
@@ -85,7 +92,7 @@ __device__ __forceinline__ void route_token(const void* __restrict__ logits, int
       ex[j] = valid[j] ? route_expf(v[j] - m) : 0.0f;
       part = (j == 0) ? ex[j] : part + ex[j];
     }
-    const float s = wave_sum_butterfly(part);
+    const float s = wave_sum_tree(part);
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
       float p = ex[j] / s;
@@ -126,55 +133,53 @@ __device__ __forceinline__ void route_token(const void* __restrict__ logits, int
     eq_before += __popcll(m);
   }
 
-  // ---- slot = rank under (value desc, id asc) among the selected ---------
-  int rank[VPL];
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) rank[j] = 0;
-#pragma unroll
-  for (int j2 = 0; j2 < VPL; ++j2) {
-    uint64_t m = ballot64(sel[j2]);
-    while (m) {
-      const int ln = __builtin_ctzll(m);
-      m &= m - 1;
-      const uint32_t ks = (uint32_t)__builtin_amdgcn_readlane((int)key[j2], ln);
-      const int is = ln + 64 * j2;
-#pragma unroll
-      for (int j = 0; j < VPL; ++j) {
-        const int id = lane + 64 * j;
-        rank[j] += (ks > key[j] || (ks == key[j] && is < id)) ? 1 : 0;
-      }
-    }
-  }
+  // ---- the k selected elements into lanes 0..k-1, ascending id ----------
+  int before = 0;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
+    const uint64_t m = ballot64(sel[j]);
     if (sel[j]) {
-      sv[rank[j]] = v[j];
-      si[rank[j]] = lane + 64 * j;
+      const int c = before + lanes_below(m);
+      sv[c] = v[j];
+      si[c] = lane + 64 * j;
     }
+    before += __popcll(m);
   }
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  wave_lds_sync();
+  const bool slot_lane = lane < k;
+  const float cv = slot_lane ? sv[lane] : 0.0f;
+  const int cid = slot_lane ? si[lane] : -1;
+  const uint32_t ck = ordered_bits(cv);
+  wave_lds_sync();  // every lane has read its element before the slots are rewritten
 
-  // ---- weights, k-way sums in slot order ---------------------------------
-  float s = 0.0f;
-  float m0 = sv[0];
-  if (use_softmax) {
-    if (renorm) {
-      for (int jj = 0; jj < k; ++jj) s = (jj == 0) ? sv[0] : s + sv[jj];
-      if (BF16) s = bf16_round(s);
-    }
-  } else {
-    for (int jj = 0; jj < k; ++jj) {
-      const float e = route_expf(sv[jj] - m0);
-      s = (jj == 0) ? e : s + e;
-    }
+  // ---- slot = rank under (value desc, id asc); lanes are in id order, so an
+  // equal key ranks first exactly when it sits in a lower lane
+  int rank = 0;
+  for (int j = 0; j < k; ++j) {
+    const uint32_t kj = (uint32_t)__builtin_amdgcn_readlane((int)ck, j);
+    rank += (kj > ck || (kj == ck && j < lane)) ? 1 : 0;
+  }
+  if (slot_lane) {
+    sv[rank] = cv;
+    si[rank] = cid;
+  }
+  wave_lds_sync();
+  const float val = slot_lane ? sv[lane] : 0.0f;  // slot order from here on
+  const int sid = slot_lane ? si[lane] : -1;
+
+  // ---- weights, k-way sums in slot order (uniform, from lane reads) -------
+  const float m0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(val), 0));
+  const float e = (!use_softmax && slot_lane) ? route_expf(val - m0) : 0.0f;
+  const float term = use_softmax ? val : e;
+  float s = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(term), 0));
+  if (!use_softmax || renorm) {
+    for (int jj = 1; jj < k; ++jj) s = s + __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(term), jj));
+    if (use_softmax && BF16) s = bf16_round(s);
   }
   int id = -1;
   float w = 0.0f;
-  if (lane < k) {
-    id = si[lane];
-    const float val = sv[lane];
+  if (slot_lane) {
+    id = sid;
     if (use_softmax) {
       w = val;
       if (renorm) {
@@ -182,7 +187,7 @@ __device__ __forceinline__ void route_token(const void* __restrict__ logits, int
         w = BF16 ? bf16_round(q) : q;
       }
     } else {
-      const float q = route_expf(val - m0) / s;
+      const float q = e / s;
       w = BF16 ? bf16_round(q) : q;
     }
   }
@@ -212,149 +217,155 @@ __global__ void __launch_bounds__(256) route_kernel(const void* __restrict__ log
 }
 
 // ---------------------------------------------------------------------------
-// K2 body: one workgroup of 16 waves groups the P = T*k pairs whose expert
-// ids sit in ids (global or LDS).  Wave w owns a contiguous range of pairs (in
-// pair order = token order).  Pass 1 counts per (wave, expert); a column scan
-// gives each wave its starting slot inside every expert's segment; pass 2
-// walks the range 64 pairs at a time and ranks equal experts inside the chunk
-// with ballots, so the permutation is stable in token order and independent
-// of scheduling.  Then the tile list: (expert, first position, rows) for
-// every BM-row slice of every expert's segment, experts ascending.
+// K2 for small batches: one workgroup of 16 waves groups the P = T*k pairs
+// (P <= kFusedRouteMaxPairs) whose expert ids sit in LDS.  Thread t owns
+// (expert e, part q) = (t / NP, t % NP): the pairs are cut into NP equal
+// consecutive parts and the thread counts the pairs of its part that go to
+// its expert.  An expert's NP counts sit in neighbouring lanes, so its total
+// takes a few DPP adds; one workgroup prefix sum over the threads, in
+// (expert, part) order, of count | tiles << 16 then gives every thread the
+// first position of its pairs inside the expert's segment and every expert
+// its first tile.  A second walk over the part writes perm / inv / tile
+// sources in pair order (stable in token order, independent of scheduling);
+// the expert's lanes write its tile records.  Two workgroup barriers in all.
 // ---------------------------------------------------------------------------
 constexpr int kGroupWaves = 16;
+constexpr int kGroupThreads = 64 * kGroupWaves;
 
-struct GroupLds {
-  int32_t hist[kGroupWaves][kMaxExperts];
-  int32_t tot[kMaxExperts];
-  int32_t off_s[kMaxExperts + 1];
-  int32_t tile_off[kMaxExperts + 1];
-};
+// parts per expert: NP lanes of one expert share a 16-lane row
+__host__ __device__ constexpr int group_parts(int E) {
+  int epad = 1;
+  while (epad < E) epad <<= 1;
+  const int np = kGroupThreads / epad;
+  return np < 16 ? np : 16;
+}
 
-__device__ __forceinline__ void group_body(const int32_t* ids, int T, int k, int E, int bm,
-                                           int max_tiles, int32_t* __restrict__ counts,
-                                           int32_t* __restrict__ offsets,
-                                           int32_t* __restrict__ perm, int32_t* __restrict__ inv,
-                                           int32_t* __restrict__ tiles,
-                                           int32_t* __restrict__ n_tiles,
-                                           int32_t* __restrict__ tile_src,
-                                           const uint8_t* __restrict__ resident, GroupLds& L) {
+// Sum over the aligned group of NP (1, 2, 4, 8 or 16) neighbouring lanes,
+// in every lane of the group.
+__device__ __forceinline__ int group_lane_sum(int v, int np) {
+  if (np >= 2) v += (int)dpp_u32<0xB1>((uint32_t)v);   // quad_perm [1,0,3,2]: lane ^ 1
+  if (np >= 4) v += (int)dpp_u32<0x4E>((uint32_t)v);   // quad_perm [2,3,0,1]: lane ^ 2
+  if (np >= 8) v += (int)dpp_u32<0x141>((uint32_t)v);  // row_half_mirror: the other quad
+  if (np >= 16) v += (int)dpp_u32<0x140>((uint32_t)v); // row_mirror: the other half row
+  return v;
+}
+
+// Bit i of the result: pair p + i (i < n <= 64) goes to expert e.
+__device__ __forceinline__ uint64_t pair_match_mask(const int32_t* ids, int p, int n, int e) {
+  uint32_t lo = 0, hi = 0;
+  for (int i = 0; i < n; i += 4) {
+    const int4 g = *(const int4*)(ids + p + i);
+    const uint32_t b = (uint32_t)(g.x == e) | ((uint32_t)(g.y == e) << 1) | ((uint32_t)(g.z == e) << 2) |
+                       ((uint32_t)(g.w == e) << 3);
+    if (i < 32)
+      lo |= b << i;
+    else
+      hi |= b << (i - 32);
+  }
+  const uint64_t m = ((uint64_t)hi << 32) | lo;
+  return n >= 64 ? m : m & ((1ull << n) - 1);
+}
+
+// ids: LDS, 16-byte aligned, at least P rounded up to 4 entries readable.
+// res_ok: this thread's expert is HBM-resident (loaded by the caller early).
+// bm: a power of two (kTileSrcCols when tile_src is given).
+__device__ __forceinline__ void group_small(const int32_t* ids, int T, int k, int E, int bm,
+                                            int max_tiles, bool res_ok, int32_t* __restrict__ counts,
+                                            int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
+                                            int32_t* __restrict__ inv, int32_t* __restrict__ tiles,
+                                            int32_t* __restrict__ n_tiles, int32_t* __restrict__ tile_src,
+                                            int32_t* wave_tot) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int P = T * k;
-  int ppw = (P + kGroupWaves - 1) / kGroupWaves;
-  ppw = (ppw + 63) & ~63;
-  const int pbeg = min(P, wave * ppw);
-  const int pend = min(P, pbeg + ppw);
+  const int np = group_parts(E);  // a power of two
+  const int lg_np = __builtin_ctz(np);
+  const int e = tid >> lg_np;
+  const int q = tid & (np - 1);
+  const bool own = e < E;
+  const int chunk = (((P + np - 1) >> lg_np) + 3) & ~3;
+  const int pb = min(P, q * chunk);
+  const int pe = min(P, pb + chunk);
 
-  for (int i = tid; i < kGroupWaves * kMaxExperts; i += blockDim.x) (&L.hist[0][0])[i] = 0;
-  __syncthreads();
-
-  for (int p = pbeg + lane; p < pend; p += 64) {
-    const int e = ids[p];
-    if (e >= 0 && e < E) atomicAdd(&L.hist[wave][e], 1);
-  }
-  __syncthreads();
-
-  // column scan over waves -> per-wave start inside each expert
-  if (tid < E) {
-    int run = 0;
-    for (int w = 0; w < kGroupWaves; ++w) {
-      const int h = L.hist[w][tid];
-      L.hist[w][tid] = run;
-      run += h;
+  // pass 1: pairs of this part that go to e, as bit masks of 64-pair windows
+  // (the first window's mask is kept for pass 2)
+  int cnt = 0;
+  uint64_t m_first = 0;
+  if (own) {
+    for (int p = pb; p < pe; p += 64) {
+      const uint64_t m = pair_match_mask(ids, p, min(64, pe - p), e);
+      if (p == pb) m_first = m;
+      cnt += __popcll(m);
     }
-    L.tot[tid] = run;
   }
-  __syncthreads();
+  const int tot = group_lane_sum(cnt, np);
+  const int nt = (own && res_ok) ? (tot + bm - 1) >> __builtin_ctz(bm) : 0;  // non-resident: no tiles
 
-  // exclusive scans over experts (wave 0, 4 experts per lane): positions and
-  // tiles (experts that are not HBM-resident get no tiles)
-  if (wave == 0) {
-    int local[4], tl[4];
-    int sum = 0, tsum = 0;
+  // workgroup exclusive prefix of (pairs | tiles << 16) in (expert, part) order
+  const int val = own ? (cnt | ((q == 0 ? nt : 0) << 16)) : 0;
+  const int incl = wave_inclusive_scan(val);
+  if (lane == 63) wave_tot[wave] = incl;
+  __syncthreads();
+  int base = 0, total = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = lane * 4 + i;
-      local[i] = (e < E) ? L.tot[e] : 0;
-      tl[i] = (e < E && (!resident || resident[e])) ? (local[i] + bm - 1) / bm : 0;
-      sum += local[i];
-      tsum += tl[i];
-    }
-    const int incl = wave_inclusive_scan(sum);
-    const int tincl = wave_inclusive_scan(tsum);
-    int run = incl - sum, trun = tincl - tsum;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = lane * 4 + i;
-      if (e < E) {
-        L.off_s[e] = run;
-        L.tile_off[e] = trun;
-      }
-      run += local[i];
-      trun += tl[i];
-    }
-    if (lane == 63) {
-      L.off_s[E] = incl;
-      L.tile_off[E] = tincl;
-    }
+  for (int w = 0; w < kGroupWaves; ++w) {
+    const int x = wave_tot[w];
+    base += (w < wave) ? x : 0;
+    total += x;
   }
-  __syncthreads();
+  const int excl = base + incl - val;
+  const int pos0 = excl & 0xffff;                      // first position of this part's pairs
+  const int off_e = __shfl(pos0, lane & ~(np - 1));    // the expert's first position
+  const int toff_e = (excl >> 16) - (q > 0 ? nt : 0);  // the expert's first tile
+  const int n_pairs = total & 0xffff;
+  const int n_tile_all = total >> 16;
 
-  if (tid < E) {
-    counts[tid] = L.tot[tid];
-    offsets[tid] = L.off_s[tid];
-    for (int w = 0; w < kGroupWaves; ++w) L.hist[w][tid] += L.off_s[tid];
-  }
-  if (tid == 0) offsets[E] = L.off_s[E];
-  __syncthreads();
-
-  int nbits = 1;
-  while ((1 << nbits) < E) ++nbits;
-  for (int base = pbeg; base < pend; base += 64) {
-    const int p = base + lane;
-    const bool valid = p < pend;
-    const int e = valid ? ids[p] : 0;
-    const bool ok = valid && e >= 0 && e < E;
-    uint64_t same = __ballot(ok);
-    for (int b = 0; b < nbits; ++b) {
-      const bool bit = (e >> b) & 1;
-      const uint64_t bb = __ballot(ok && bit);
-      same &= bit ? bb : ~bb;
-    }
-    if (ok) {
-      const int rank = lanes_below(same);
-      const int cnt = __popcll(same);
-      const int pos = L.hist[wave][e] + rank;
-      perm[pos] = p;
-      inv[p] = pos;
-      if (tile_src && (!resident || resident[e])) {
-        const int rel = pos - L.off_s[e];
-        const int ti = L.tile_off[e] + rel / bm;
-        if (ti < max_tiles) tile_src[ti * kTileSrcCols + rel % bm] = p / k;
+  // pass 2: positions in pair order, one iteration per matching pair; the
+  // token of pair p is p / k = (p * ceil(2^32 / k)) >> 32 (exact for p < 2^16)
+  if (cnt > 0) {
+    const uint64_t kmagic = ((1ull << 32) + (uint64_t)k - 1) / (uint64_t)k;
+    int pos = pos0;
+    for (int p = pb; p < pe; p += 64) {
+      uint64_t m = (p == pb) ? m_first : pair_match_mask(ids, p, min(64, pe - p), e);
+      while (m) {
+        const int pp = p + __builtin_ctzll(m);
+        m &= m - 1;
+        perm[pos] = pp;
+        inv[pp] = pos;
+        if (tile_src && nt > 0) {
+          const int rel = pos - off_e;
+          const int ti = toff_e + rel / kTileSrcCols;
+          if (ti < max_tiles) tile_src[ti * kTileSrcCols + rel % kTileSrcCols] = (int)(((uint64_t)pp * kmagic) >> 32);
+        }
+        ++pos;
       }
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): every lane has read its start
-      if (rank == cnt - 1) L.hist[wave][e] += cnt;
     }
   }
 
-  // tile list for the grouped GEMMs: (expert, first position, rows); lane
-  // group lane/16 takes a tile, its 16 lanes the tile's source-row padding
-  for (int e = wave; e < E; e += kGroupWaves) {
-    const int c = L.tot[e];
-    const int nt = (!resident || resident[e]) ? (c + bm - 1) / bm : 0;
-    for (int m = lane >> 4; m < nt; m += 4) {
-      const int ti = L.tile_off[e] + m;
-      if (ti < max_tiles) {
-        const int rows = min(bm, c - m * bm);
-        if ((lane & 15) == 0) *(int4*)(tiles + 4 * ti) = int4{e, L.off_s[e] + m * bm, rows, 0};
-        if (tile_src && (lane & 15) >= rows) tile_src[ti * kTileSrcCols + (lane & 15)] = 0;
-      }
+  // the expert's tile records (expert, first position, rows); its lanes pad
+  // the unused source columns of every tile
+  if (own) {
+    if (q == 0) {
+      counts[e] = tot;
+      offsets[e] = off_e;
     }
+    for (int m = 0; m < nt; ++m) {
+      const int ti = toff_e + m;
+      if (ti >= max_tiles) break;
+      const int rows = min(bm, tot - m * bm);
+      if (q == 0) *(int4*)(tiles + 4 * ti) = int4{e, off_e + m * bm, rows, 0};
+      if (tile_src)
+        for (int c = q; c < kTileSrcCols; c += np)
+          if (c >= rows) tile_src[ti * kTileSrcCols + c] = 0;
+    }
+  }
+  if (tid == 0) {
+    offsets[E] = n_pairs;
+    n_tiles[0] = min(n_tile_all, max_tiles);
   }
   // records past the last tile say "no rows" (the decode form reads every record up to max_tiles)
-  for (int ti = L.tile_off[E] + tid; ti < max_tiles; ti += blockDim.x) *(int4*)(tiles + 4 * ti) = int4{0, 0, 0, 0};
-  if (tid == 0) n_tiles[0] = min(L.tile_off[E], max_tiles);
+  for (int ti = n_tile_all + tid; ti < max_tiles; ti += kGroupThreads) *(int4*)(tiles + 4 * ti) = int4{0, 0, 0, 0};
 }
 
 // ---------------------------------------------------------------------------
@@ -538,18 +549,21 @@ hipError_t launch_group_multi(const int32_t* ids, int T, int k, int E, int bm, i
 // Route and group in one workgroup of 16 waves (small batches): wave w routes
 // tokens w, w + 16, ...; the ids stay in LDS for the grouping.
 template <int VPL, bool BF16>
-__global__ void __launch_bounds__(1024) route_group_kernel(
+__global__ void __launch_bounds__(kGroupThreads) route_group_kernel(
     const void* __restrict__ logits, int T, int E, int k, unsigned flags, int bm, int max_tiles,
     int32_t* __restrict__ ids_out, float* __restrict__ w_out, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ inv,
     int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles, int32_t* __restrict__ tile_src,
     const uint8_t* __restrict__ resident) {
-  __shared__ GroupLds L;
-  __shared__ int32_t ids_s[kFusedRouteMaxPairs];
+  __shared__ __attribute__((aligned(16))) int32_t ids_s[kFusedRouteMaxPairs];
+  __shared__ int32_t wave_tot[kGroupWaves];
   __shared__ float sv[kGroupWaves][kMaxTopK];
   __shared__ int si[kGroupWaves][kMaxTopK];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
+  // the grouping thread's residency flag, read before routing so its latency hides
+  const int ge = threadIdx.x / group_parts(E);
+  const bool res_ok = !resident || (ge < E && resident[ge]);
   for (int t = wave; t < T; t += kGroupWaves) {
     int id;
     float w;
@@ -561,7 +575,8 @@ __global__ void __launch_bounds__(1024) route_group_kernel(
     }
   }
   __syncthreads();
-  group_body(ids_s, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, tile_src, resident, L);
+  group_small(ids_s, T, k, E, bm, max_tiles, res_ok, counts, offsets, perm, inv, tiles, n_tiles, tile_src,
+              wave_tot);
 }
 
 #define NKT_VPL_SWITCH(E, CASE) \
@@ -601,6 +616,7 @@ hipError_t launch_route_group(const void* logits, int act_bf16, int T, int E, in
                               const uint8_t* resident, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
   if (!route_group_fused(T, k)) return hipErrorInvalidValue;
+  if (bm <= 0 || (bm & (bm - 1)) != 0) return hipErrorInvalidValue;
   if (tile_src && bm != kTileSrcCols) return hipErrorInvalidValue;
   dim3 grid(1), block(64 * kGroupWaves);
 #define NKT_RG_CASE(V)                                                                          \
