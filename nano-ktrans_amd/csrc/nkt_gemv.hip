@@ -87,47 +87,88 @@ __device__ __forceinline__ float group_sum_full(const u32x4 (&x)[4]) {
       xs += __uint_as_float(x[s][h] << 16);
       xs += __uint_as_float(x[s][h] & 0xffff0000u);
     }
-  xs += __shfl_xor(xs, 16);
-  xs += __shfl_xor(xs, 32);
-  return xs;
+  xs = add_xor16(xs);
+  return add_xor32(xs);
 }
 
-// Single-position tiles (most decode tiles) load their activations compactly:
-// lane j = l%16 of row q = l/16 loads chunk s = j%4, i.e.
-// x[row][128g + 32s + 8q .. +7] (lanes j >= 4 repeat j%4).  DPP row_newbcast:s
-// copies lane s of every 16-lane row to the whole row, which is exactly the B
-// operand of step s: one load and 16 lane moves in place of four loads.
-template <int N>
-__device__ __forceinline__ uint32_t row_bcast(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x150 + N, 0xf, 0xf, false);
+// Tiles of at most four positions (almost every decode tile) load their
+// activations compactly, one 16-byte load per lane per group: lane (q, j) =
+// (l / 16, l % 16) holds x[row j % 4][128g + 32 (j / 4) + 8q .. +7].  The B
+// operand of step s needs, in lane (q, c), x[row c][128g + 32s + 8q ..], held
+// by lane (q, 4s + c) of the same row: a DPP row_shl by 4s.  Only columns
+// c < 4 carry data; the others hold copies of other rows and their outputs are
+// never stored (rows past the tile's count are padding).
+__device__ __forceinline__ u32x4 quad_operand(u32x4 xq, int s) {
+  switch (s) {
+    case 1:
+      return u32x4{dpp_u32<0x104>(xq[0]), dpp_u32<0x104>(xq[1]), dpp_u32<0x104>(xq[2]), dpp_u32<0x104>(xq[3])};
+    case 2:
+      return u32x4{dpp_u32<0x108>(xq[0]), dpp_u32<0x108>(xq[1]), dpp_u32<0x108>(xq[2]), dpp_u32<0x108>(xq[3])};
+    case 3:
+      return u32x4{dpp_u32<0x10C>(xq[0]), dpp_u32<0x10C>(xq[1]), dpp_u32<0x10C>(xq[2]), dpp_u32<0x10C>(xq[3])};
+    default:
+      return xq;
+  }
 }
 
-template <int N>
-__device__ __forceinline__ u32x4 row_bcast4(u32x4 v) {
-  return u32x4{row_bcast<N>(v[0]), row_bcast<N>(v[1]), row_bcast<N>(v[2]), row_bcast<N>(v[3])};
-}
-
-__device__ __forceinline__ void single_operands(u32x4 xc, u32x4 (&xb)[4]) {
-  xb[0] = row_bcast4<0>(xc);
-  xb[1] = row_bcast4<1>(xc);
-  xb[2] = row_bcast4<2>(xc);
-  xb[3] = row_bcast4<3>(xc);
-}
-
-// Group sum of a single-position load: the 16 distinct chunks sit in lanes
-// (j%4, q); every lane ends with the total.
-__device__ __forceinline__ float single_group_sum(u32x4 xc) {
+// Group sum of a quad-form load: lanes c < 4 of every row end with the sum of
+// the group's 128 activations of column c.
+__device__ __forceinline__ float quad_group_sum(u32x4 xq) {
   float v = 0.f;
 #pragma unroll
   for (int h = 0; h < 4; ++h) {
-    v += __uint_as_float(xc[h] << 16);
-    v += __uint_as_float(xc[h] & 0xffff0000u);
+    v += __uint_as_float(xq[h] << 16);
+    v += __uint_as_float(xq[h] & 0xffff0000u);
   }
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  v = v + __uint_as_float(dpp_u32<0x108>(__float_as_uint(v)));  // + lane c + 8
+  v = v + __uint_as_float(dpp_u32<0x104>(__float_as_uint(v)));  // + lanes c + 4, c + 12
+  v = add_xor16(v);
+  return add_xor32(v);
+}
+
+// A operand of tile t, step s.
+template <int WF, int NT>
+__device__ __forceinline__ u32x4 a_operand(const WSlot<WF, NT>& r, int t, int s) {
+  if (WF == WF_I4) return dq_i4(r.w[t][0][s]);
+  if (WF == WF_I8) return dq_i8(r.w[t][s >> 1][2 * (s & 1)], r.w[t][s >> 1][2 * (s & 1) + 1]);
+  return r.w[t][s];
+}
+
+// Marks the slot's registers as redefined here: dequantisation that both
+// activation forms share stays inside each form's branch instead of being
+// hoisted above it with every group's operands live at once.
+template <int WF, int NT>
+__device__ __forceinline__ void pin_slot(WSlot<WF, NT>& r) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int i = 0; i < WSlot<WF, NT>::NBLK; ++i) __asm__ volatile("" : "+v"(r.w[t][i]));
+  if (WF == WF_I4)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) __asm__ volatile("" : "+v"(r.s[t]));
+}
+
+// One group of a quad-form tile: the B operand of each step is built once and
+// feeds the NT tiles.  use == false computes and adds nothing.
+template <int WF, int NT>
+__device__ __forceinline__ void mma_group_quad(const WSlot<WF, NT>& r, u32x4 xq, float xs, f32x4 (&acc)[NT],
+                                               bool use) {
+  const float c = WF == WF_I4 ? -136.0f * xs : WF == WF_I8 ? -128.0f * xs : 0.0f;
+  f32x4 tmp[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) tmp[t] = f32x4{c, c, c, c};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const u32x4 b = quad_operand(xq, s);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) tmp[t] = mfma_bf16(a_operand<WF, NT>(r, t, s), b, tmp[t]);
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    if (WF == WF_I4) tmp[t] = bf16x4_to_f32(r.s[t]) * tmp[t];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[t][v] = use ? acc[t][v] + tmp[t][v] : acc[t][v];
+  }
 }
 
 // Adds one group's contribution to acc; use == false computes it and adds
@@ -221,8 +262,11 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
   const int col = lane & 15;
   // the input row of the lane's column comes straight from the tile index, so
   // this load is issued first and waiting for it never waits for weights
-  int src = 0;
-  if (a.tile_src) src = a.tile_src[tile * kTileSrcCols + col];
+  int src = 0, srcq = 0;
+  if (a.tile_src) {
+    src = a.tile_src[tile * kTileSrcCols + col];
+    srcq = a.tile_src[tile * kTileSrcCols + (col & 3)];
+  }
 
   const int wave = threadIdx.x >> 6;
   const int kpart = wave % S;
@@ -246,7 +290,10 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
     rows = min(16, a.num_rows - row0);
   }
   if (rows <= 0) return;
-  if (!a.tile_src) src = row0 + (col < rows ? col : 0);  // rows read in place
+  if (!a.tile_src) {  // rows read in place
+    src = row0 + (col < rows ? col : 0);
+    srcq = row0 + ((col & 3) < rows ? (col & 3) : 0);
+  }
   const uint8_t* xbase = (const uint8_t*)a.in + 16 * (lane >> 4);
 
   const uint8_t* wexp = a.w + (int64_t)expert * a.w_expert_bytes;
@@ -278,32 +325,30 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
 #pragma unroll
     for (int i = 0; i < NG; ++i) load_w<WF, NT>(sl[i], wexp, sexp, rbo, sbo, g_base + S * min(i, n_last), lane);
     __builtin_amdgcn_sched_barrier(0);
-    // the B operands and group sums of the wave's groups; only these differ
-    // between the two activation forms (the weight math after the branch is
-    // shared, so nothing that waits for weights is hoisted above it)
-    u32x4 xb[NG > 0 ? NG : 1][4];
-    float xs[NG > 0 ? NG : 1];
-    if (rows == 1) {
-      const uint8_t* xtok = xbase + (int64_t)__builtin_amdgcn_readlane(src, 0) * a.K * 2 + 64 * (lane & 3);
-      u32x4 xc[NG > 0 ? NG : 1];
+    if (rows <= 4) {
+      // quad form: one load per group, the B operands built per step
+      const uint8_t* xq_row = (const uint8_t*)a.in + (int64_t)srcq * a.K * 2 + 64 * (col >> 2) + 16 * (lane >> 4);
+      u32x4 xq[NG > 0 ? NG : 1];
 #pragma unroll
-      for (int i = 0; i < NG; ++i) xc[i] = *(const u32x4*)(xtok + (g_base + S * min(i, n_last)) * 256);
+      for (int i = 0; i < NG; ++i) xq[i] = *(const u32x4*)(xq_row + (g_base + S * min(i, n_last)) * 256);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < NG; ++i) {
-        single_operands(xc[i], xb[i]);
-        xs[i] = IS_INT ? single_group_sum(xc[i]) : 0.f;
+        pin_slot<WF, NT>(sl[i]);
+        mma_group_quad<WF, NT>(sl[i], xq[i], IS_INT ? quad_group_sum(xq[i]) : 0.f, acc, i < n);
       }
     } else {
+      // larger tiles: full B operands, one group's at a time (few registers)
       const uint8_t* xrow = xbase + (int64_t)src * a.K * 2;
 #pragma unroll
-      for (int i = 0; i < NG; ++i) load_x_full(xb[i], xrow, g_base + S * min(i, n_last));
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < NG; ++i) xs[i] = IS_INT ? group_sum_full(xb[i]) : 0.f;
+      for (int i = 0; i < NG; ++i) {
+        u32x4 xb[4];
+        load_x_full(xb, xrow, g_base + S * min(i, n_last));
+        pin_slot<WF, NT>(sl[i]);
+        mma_group<WF, NT>(sl[i], xb, IS_INT ? group_sum_full(xb) : 0.f, acc, i < n);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-#pragma unroll
-    for (int i = 0; i < NG; ++i) mma_group<WF, NT>(sl[i], xb[i], xs[i], acc, i < n);
   } else {
     const uint8_t* xrow = xbase + (int64_t)src * a.K * 2;
     RSlot<WF, NT> ring[D];
@@ -361,26 +406,56 @@ hipError_t launch_gemv_s(const GemmArgs& a, int max_tiles, int n_rowsets, hipStr
   return hipGetLastError();
 }
 
-// Every wave takes kGemvGroupsPerWave K groups, all loads in flight at once
-// (many short waves stream HBM better than few long ones); K too long for
-// eight such waves streams through the ring instead.
-constexpr int kGemvGroupsPerWave = 2;
+// Every wave takes NG K groups and issues all of their loads at once (many
+// short waves stream HBM better than few long ones): about 8 KiB of weights
+// per wave, i.e. a target of 4 groups of int4 and 2 of int8 or bf16 for two
+// row tiles.  The S = ceil(G / target) K parts (at most 8) then split the G
+// groups as evenly as they go, NG = ceil(G / S) each; K too long for eight
+// parts of four groups streams through the ring instead.
+__host__ __device__ constexpr int gemv_target_groups(int wf) { return wf == WF_I4 ? 4 : 2; }
+
+template <int WF, int PHASE, int RT, int NG>
+hipError_t launch_gemv_ng(const GemmArgs& a, int S, int max_tiles, int n_rowsets, hipStream_t stream,
+                          const KernelTimer* tm) {
+  switch (S) {
+    case 1:
+      return launch_gemv_s<WF, PHASE, RT, 1, NG>(a, max_tiles, n_rowsets, stream, tm);
+    case 2:
+      return launch_gemv_s<WF, PHASE, RT, 2, NG>(a, max_tiles, n_rowsets, stream, tm);
+    case 3:
+      return launch_gemv_s<WF, PHASE, RT, 3, NG>(a, max_tiles, n_rowsets, stream, tm);
+    case 4:
+      return launch_gemv_s<WF, PHASE, RT, 4, NG>(a, max_tiles, n_rowsets, stream, tm);
+    case 5:
+    case 6:
+      return launch_gemv_s<WF, PHASE, RT, 6, NG>(a, max_tiles, n_rowsets, stream, tm);
+    default:
+      return launch_gemv_s<WF, PHASE, RT, 8, NG>(a, max_tiles, n_rowsets, stream, tm);
+  }
+}
 
 template <int WF, int PHASE, int RT>
 hipError_t launch_gemv_rt(const GemmArgs& a, int max_tiles, hipStream_t stream, const KernelTimer* tm) {
   const int out_dim = (PHASE == PHASE_GATE_UP) ? a.I : a.N;
   const int n_rowsets = out_dim / (RT * 16);
   const int G = a.K / 128;
-  constexpr int NG = kGemvGroupsPerWave;
-  const int need = (G + NG - 1) / NG;
-  if (need <= 1) return launch_gemv_s<WF, PHASE, RT, 1, NG>(a, max_tiles, n_rowsets, stream, tm);
-  if (need <= 2) return launch_gemv_s<WF, PHASE, RT, 2, NG>(a, max_tiles, n_rowsets, stream, tm);
-  if (need <= 3) return launch_gemv_s<WF, PHASE, RT, 3, NG>(a, max_tiles, n_rowsets, stream, tm);
-  if (need <= 4) return launch_gemv_s<WF, PHASE, RT, 4, NG>(a, max_tiles, n_rowsets, stream, tm);
-  if (need <= 6) return launch_gemv_s<WF, PHASE, RT, 6, NG>(a, max_tiles, n_rowsets, stream, tm);
-  if (need <= 8) return launch_gemv_s<WF, PHASE, RT, 8, NG>(a, max_tiles, n_rowsets, stream, tm);
-  if (need <= 16) return launch_gemv_s<WF, PHASE, RT, 8, 2 * NG>(a, max_tiles, n_rowsets, stream, tm);
-  return launch_gemv_s<WF, PHASE, RT, 8, 0>(a, max_tiles, n_rowsets, stream, tm);
+  constexpr int target = gemv_target_groups(WF);
+  int S = (G + target - 1) / target;
+  if (S > 8) S = 8;
+  if (S == 5 || S == 7) ++S;  // instantiated part counts: 1, 2, 3, 4, 6, 8
+  const int NG = (G + S - 1) / S;
+  switch (NG) {
+    case 1:
+      return launch_gemv_ng<WF, PHASE, RT, 1>(a, S, max_tiles, n_rowsets, stream, tm);
+    case 2:
+      return launch_gemv_ng<WF, PHASE, RT, 2>(a, S, max_tiles, n_rowsets, stream, tm);
+    case 3:
+      return launch_gemv_ng<WF, PHASE, RT, 3>(a, S, max_tiles, n_rowsets, stream, tm);
+    case 4:
+      return launch_gemv_ng<WF, PHASE, RT, 4>(a, S, max_tiles, n_rowsets, stream, tm);
+    default:
+      return launch_gemv_s<WF, PHASE, RT, 8, 0>(a, max_tiles, n_rowsets, stream, tm);
+  }
 }
 
 template <int WF>
