@@ -55,7 +55,7 @@ struct RSlot {
 
 // Weight loads address a uniform per-expert base plus a 32-bit offset
 // (global_load ... saddr form: one offset register per load).
-template <int WF, int NT>
+template <int WF, int NT, bool SCALES = true>
 __device__ __forceinline__ void load_w(WSlot<WF, NT>& r, const uint8_t* wexp, const uint16_t* sexp,
                                        const uint32_t (&rbo)[NT], const uint32_t (&sbo)[NT], int g,
                                        uint32_t lane) {
@@ -65,8 +65,26 @@ __device__ __forceinline__ void load_w(WSlot<WF, NT>& r, const uint8_t* wexp, co
 #pragma unroll
     for (int i = 0; i < NBLK; ++i)
       r.w[t][i] = *(const u32x4*)(wexp + (rbo[t] + (uint32_t)(g * NBLK + i) * 1024u + lane * 16u));
-    if (WF == WF_I4) r.s[t] = *(const u32x2*)(sexp + (sbo[t] + (uint32_t)g * 16u + 4u * (lane >> 4)));
+    if (WF == WF_I4 && SCALES) r.s[t] = *(const u32x2*)(sexp + (sbo[t] + (uint32_t)g * 16u + 4u * (lane >> 4)));
   }
+}
+
+// Direct-to-LDS loads (global_load_lds): lane l's 16 (4) bytes from src land
+// at dst + 16 l (dst + 4 l); dst must be the same in every lane.  Waited for
+// with the vector-memory counter.
+__device__ __forceinline__ void load16_to_lds(const void* src, uint8_t* dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+}
+__device__ __forceinline__ void load4_to_lds(const void* src, uint8_t* dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
+}
+
+// Waits for every vector-memory load of this wave (direct-to-LDS ones
+// included) before the LDS is read.
+__device__ __forceinline__ void wait_vmem() {
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __asm__ volatile("" ::: "memory");
 }
 
 // B operand of group g, one load per MFMA step: lane l holds
@@ -76,18 +94,25 @@ __device__ __forceinline__ void load_x_full(u32x4 (&x)[4], const uint8_t* xrow, 
   for (int s = 0; s < 4; ++s) x[s] = *(const u32x4*)(xrow + (g * 128 + 32 * s) * 2);
 }
 
+// Sum of the two bf16 values of w added to acc (v_dot2 with (1, 1)).
+__device__ __forceinline__ float add_bf16_pair(uint32_t w, float acc) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w), __builtin_bit_cast(bf16x2, 0x3f803f80u), acc,
+                                         false);
+}
+
 // Sum of the group's 128 activations of the lane's column (lanes l, l^16,
 // l^32, l^48 hold its four 32-wide quarters).
 __device__ __forceinline__ float group_sum_full(const u32x4 (&x)[4]) {
-  float xs = 0.f;
+  float a = 0.f, b = 0.f;
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
-#pragma unroll
-    for (int h = 0; h < 4; ++h) {
-      xs += __uint_as_float(x[s][h] << 16);
-      xs += __uint_as_float(x[s][h] & 0xffff0000u);
-    }
-  xs = add_xor16(xs);
+  for (int s = 0; s < 4; ++s) {
+    a = add_bf16_pair(x[s][0], a);
+    b = add_bf16_pair(x[s][1], b);
+    a = add_bf16_pair(x[s][2], a);
+    b = add_bf16_pair(x[s][3], b);
+  }
+  float xs = add_xor16(a + b);
   return add_xor32(xs);
 }
 
@@ -98,14 +123,22 @@ __device__ __forceinline__ float group_sum_full(const u32x4 (&x)[4]) {
 // by lane (q, 4s + c) of the same row: a DPP row_shl by 4s.  Only columns
 // c < 4 carry data; the others hold copies of other rows and their outputs are
 // never stored (rows past the tile's count are padding).
+template <int CTRL>
+__device__ __forceinline__ u32x4 row_shl4(u32x4 v) {
+  return u32x4{(uint32_t)__builtin_amdgcn_mov_dpp((int)v[0], CTRL, 0xf, 0xf, true),
+               (uint32_t)__builtin_amdgcn_mov_dpp((int)v[1], CTRL, 0xf, 0xf, true),
+               (uint32_t)__builtin_amdgcn_mov_dpp((int)v[2], CTRL, 0xf, 0xf, true),
+               (uint32_t)__builtin_amdgcn_mov_dpp((int)v[3], CTRL, 0xf, 0xf, true)};
+}
+
 __device__ __forceinline__ u32x4 quad_operand(u32x4 xq, int s) {
   switch (s) {
     case 1:
-      return u32x4{dpp_u32<0x104>(xq[0]), dpp_u32<0x104>(xq[1]), dpp_u32<0x104>(xq[2]), dpp_u32<0x104>(xq[3])};
+      return row_shl4<0x104>(xq);
     case 2:
-      return u32x4{dpp_u32<0x108>(xq[0]), dpp_u32<0x108>(xq[1]), dpp_u32<0x108>(xq[2]), dpp_u32<0x108>(xq[3])};
+      return row_shl4<0x108>(xq);
     case 3:
-      return u32x4{dpp_u32<0x10C>(xq[0]), dpp_u32<0x10C>(xq[1]), dpp_u32<0x10C>(xq[2]), dpp_u32<0x10C>(xq[3])};
+      return row_shl4<0x10C>(xq);
     default:
       return xq;
   }
@@ -114,29 +147,61 @@ __device__ __forceinline__ u32x4 quad_operand(u32x4 xq, int s) {
 // Group sum of a quad-form load: lanes c < 4 of every row end with the sum of
 // the group's 128 activations of column c.
 __device__ __forceinline__ float quad_group_sum(u32x4 xq) {
-  float v = 0.f;
-#pragma unroll
-  for (int h = 0; h < 4; ++h) {
-    v += __uint_as_float(xq[h] << 16);
-    v += __uint_as_float(xq[h] & 0xffff0000u);
-  }
+  float v = add_bf16_pair(xq[0], 0.f);
+  v = add_bf16_pair(xq[1], v);
+  v = add_bf16_pair(xq[2], v);
+  v = add_bf16_pair(xq[3], v);
   v = v + __uint_as_float(dpp_u32<0x108>(__float_as_uint(v)));  // + lane c + 8
   v = v + __uint_as_float(dpp_u32<0x104>(__float_as_uint(v)));  // + lanes c + 4, c + 12
   v = add_xor16(v);
   return add_xor32(v);
 }
 
+// int4 dequantisation with v_and_or_b32: (w >> 4j) & 0x000F000F | 0x43004300
+// in one instruction after the shift (the mask comes from an SGPR, the bf16
+// exponent bits from a VGPR: one constant-bus read per instruction).
+struct DqConst {
+  uint32_t mask;  // SGPR: 0x000F000F
+  uint32_t bits;  // VGPR: 0x43004300
+};
+
+__device__ __forceinline__ DqConst dq_const() {
+  DqConst k;
+  __asm__ volatile("s_mov_b32 %0, 0xf000f" : "=s"(k.mask));
+  __asm__ volatile("v_mov_b32 %0, 0x43004300" : "=v"(k.bits));
+  return k;
+}
+
+// (w >> SH) & mask | bits; the shift sits inside the same statement so that
+// nothing of the dequantisation can move away from the constants' block
+template <int SH>
+__device__ __forceinline__ uint32_t dq_word(uint32_t w, const DqConst& k) {
+  uint32_t r;
+  if (SH == 0)
+    __asm__("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(k.mask), "v"(k.bits));
+  else
+    __asm__("v_lshrrev_b32 %0, %4, %1\n\tv_and_or_b32 %0, %0, %2, %3"
+            : "=&v"(r)
+            : "v"(w), "s"(k.mask), "v"(k.bits), "i"(SH));
+  return r;
+}
+
+__device__ __forceinline__ u32x4 dq_i4_k(uint32_t w, const DqConst& k) {
+  return u32x4{dq_word<0>(w, k), dq_word<4>(w, k), dq_word<8>(w, k), dq_word<12>(w, k)};
+}
+
 // A operand of tile t, step s.
 template <int WF, int NT>
-__device__ __forceinline__ u32x4 a_operand(const WSlot<WF, NT>& r, int t, int s) {
-  if (WF == WF_I4) return dq_i4(r.w[t][0][s]);
+__device__ __forceinline__ u32x4 a_operand(const WSlot<WF, NT>& r, int t, int s, const DqConst& k) {
+  if (WF == WF_I4) return dq_i4_k(r.w[t][0][s], k);
   if (WF == WF_I8) return dq_i8(r.w[t][s >> 1][2 * (s & 1)], r.w[t][s >> 1][2 * (s & 1) + 1]);
   return r.w[t][s];
 }
 
 // Marks the slot's registers as redefined here: dequantisation that both
 // activation forms share stays inside each form's branch instead of being
-// hoisted above it with every group's operands live at once.
+// hoisted above it with every group's operands live at once (int8 and bf16;
+// the int4 path gets the same from its branch-local constants).
 template <int WF, int NT>
 __device__ __forceinline__ void pin_slot(WSlot<WF, NT>& r) {
 #pragma unroll
@@ -148,20 +213,25 @@ __device__ __forceinline__ void pin_slot(WSlot<WF, NT>& r) {
     for (int t = 0; t < NT; ++t) __asm__ volatile("" : "+v"(r.s[t]));
 }
 
-// One group of a quad-form tile: the B operand of each step is built once and
-// feeds the NT tiles.  use == false computes and adds nothing.
-template <int WF, int NT>
-__device__ __forceinline__ void mma_group_quad(const WSlot<WF, NT>& r, u32x4 xq, float xs, f32x4 (&acc)[NT],
-                                               bool use) {
+// One group: BOP(s) gives the B operand of step s (built once, it feeds the
+// NT tiles); xs: the group sum of the lane's column (int formats).  use ==
+// false computes and adds nothing (a select, so no load is ever
+// control-dependent).
+template <int WF, int NT, class BOp>
+__device__ __forceinline__ void mma_group_b(const WSlot<WF, NT>& r, BOp bop, float xs, f32x4 (&acc)[NT], bool use,
+                                            const DqConst& k) {
   const float c = WF == WF_I4 ? -136.0f * xs : WF == WF_I8 ? -128.0f * xs : 0.0f;
   f32x4 tmp[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) tmp[t] = f32x4{c, c, c, c};
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    const u32x4 b = quad_operand(xq, s);
+    const u32x4 b = bop(s);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) tmp[t] = mfma_bf16(a_operand<WF, NT>(r, t, s), b, tmp[t]);
+    for (int t = 0; t < NT; ++t) tmp[t] = mfma_bf16(a_operand<WF, NT>(r, t, s, k), b, tmp[t]);
+    // one step's operands at a time (the scheduler would dequantise every
+    // step ahead, a register per value)
+    __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
@@ -251,11 +321,20 @@ __host__ __device__ constexpr int gemv_rowsets_per_wg(int S) { return S == 1 ? 4
 // count exits at once).  NG > 0: each wave issues the loads of all its (at
 // most NG) groups at once and then consumes them; NG == 0: each wave streams
 // its groups through the D-deep ring.
-template <int WF, int PHASE, int RT, int S, int NG, int D>
+template <int WF, int PHASE, int RT, int S, int NG, int D, bool FULL>
 __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(GemmArgs a, int n_rowsets) {
   constexpr int P = gemv_rowsets_per_wg(S);
   constexpr int NT = (PHASE == PHASE_GATE_UP) ? 2 * RT : RT;
-  __shared__ f32x4 red[S > 1 ? S * P : 1][NT][64];
+  // Per-wave LDS region: the direct-to-LDS staging of the quad-form
+  // activations (NG KiB) and the int4 scales (32 B per tile and group), then
+  // reused for the wave's K-part partial sums (NT KiB).
+  constexpr int kStageX = NG * 1024;
+  constexpr int kStageS = (WF == WF_I4) ? NT * NG * 32 : 0;
+  constexpr int kRed = S > 1 ? NT * 1024 : 0;
+  constexpr int kRegion = (kStageX + kStageS > kRed ? kStageX + kStageS : kRed) > 16
+                              ? (kStageX + kStageS > kRed ? kStageX + kStageS : kRed)
+                              : 16;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[S * P][kRegion];
 
   const int tile = blockIdx.y;
   const uint32_t lane = threadIdx.x & 63;
@@ -310,9 +389,10 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
   }
 
   // this wave's groups: kpart + S*i, i < n
-  const int n = kpart < G ? (G - kpart + S - 1) / S : 0;
-  const int n_last = n > 0 ? n - 1 : 0;
-  const int g_base = kpart < G ? kpart : 0;
+  // (FULL: G == S * NG, every wave has exactly NG groups)
+  const int n = FULL ? NG : kpart < G ? (G - kpart + S - 1) / S : 0;
+  const int n_last = FULL ? NG - 1 : n > 0 ? n - 1 : 0;
+  const int g_base = FULL ? kpart : kpart < G ? kpart : 0;
   constexpr bool IS_INT = WF == WF_I4 || WF == WF_I8;
 
   f32x4 acc[NT];
@@ -320,32 +400,60 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
   for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (NG > 0) {
-    // weights first: the activation addresses may still wait for src
+    uint8_t* region = lds[__builtin_amdgcn_readfirstlane(wave)];
+    // weights first (registers), then the scales (LDS): the activation
+    // addresses may still wait for src
     WSlot<WF, NT> sl[NG > 0 ? NG : 1];
 #pragma unroll
-    for (int i = 0; i < NG; ++i) load_w<WF, NT>(sl[i], wexp, sexp, rbo, sbo, g_base + S * min(i, n_last), lane);
+    for (int i = 0; i < NG; ++i)
+      load_w<WF, NT, false>(sl[i], wexp, sexp, rbo, sbo, g_base + S * min(i, n_last), lane);
+    // the int4 scales: lane (t, i, part) = (l / 8NG, l / 8 % NG, l % 8) loads
+    // 4 bytes (rows 2 part, 2 part + 1) of tile t's scales for group i
+    const uint16_t* s_src = sexp;
+    if (WF == WF_I4) {
+      const int t = lane / (8 * NG), i = (lane / 8) % NG;
+      uint32_t sb = sbo[0];
+#pragma unroll
+      for (int tt = 1; tt < NT; ++tt) sb = (t == tt) ? sbo[tt] : sb;
+      s_src = sexp + sb + (uint32_t)(g_base + S * min(i, n_last)) * 16u + 2u * (lane % 8);
+    }
     __builtin_amdgcn_sched_barrier(0);
     if (rows <= 4) {
-      // quad form: one load per group, the B operands built per step
+      // quad form: one load per group into LDS, the B operands built per step
       const uint8_t* xq_row = (const uint8_t*)a.in + (int64_t)srcq * a.K * 2 + 64 * (col >> 2) + 16 * (lane >> 4);
-      u32x4 xq[NG > 0 ? NG : 1];
 #pragma unroll
-      for (int i = 0; i < NG; ++i) xq[i] = *(const u32x4*)(xq_row + (g_base + S * min(i, n_last)) * 256);
-      __builtin_amdgcn_sched_barrier(0);
+      for (int i = 0; i < NG; ++i) load16_to_lds(xq_row + (g_base + S * min(i, n_last)) * 256, region + i * 1024);
+      if (WF == WF_I4 && lane < (uint32_t)(NT * NG * 8)) load4_to_lds(s_src, region + kStageX);
+      wait_vmem();
+      // defined inside each form's branch (an opaque value): the int4
+      // dequantisation cannot be hoisted above the branch
+      const DqConst kdq = dq_const();
 #pragma unroll
       for (int i = 0; i < NG; ++i) {
-        pin_slot<WF, NT>(sl[i]);
-        mma_group_quad<WF, NT>(sl[i], xq[i], IS_INT ? quad_group_sum(xq[i]) : 0.f, acc, i < n);
+        const u32x4 xq = *(const u32x4*)(region + i * 1024 + lane * 16);
+        if (WF == WF_I4)
+#pragma unroll
+          for (int t = 0; t < NT; ++t) sl[i].s[t] = *(const u32x2*)(region + kStageX + (t * NG + i) * 32 + 8 * (lane >> 4));
+        if (WF != WF_I4) pin_slot<WF, NT>(sl[i]);  // (int4: the constants above)
+        mma_group_b<WF, NT>(sl[i], [&](int st) { return quad_operand(xq, st); }, IS_INT ? quad_group_sum(xq) : 0.f,
+                            acc, FULL || i < n, kdq);
       }
     } else {
-      // larger tiles: full B operands, one group's at a time (few registers)
+      // larger tiles: full B operands in registers, one group's at a time
       const uint8_t* xrow = xbase + (int64_t)src * a.K * 2;
+      if (WF == WF_I4 && lane < (uint32_t)(NT * NG * 8)) load4_to_lds(s_src, region + kStageX);
+      const DqConst kdq = dq_const();
 #pragma unroll
       for (int i = 0; i < NG; ++i) {
         u32x4 xb[4];
         load_x_full(xb, xrow, g_base + S * min(i, n_last));
-        pin_slot<WF, NT>(sl[i]);
-        mma_group<WF, NT>(sl[i], xb, IS_INT ? group_sum_full(xb) : 0.f, acc, i < n);
+        wait_vmem();
+        if (WF == WF_I4)
+#pragma unroll
+          for (int t = 0; t < NT; ++t) sl[i].s[t] = *(const u32x2*)(region + kStageX + (t * NG + i) * 32 + 8 * (lane >> 4));
+        if (WF != WF_I4) pin_slot<WF, NT>(sl[i]);
+        mma_group_b<WF, NT>(sl[i], [&](int st) { return xb[st]; }, IS_INT ? group_sum_full(xb) : 0.f, acc,
+                            FULL || i < n, kdq);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -375,15 +483,17 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
   }
 
   if (S > 1) {
+    // each wave's partial sums go to its own region (its staged data is
+    // consumed), the K part 0 wave adds the S parts in order
 #pragma unroll
-    for (int t = 0; t < NT; ++t) red[S > 1 ? wave : 0][t][lane] = acc[t];
+    for (int t = 0; t < NT; ++t) *(f32x4*)(lds[wave] + t * 1024 + lane * 16) = acc[t];
     __syncthreads();
     if (kpart != 0) return;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      f32x4 s = red[S > 1 ? wave : 0][t][lane];
+      f32x4 s = *(const f32x4*)(lds[wave] + t * 1024 + lane * 16);
 #pragma unroll
-      for (int k = 1; k < S; ++k) s += red[S > 1 ? wave + k : 0][t][lane];
+      for (int k = 1; k < S; ++k) s += *(const f32x4*)(lds[wave + k] + t * 1024 + lane * 16);
       acc[t] = s;
     }
   }
@@ -402,7 +512,10 @@ hipError_t launch_gemv_s(const GemmArgs& a, int max_tiles, int n_rowsets, hipStr
   constexpr int P = gemv_rowsets_per_wg(S);
   constexpr int D = (WF == WF_BF16) ? 2 : 3;
   dim3 grid((n_rowsets + P - 1) / P, max_tiles);
-  launch_timed(gemv_kernel<WF, PHASE, RT, S, NG, D>, grid, dim3(S * P * 64), 0, stream, tm, a, n_rowsets);
+  if (NG > 0 && a.K / 128 == S * NG)
+    launch_timed(gemv_kernel<WF, PHASE, RT, S, NG, D, true>, grid, dim3(S * P * 64), 0, stream, tm, a, n_rowsets);
+  else
+    launch_timed(gemv_kernel<WF, PHASE, RT, S, NG, D, false>, grid, dim3(S * P * 64), 0, stream, tm, a, n_rowsets);
   return hipGetLastError();
 }
 
