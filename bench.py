@@ -18,7 +18,13 @@ Printed JSON fields beyond the standard ones:
                  activations in/out) / its average event-timed duration vs 8 TB/s
   cpu_baseline   the oracle's restatement of the reference CPU expert loop
                  (nano_ktrans/kernels/cpu_moe.py:491-539), timed on this host
-  secondary      other token counts and the int8 prefill configuration
+  secondary      other token counts (T=1, 4), the layer from hidden states
+                 (router GEMV fused; plus RMSNorm and residual), the int8
+                 per-channel prefill at T=512/2048/4096 (Zipf-skewed routing),
+                 a Mixtral-8x7B-shaped int4 layer (T=1, 16, 2048) and a
+                 Qwen1.5-MoE-shaped int8 layer with its shared expert (T=1, 16,
+                 1024); roofline_alt gives the other bound's fraction where a
+                 shape sits near the ridge
 """
 import argparse
 import json
@@ -41,22 +47,37 @@ def log(*a):
 
 # --------------------------------------------------------------------- problem
 class Workload:
-    def __init__(self, name, H, E, k, I, wfmt, softmax, renorm, tokens, zipf=0.0, seed=1):
+    def __init__(self, name, H, E, k, I, wfmt, softmax, renorm, tokens, zipf=0.0, seed=1, shared=0):
         self.name, self.H, self.E, self.k, self.I = name, H, E, k, I
         self.wfmt, self.softmax, self.renorm, self.tokens, self.zipf, self.seed = wfmt, softmax, renorm, tokens, zipf, seed
+        self.shared = shared  # shared-expert intermediate size (0: none)
 
-    def bytes_per_expert(self, proj):
-        import math
-        n, kk = (2 * self.I, self.H) if proj == "gate_up" else (self.H, self.I)
+    def _bytes(self, n, kk):
         if self.wfmt == "int4_g128":
             return n * kk // 2 + n * (kk // 128) * 2
         if self.wfmt == "int8_per_channel":
             return n * kk + n * 2
         return n * kk * 2
 
+    def bytes_per_expert(self, proj):
+        n, kk = (2 * self.I, self.H) if proj == "gate_up" else (self.H, self.I)
+        return self._bytes(n, kk)
+
+    def shared_bytes(self):
+        """Shared expert (gate_up + down) plus its gate vector, read once per layer call."""
+        if not self.shared:
+            return 0
+        return self._bytes(2 * self.shared, self.H) + self._bytes(self.H, self.shared) + self.H * 2
+
 
 QWEN3_INT4 = dict(H=2048, E=128, k=8, I=768, wfmt="int4_g128", softmax=True, renorm=True, seed=1)
 QWEN3_INT8 = dict(H=2048, E=128, k=8, I=768, wfmt="int8_per_channel", softmax=True, renorm=True, seed=1, zipf=1.1)
+# Mixtral-8x7B-shaped layer (top-k on the logits, then softmax over the k) and
+# Qwen1.5-MoE-A2.7B-shaped layer (60 experts, softmax without renormalisation,
+# shared expert with a sigmoid gate)
+MIXTRAL_INT4 = dict(H=4096, E=8, k=2, I=14336, wfmt="int4_g128", softmax=False, renorm=False, seed=2)
+QWEN15_INT8 = dict(H=2048, E=60, k=4, I=1408, wfmt="int8_per_channel", softmax=True, renorm=False, seed=3,
+                   shared=5632)
 
 
 def make_layers(w, n_layers, device, max_tokens):
@@ -73,17 +94,24 @@ def make_layers(w, n_layers, device, max_tokens):
     router = torch.randn(w.E, w.H, generator=g, device=device) * 0.02
     layers = []
     first = NativeMoE(num_experts=w.E, top_k=w.k, hidden_size=w.H, intermediate_size=w.I,
-                      weight_format=w.wfmt, act_dtype=torch.bfloat16, use_softmax=w.softmax,
-                      renorm=w.renorm, max_tokens=max_tokens, device=device)
+                      shared_intermediate_size=w.shared, weight_format=w.wfmt, act_dtype=torch.bfloat16,
+                      use_softmax=w.softmax, renorm=w.renorm, max_tokens=max_tokens, device=device)
     for e in range(w.E):
         gate_up = torch.randn(2 * w.I, w.H, generator=g, device=device) * 0.02
         down = torch.randn(w.H, w.I, generator=g, device=device) * 0.02
         first.load_expert(e, quant(gate_up[: w.I]), quant(gate_up[w.I:]), quant(down))
+        del gate_up, down
+    if w.shared:
+        gs = torch.randn(2 * w.shared, w.H, generator=g, device=device) * 0.02
+        ds = torch.randn(w.H, w.shared, generator=g, device=device) * 0.02
+        gw = torch.randn(1, w.H, generator=g, device=device) * 0.02
+        first.load_shared_expert(quant(gs[: w.shared]), quant(gs[w.shared:]), quant(ds), gw)
+        del gs, ds
     layers.append(first)
     for _ in range(1, n_layers):
         n = NativeMoE(num_experts=w.E, top_k=w.k, hidden_size=w.H, intermediate_size=w.I,
-                      weight_format=w.wfmt, act_dtype=torch.bfloat16, use_softmax=w.softmax,
-                      renorm=w.renorm, max_tokens=max_tokens, device=device)
+                      shared_intermediate_size=w.shared, weight_format=w.wfmt, act_dtype=torch.bfloat16,
+                      use_softmax=w.softmax, renorm=w.renorm, max_tokens=max_tokens, device=device)
         for slot, t in first.slots.items():
             n.slots[slot].copy_(t)
         layers.append(n)
@@ -275,7 +303,7 @@ def bench_workload(w, T, layers, router, steps, warmup, device):
     gate_up_bytes = mean_act * w.bytes_per_expert("gate_up") + T * w.H * 2 + P * w.I * 2
     down_bytes = mean_act * w.bytes_per_expert("down") + P * w.I * 2 + P * w.H * 4
     layer_bytes = (mean_act * (w.bytes_per_expert("gate_up") + w.bytes_per_expert("down"))
-                   + T * w.H * 2 * 2 + T * w.E * 2)
+                   + w.shared_bytes() + T * w.H * 2 * 2 + T * w.E * 2)
     gate_up_flops = 2.0 * P * 2 * w.I * w.H
     down_flops = 2.0 * P * w.H * w.I
     form = kernel_form(w, T)
@@ -306,10 +334,13 @@ def traffic_table():
     return out
 
 
-def roofline_for(res, bound):
+def roofline_for(res, bound=None):
     """Roofline of the dominant kernel (the longer of the two expert-GEMM kernels),
-    its duration from the dispatch-stamped events of time_kernel."""
+    its duration from the dispatch-stamped events of time_kernel.  bound None:
+    HBM for the decode form, MFMA for the prefill form."""
     k = "gate_up" if res["gate_up"]["us"] >= res["down"]["us"] else "down"
+    if bound is None:
+        bound = "hbm" if res[k]["kernel"] == "gemv_kernel" else "mfma"
     d = res[k]
     sec = d["us"] * 1e-6
     name = f"{d['kernel']} ({k}, {res['wfmt']}, T={res['tokens']})"
@@ -555,15 +586,30 @@ def main():
     del layers
     torch.cuda.empty_cache()
     if not args.no_secondary:
-        w = Workload("qwen3_30b_a3b_moe_layer_int8_pc_prefill_zipf", tokens=4096, **QWEN3_INT8)
-        log(f"secondary: {w.name} T=4096")
-        router8, layers8 = make_layers(w, 2, dev, max_tokens=4096)
-        r = bench_workload(w, 4096, layers8, router8, 20, 4, dev)
-        r["roofline"] = roofline_for(r, "mfma")
-        log(json.dumps(r))
-        secondary.append(r)
-        del layers8
-        torch.cuda.empty_cache()
+        # prefill and the other model shapes: (workload, weight copies, [(T, steps, warmup, bounds)])
+        # bounds: the roofline(s) reported; at the ridge both
+        plan = [
+            (Workload("qwen3_30b_a3b_moe_layer_int8_pc_prefill_zipf", tokens=4096, **QWEN3_INT8), 2,
+             [(4096, 20, 4, ("mfma",)), (512, 100, 10, ("mfma", "hbm")), (2048, 40, 6, ("mfma", "hbm"))]),
+            (Workload("mixtral_8x7b_moe_layer_int4_g128", tokens=16, **MIXTRAL_INT4), 4,
+             [(1, 200, 20, ("hbm",)), (16, 200, 20, ("hbm",)), (2048, 20, 4, ("mfma",))]),
+            (Workload("qwen15_moe_a27b_layer_int8_pc_shared", tokens=16, **QWEN15_INT8), 4,
+             [(1, 200, 20, ("hbm",)), (16, 200, 20, ("hbm",)), (1024, 40, 6, ("hbm", "mfma"))]),
+        ]
+        for w, copies, runs in plan:
+            max_t = max(T for T, *_ in runs)
+            log(f"secondary: building {copies} copies of {w.name}")
+            rtr, lays = make_layers(w, copies, dev, max_tokens=max_t)
+            for T, steps, warm, bounds in runs:
+                log(f"secondary: {w.name} T={T}")
+                r = bench_workload(w, T, lays, rtr, steps, warm, dev)
+                r["roofline"] = roofline_for(r, bounds[0])
+                if len(bounds) > 1:
+                    r["roofline_alt"] = roofline_for(r, bounds[1])
+                log(json.dumps(r))
+                secondary.append(r)
+            del lays
+            torch.cuda.empty_cache()
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle port of the reference CPU loop)")
@@ -592,7 +638,8 @@ def main():
         "cpu_baseline": cpu,
         "secondary": [{k: v for k, v in r.items() if k in ("workload", "tokens", "us_per_layer", "tokens_per_s",
                                                            "mean_active_experts", "breakdown_us", "roofline",
-                                                           "layer_hbm_frac")} for r in secondary],
+                                                           "roofline_alt", "layer_hbm_frac")}
+                      for r in secondary],
     }
     print(json.dumps(line), flush=True)
 

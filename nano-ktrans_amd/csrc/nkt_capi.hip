@@ -101,6 +101,8 @@ struct WsLayout {
   int max_tiles;
 };
 
+constexpr int kSharedDecodeMaxTokens = 256;
+
 // the prefill form covers both projections of the routed (or shared) experts
 bool prefill_form_ok(const Handle* h, bool shared) {
   const int I = shared ? h->Is : h->I;
@@ -115,7 +117,14 @@ WsLayout ws_layout(const Handle* h, int T) {
   const size_t P = (size_t)T * h->k;
   const size_t es = h->act_bf16 ? 2 : 4;
   L.bm = gemm_tile_m(T > 0 ? T : 1, h->k, h->E, h->wf, prefill_form_ok(h, false));
-  L.bm_shared = gemm_tile_m(T > 0 ? T : 1, 1, 1, h->wf, prefill_form_ok(h, true));
+  // the shared expert takes every token as one group: its prefill-form grid
+  // (weight slabs x token tiles) stays far below the CU count until T is in
+  // the hundreds, while the decode form's split-K grid fills the GPU
+  L.bm_shared = (T <= kSharedDecodeMaxTokens && h->Is > 0 &&
+                 gemv_supported(h->wf, PHASE_GATE_UP, 2 * h->Is, h->H, h->Is) &&
+                 gemv_supported(h->wf, PHASE_DOWN, h->H, h->Is, h->Is))
+                    ? 16
+                    : gemm_tile_m(T > 0 ? T : 1, 1, 1, h->wf, prefill_form_ok(h, true));
   L.max_tiles = (int)(P / L.bm) + (int)(P < (size_t)h->E ? P : (size_t)h->E);
   size_t sz[kWsAll];
   sz[NKT_WS_TOPK_IDS] = P * 4;
