@@ -9,19 +9,23 @@
 // One wave owns one (tile, row set, K part): a tile is up to 16 positions of
 // one expert, a row set is RT 16-row output tiles (gate_up: RT gate tiles and
 // the RT matching up tiles, so SwiGLU is local), the K part is every S-th
-// 128-wide K group.  The wave reads its weight blocks straight from HBM, one
-// 16-byte load per lane per 1 KiB block.  Normally K is split over S waves
-// of one workgroup so that each wave owns two groups and issues all of their
-// loads at once (many short waves stream HBM better than few long ones); for
-// long K the wave streams its groups through a D-deep register ring whose
-// refills are issued right after the slot is consumed, always (past the last
-// group they re-read it, an L2 hit), so the loop has no branch, store or
-// barrier.  The matrix core takes the weights as the A operand and the tile's
-// activations as B: in the B-operand lane layout (four loads per group), or,
-// for single-position tiles, one load per group spread over the B layout by
-// DPP row broadcasts.  Gathered rows come from the per-tile source rows K2
-// writes (indexed by tile, so their load overlaps the tile record's).  The S
-// partial sums meet in LDS and are added in K-part order.
+// 128-wide K group.  The wave reads its weight blocks straight from HBM into
+// registers, one 16-byte load per lane per 1 KiB block.  Normally K is split
+// over S waves of one workgroup so that each wave owns NG groups (about 8 KiB
+// of weights) and issues all of their loads at once (many short waves stream
+// HBM better than few long ones); for long K the wave streams its groups
+// through a D-deep register ring whose refills are issued right after the
+// slot is consumed, always (past the last group they re-read it, an L2 hit),
+// so the loop has no branch, store or barrier.  The matrix core takes the
+// weights as the A operand and the tile's activations as B.  Tiles of at most
+// four positions use the quad form: one 16-byte load per lane per group,
+// landing in LDS through a direct-to-LDS load (no registers held while in
+// flight), each step's B operand built by a DPP row shift; larger tiles load
+// the B-operand layout (four loads per group) into registers one group at a
+// time.  int4 scales also arrive through a direct-to-LDS load.  Gathered rows
+// come from the per-tile source rows K2 writes (indexed by tile, so their
+// load overlaps the tile record's).  The S partial sums meet in LDS and are
+// added in K-part order.
 //
 // Dequantisation is the same as the prefill kernel's: codes enter the matrix
 // core as exact bf16 integers with an offset (int4: 136 + q, int8: 128 + q),
