@@ -461,6 +461,33 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+  } else if (rows <= 4) {
+    // the ring with quad-form activations (one register load per group)
+    const uint8_t* xq_row = (const uint8_t*)a.in + (int64_t)srcq * a.K * 2 + 64 * (col >> 2) + 16 * (lane >> 4);
+    WSlot<WF, NT> rw[D];
+    u32x4 rx[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int g = g_base + S * min(d, n_last);
+      load_w<WF, NT>(rw[d], wexp, sexp, rbo, sbo, g, lane);
+      rx[d] = *(const u32x4*)(xq_row + g * 256);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const DqConst kdq = dq_const();
+    for (int i0 = 0; i0 < n; i0 += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        if (WF != WF_I4) pin_slot<WF, NT>(rw[d]);
+        const u32x4 xq = rx[d];
+        mma_group_b<WF, NT>(rw[d], [&](int st) { return quad_operand(xq, st); }, IS_INT ? quad_group_sum(xq) : 0.f,
+                            acc, i0 + d < n, kdq);
+        __builtin_amdgcn_sched_barrier(0);
+        const int g = g_base + S * min(i0 + d + D, n_last);
+        load_w<WF, NT>(rw[d], wexp, sexp, rbo, sbo, g, lane);
+        rx[d] = *(const u32x4*)(xq_row + g * 256);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
   } else {
     const uint8_t* xrow = xbase + (int64_t)src * a.K * 2;
     RSlot<WF, NT> ring[D];
@@ -473,10 +500,13 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
     // sched_barrier: the scheduler would otherwise sink each refill down to
     // its use in the next iteration (shorter live ranges, no latency hiding)
     __builtin_amdgcn_sched_barrier(0);
+    const DqConst kdq = dq_const();
     for (int i0 = 0; i0 < n; i0 += D) {
 #pragma unroll
       for (int d = 0; d < D; ++d) {
-        mma_group<WF, NT>(ring[d].w, ring[d].x, IS_INT ? group_sum_full(ring[d].x) : 0.f, acc, i0 + d < n);
+        if (WF != WF_I4) pin_slot<WF, NT>(ring[d].w);
+        mma_group_b<WF, NT>(ring[d].w, [&](int st) { return ring[d].x[st]; },
+                            IS_INT ? group_sum_full(ring[d].x) : 0.f, acc, i0 + d < n, kdq);
         __builtin_amdgcn_sched_barrier(0);
         const int g = g_base + S * min(i0 + d + D, n_last);
         load_w<WF, NT>(ring[d].w, wexp, sexp, rbo, sbo, g, lane);
