@@ -219,6 +219,24 @@ __device__ __forceinline__ void lds_barrier() {
   __asm__ volatile("" ::: "memory");
 }
 
+// Direct-to-LDS loads (global_load_lds): lane l's 16 (4) bytes from src land
+// at dst + 16 l (dst + 4 l); dst must be the same in every lane.  Waited for
+// with the vector-memory counter.
+__device__ __forceinline__ void load16_to_lds(const void* src, uint8_t* dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+}
+__device__ __forceinline__ void load4_to_lds(const void* src, uint8_t* dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
+}
+
+// Waits for every vector-memory load of this wave (direct-to-LDS ones
+// included) before the LDS is read.
+__device__ __forceinline__ void wait_vmem() {
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __asm__ volatile("" ::: "memory");
+}
+
 // ---------------------------------------------------------------------------
 // MFMA wrappers (gfx950)
 //   16x16x32 bf16: lane l supplies A[l%16][8*(l/16) .. +7] and

@@ -47,6 +47,143 @@ struct ARegs {
 
 }  // namespace
 
+// One workgroup's work item: (token tile, weight slab) and the tile record.
+// XCD-aware work order: workgroup b runs on XCD b % 8, so XCD x takes the
+// x-th contiguous eighth of the (tile-major, slab-minor) item list.  The
+// slabs of one token tile and the tiles of one expert then run side by side
+// on one XCD and share its L2 (token rows and weight slabs are read from HBM
+// about once instead of once per XCD).  (The 1-D grid is a multiple of 8 and
+// at least 8 * per_xcd, so every item below n_items has exactly one
+// workgroup.)  Returns false for a workgroup without an item.
+struct TileItem {
+  int expert, row0, rows, slab;
+};
+
+__device__ __forceinline__ bool gemm2_item(const GemmArgs& a, int n_slabs, TileItem& it) {
+  const int n_tiles = a.n_tiles ? a.n_tiles[0] : (a.num_rows + kBM - 1) / kBM;
+  const int n_items = n_tiles * n_slabs;
+  const int b = blockIdx.x;
+  const int per_xcd = (n_items + kXcds - 1) / kXcds;
+  const int j = b / kXcds;
+  if (j >= per_xcd) return false;
+  const int item = (b % kXcds) * per_xcd + j;
+  if (item >= n_items) return false;
+  const int tile = item / n_slabs;
+  it.slab = item - tile * n_slabs;
+  if (a.n_tiles) {
+    const int4 rec = *(const int4*)(a.tiles + 4 * tile);
+    it.expert = rec.x;
+    it.row0 = rec.y;
+    it.rows = rec.z;
+  } else {
+    it.expert = 0;
+    it.row0 = tile * kBM;
+    it.rows = min(kBM, a.num_rows - it.row0);
+  }
+  return true;
+}
+
+// Source row of each tile position (positions past the tile's rows repeat
+// the first), into LDS; the caller's barrier publishes it.
+__device__ __forceinline__ void gemm2_sources(const GemmArgs& a, const TileItem& it, int* srcl) {
+  const int tid = threadIdx.x;
+  if (tid < kBM) {
+    const int p = it.row0 + (tid < it.rows ? tid : 0);
+    srcl[tid] = a.perm ? a.perm[p] / a.topk : p;
+  }
+}
+
+// Epilogue of the prefill form (shared by its kernels): int8 code offset,
+// per-row scales, then gate_up SwiGLU -> bf16 h (+ h's group sums) or down
+// fp32 y.  acc[r][c]: this wave's row tile r x column tile c.
+template <int WF, int PHASE, int kWaves>
+__device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[16 / kWaves][kCT], const int* srcl,
+                                               float (*hpart)[kBM], float* xtot_l, const int* wrow,
+                                               const uint16_t* sexp, int row0, int rows, int slab) {
+  constexpr int kRT = 16 / kWaves;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int G = a.K / 128;
+  const int rq = 4 * (lane >> 4);
+  if (WF == WF_I8) {
+    // the code offset: -128 x the row's K sum (group sums added in order)
+    if (tid < kBM) {
+      const float* xr = a.xsum + (int64_t)srcl[tid] * G;
+      float t = 0.f;
+      for (int g = 0; g < G; ++g) t += xr[g];
+      xtot_l[tid] = t;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < kCT; ++c) {
+      const float cv = -128.0f * xtot_l[c * 16 + (lane & 15)];
+#pragma unroll
+      for (int r = 0; r < kRT; ++r) acc[r][c] += f32x4{cv, cv, cv, cv};
+    }
+  }
+  if (PHASE == PHASE_GATE_UP) {
+    const int hcol0 = slab * 128 + wave * (128 / kWaves);
+    constexpr int HR = kRT / 2;
+    f32x4 sg[HR], su[HR];
+    if (WF == WF_I8) {
+#pragma unroll
+      for (int r = 0; r < HR; ++r) {
+        sg[r] = bf16x4_to_f32(*(const u32x2*)(sexp + wrow[r] + rq));
+        su[r] = bf16x4_to_f32(*(const u32x2*)(sexp + wrow[r + HR] + rq));
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < kCT; ++c) {
+      const int pl = c * 16 + (lane & 15);
+      float part = 0.f;
+#pragma unroll
+      for (int r = 0; r < HR; ++r) {
+        f32x4 gv = acc[r][c], uv = acc[r + HR][c];
+        if (WF == WF_I8) {
+          gv *= sg[r];
+          uv *= su[r];
+        }
+        u32x2 pk;
+        pk[0] = pack_bf16x2(silu_f32(gv[0]) * uv[0], silu_f32(gv[1]) * uv[1]);
+        pk[1] = pack_bf16x2(silu_f32(gv[2]) * uv[2], silu_f32(gv[3]) * uv[3]);
+        const f32x4 hb = bf16x4_to_f32(pk);
+        part += hb[0];
+        part += hb[1];
+        part += hb[2];
+        part += hb[3];
+        if (pl < rows) *(u32x2*)((uint16_t*)a.out + (int64_t)(row0 + pl) * a.I + hcol0 + r * 16 + rq) = pk;
+      }
+      // the 4 lanes holding one position's columns: fixed-order butterfly
+      part += __shfl_xor(part, 16);
+      part += __shfl_xor(part, 32);
+      if (lane < 16) hpart[wave][pl] = part;
+    }
+    if (a.hsum) {
+      __syncthreads();
+      if (tid < kBM && tid < rows) {
+        float s = hpart[0][tid];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) s += hpart[w][tid];
+        a.hsum[(int64_t)(row0 + tid) * (a.I / 128) + slab] = s;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < kRT; ++r) {
+      f32x4 sr = f32x4{1.f, 1.f, 1.f, 1.f};
+      if (WF == WF_I8) sr = bf16x4_to_f32(*(const u32x2*)(sexp + wrow[r] + rq));
+#pragma unroll
+      for (int c = 0; c < kCT; ++c) {
+        const int pl = c * 16 + (lane & 15);
+        f32x4 v = acc[r][c];
+        if (WF == WF_I8) v *= sr;
+        if (pl < rows) *(f32x4*)((float*)a.out + (int64_t)(row0 + pl) * a.N + wrow[r] + rq) = v;
+      }
+    }
+  }
+}
+
 template <int WF, int PHASE, int kWaves>
 __global__ void __launch_bounds__(64 * kWaves, 2) gemm2_kernel(GemmArgs a, int n_slabs) {
   constexpr int kRT = 16 / kWaves;  // 16-row weight tiles per wave
@@ -61,44 +198,15 @@ __global__ void __launch_bounds__(64 * kWaves, 2) gemm2_kernel(GemmArgs a, int n
   __shared__ float hpart[kWaves][kBM];
   __shared__ float xtot_l[kBM];
 
-  // XCD-aware work order: workgroup b runs on XCD b % 8, so XCD x takes the
-  // x-th contiguous eighth of the (tile-major, slab-minor) item list.  The
-  // slabs of one token tile and the tiles of one expert then run side by
-  // side on one XCD and share its L2 (token rows and weight slabs are read
-  // from HBM about once instead of once per XCD).
-  // (the 1-D grid is a multiple of 8 and at least 8 * per_xcd, so every
-  // item below n_items has exactly one workgroup)
-  const int n_tiles = a.n_tiles ? a.n_tiles[0] : (a.num_rows + kBM - 1) / kBM;
-  const int n_items = n_tiles * n_slabs;
-  const int b = blockIdx.x;
-  const int per_xcd = (n_items + kXcds - 1) / kXcds;
-  const int j = b / kXcds;
-  if (j >= per_xcd) return;
-  const int item = (b % kXcds) * per_xcd + j;
-  if (item >= n_items) return;
-  const int tile = item / n_slabs;
-  const int slab = item - tile * n_slabs;
+  TileItem it;
+  if (!gemm2_item(a, n_slabs, it)) return;
+  const int expert = it.expert, row0 = it.row0, rows = it.rows, slab = it.slab;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int G = a.K / 128;
   const int NKB = a.K / block_k(WF);
-
-  int expert, row0, rows;
-  if (a.n_tiles) {
-    const int4 rec = *(const int4*)(a.tiles + 4 * tile);
-    expert = rec.x;
-    row0 = rec.y;
-    rows = rec.z;
-  } else {
-    expert = 0;
-    row0 = tile * kBM;
-    rows = min(kBM, a.num_rows - row0);
-  }
-  if (tid < kBM) {
-    const int p = row0 + (tid < rows ? tid : 0);
-    srcl[tid] = a.perm ? a.perm[p] / a.topk : p;
-  }
+  gemm2_sources(a, it, srcl);
   __syncthreads();
 
   // ---- this wave's weight rows ------------------------------------------
@@ -246,84 +354,179 @@ __global__ void __launch_bounds__(64 * kWaves, 2) gemm2_kernel(GemmArgs a, int n
   }
   __syncthreads();
 
-  // ---- epilogue ----------------------------------------------------------
-  const int rq = 4 * (lane >> 4);
-  if (WF == WF_I8) {
-    // the code offset: -128 x the row's K sum (group sums added in order)
-    if (tid < kBM) {
-      const float* xr = a.xsum + (int64_t)srcl[tid] * G;
-      float t = 0.f;
-      for (int g = 0; g < G; ++g) t += xr[g];
-      xtot_l[tid] = t;
-    }
-    __syncthreads();
+  gemm2_epilogue<WF, PHASE, kWaves>(a, acc, srcl, hpart, xtot_l, wrow, sexp, row0, rows, slab);
+}
+
+// ---------------------------------------------------------------------------
+// int8 weights, three-stage direct-to-LDS pipeline.  Same tile, waves, work
+// order, MFMA sequence and epilogue as gemm2_kernel<WF_I8, ...> (so the
+// results are the same bit for bit), but both operands reach LDS by
+// direct-to-LDS loads (global_load_lds_dwordx4), no register staging, and K
+// advances in 64-wide stages through three LDS buffers, so two stages load
+// while one computes:
+//   * weights: each wave loads and reads only its own 4 row tiles, one 1 KiB
+//     block (16 rows x 64 K, lane l's MFMA fragments at 16 l) per row tile;
+//   * tokens: 64 positions x 128 B per stage, written by 8 loads of 8
+//     positions (2 per wave); lane l carries position 8 i + l / 8 into LDS
+//     slot l % 8 of that position's row, fetched from source chunk
+//     (l % 8) ^ ((position / 2) % 8): the MFMA operand reads of 16
+//     consecutive positions then cover all 64 LDS banks;
+//   * per stage a wave waits for its own loads of that stage (the next
+//     stage's 6 may stay in flight) and the workgroup meets at one
+//     LDS-only barrier, after which the buffer read two stages ago is
+//     refilled.
+// Six separate LDS objects: the compiler tells a direct-to-LDS load into one
+// buffer from reads of another and waits only where they alias.
+// ---------------------------------------------------------------------------
+constexpr int kI8Stage = 64;                   // K per stage
+constexpr int kI8WaveBytes = 4 * 1024;         // one wave's 4 weight blocks per stage
+constexpr int kI8TokBytes = kBM * kI8Stage * 2;
+constexpr uint32_t kI8Skip = 0xFFFFFF00u;     // a buffer offset past every range the kernel is given
+
+template <int PHASE>
+__global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slabs) {
+  constexpr int kWaves = 4;
+  constexpr int kRT = 4;
+  __shared__ __attribute__((aligned(1024))) uint8_t wb0[kWaves * kI8WaveBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t wb1[kWaves * kI8WaveBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t wb2[kWaves * kI8WaveBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t tb0[kI8TokBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t tb1[kI8TokBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t tb2[kI8TokBytes];
+  __shared__ int srcl[kBM];
+  __shared__ float hpart[kWaves][kBM];
+  __shared__ float xtot_l[kBM];
+
+  TileItem it;
+  if (!gemm2_item(a, n_slabs, it)) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  gemm2_sources(a, it, srcl);
+  __syncthreads();
+
+  const uint16_t* sexp = a.scales + (int64_t)it.expert * a.s_expert_elems;
+  const int NS = a.K / kI8Stage;  // stages = 1 KiB blocks per 16-row block
+  // buffer resources over this expert's weights and the activation rows; a
+  // load at offset kI8Skip is out of range: it reads nothing and writes zeros
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.w + (int64_t)it.expert * a.w_expert_bytes), (short)0, a.N * a.K, 0x00020000);
+  const __amdgpu_buffer_rsrc_t tres = __builtin_amdgcn_make_buffer_rsrc((void*)a.in, (short)0, a.in_bytes, 0x00020000);
+  int wrow[kRT];
+  uint32_t wsrc[kRT];
 #pragma unroll
-    for (int c = 0; c < kCT; ++c) {
-      const float cv = -128.0f * xtot_l[c * 16 + (lane & 15)];
-#pragma unroll
-      for (int r = 0; r < kRT; ++r) acc[r][c] += f32x4{cv, cv, cv, cv};
-    }
+  for (int r = 0; r < kRT; ++r) {
+    if (PHASE == PHASE_GATE_UP)
+      wrow[r] = (r < kRT / 2 ? 0 : a.I) + it.slab * 128 + wave * (128 / kWaves) + (r % (kRT / 2)) * 16;
+    else
+      wrow[r] = it.slab * 256 + wave * (256 / kWaves) + r * 16;
+    wsrc[r] = (uint32_t)(wrow[r] >> 4) * (uint32_t)NS * 1024u + lane * 16u;
   }
-  if (PHASE == PHASE_GATE_UP) {
-    const int hcol0 = slab * 128 + wave * (128 / kWaves);
-    constexpr int HR = kRT / 2;
-    f32x4 sg[HR], su[HR];
-    if (WF == WF_I8) {
+  uint32_t tsrc[2];
 #pragma unroll
-      for (int r = 0; r < HR; ++r) {
-        sg[r] = bf16x4_to_f32(*(const u32x2*)(sexp + wrow[r] + rq));
-        su[r] = bf16x4_to_f32(*(const u32x2*)(sexp + wrow[r + HR] + rq));
-      }
-    }
+  for (int j = 0; j < 2; ++j) {
+    const int p = 16 * wave + 8 * j + (lane >> 3);
+    const int chunk = (lane & 7) ^ ((p >> 1) & 7);
+    tsrc[j] = (uint32_t)srcl[p] * (uint32_t)a.K * 2u + chunk * 16u;
+  }
+  // this wave's slices of the buffers
+  const int wofs = wave * kI8WaveBytes;
+  const int tofs = wave * 2048;
+
+  // the 6 loads of stage st (st >= NS: out of range, no memory traffic)
+  auto issue = [&](int st, uint8_t* wb, uint8_t* tb) {
+    const bool live = st < NS;
 #pragma unroll
-    for (int c = 0; c < kCT; ++c) {
-      const int pl = c * 16 + (lane & 15);
-      float part = 0.f;
+    for (int r = 0; r < kRT; ++r)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (__attribute__((address_space(3))) void*)(wb + wofs + r * 1024),
+                                               16, live ? wsrc[r] + st * 1024u : kI8Skip, 0, 0, 0);
 #pragma unroll
-      for (int r = 0; r < HR; ++r) {
-        f32x4 gv = acc[r][c], uv = acc[r + HR][c];
-        if (WF == WF_I8) {
-          gv *= sg[r];
-          uv *= su[r];
-        }
-        u32x2 pk;
-        pk[0] = pack_bf16x2(silu_f32(gv[0]) * uv[0], silu_f32(gv[1]) * uv[1]);
-        pk[1] = pack_bf16x2(silu_f32(gv[2]) * uv[2], silu_f32(gv[3]) * uv[3]);
-        const f32x4 hb = bf16x4_to_f32(pk);
-        part += hb[0];
-        part += hb[1];
-        part += hb[2];
-        part += hb[3];
-        if (pl < rows) *(u32x2*)((uint16_t*)a.out + (int64_t)(row0 + pl) * a.I + hcol0 + r * 16 + rq) = pk;
-      }
-      // the 4 lanes holding one position's columns: fixed-order butterfly
-      part += __shfl_xor(part, 16);
-      part += __shfl_xor(part, 32);
-      if (lane < 16) hpart[wave][pl] = part;
-    }
-    if (a.hsum) {
-      __syncthreads();
-      if (tid < kBM && tid < rows) {
-        float s = hpart[0][tid];
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(tres, (__attribute__((address_space(3))) void*)(tb + tofs + j * 1024),
+                                               16, live ? tsrc[j] + st * (kI8Stage * 2u) : kI8Skip, 0, 0, 0);
+  };
+
+  f32x4 acc[kRT][kCT];
 #pragma unroll
-        for (int w = 1; w < kWaves; ++w) s += hpart[w][tid];
-        a.hsum[(int64_t)(row0 + tid) * (a.I / 128) + slab] = s;
-      }
-    }
-  } else {
+  for (int r = 0; r < kRT; ++r)
 #pragma unroll
-    for (int r = 0; r < kRT; ++r) {
-      f32x4 sr = f32x4{1.f, 1.f, 1.f, 1.f};
-      if (WF == WF_I8) sr = bf16x4_to_f32(*(const u32x2*)(sexp + wrow[r] + rq));
+    for (int c = 0; c < kCT; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // one stage's MFMA operands: this wave's 4 weight fragments (both 32-wide
+  // K steps) and the 2 x 4 token fragments
+  struct Frags {
+    u32x4 w[kRT];
+    u32x4 b[2][kCT];
+  };
+  auto read_frags = [&](Frags& f, const uint8_t* wb, const uint8_t* tb) {
+#pragma unroll
+    for (int r = 0; r < kRT; ++r) f.w[r] = *(const u32x4*)(wb + wofs + r * 1024 + lane * 16);
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int c = 0; c < kCT; ++c) {
-        const int pl = c * 16 + (lane & 15);
-        f32x4 v = acc[r][c];
-        if (WF == WF_I8) v *= sr;
-        if (pl < rows) *(f32x4*)((float*)a.out + (int64_t)(row0 + pl) * a.N + wrow[r] + rq) = v;
+        const int p = c * 16 + (lane & 15);
+        const int chunk = 4 * s + (lane >> 4);
+        f.b[s][c] = *(const u32x4*)(tb + p * (kI8Stage * 2) + ((chunk ^ ((p >> 1) & 7)) * 16));
       }
+  };
+  auto mma = [&](const Frags& f) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      u32x4 ad[kRT];
+#pragma unroll
+      for (int r = 0; r < kRT; ++r) ad[r] = dq_i8(f.w[r][2 * s], f.w[r][2 * s + 1]);
+#pragma unroll
+      for (int c = 0; c < kCT; ++c)
+#pragma unroll
+        for (int r = 0; r < kRT; ++r) acc[r][c] = mfma_bf16(ad[r], f.b[s][c], acc[r][c]);
     }
+  };
+
+  // Step x: stage x + 1's loads landed (this wave's: all but the newest 6,
+  // the loads of stage x + 2; then every wave's at the barrier, where every
+  // wave has also finished reading stage x from LDS); stage x + 3 starts
+  // loading into stage x's buffer; stage x + 1's fragments are read while
+  // stage x's MFMAs run.
+  Frags f0, f1;
+  auto step = [&](Frags& cur, Frags& nxt, uint8_t* wb_x, uint8_t* tb_x, const uint8_t* wb_n, const uint8_t* tb_n,
+                  int x) {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6)
+    lds_barrier();
+    issue(x + 3, wb_x, tb_x);
+    read_frags(nxt, wb_n, tb_n);
+    mma(cur);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  issue(0, wb0, tb0);
+  issue(1, wb1, tb1);
+  issue(2, wb2, tb2);
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F7C);  // vmcnt(12): stage 0 landed
+  lds_barrier();
+  read_frags(f0, wb0, tb0);
+  // six steps per iteration return the fragments and buffers to their
+  // starting roles; the last NS % 6 steps follow.  Every step issues 6
+  // loads, so "all but the newest 6" always means the next stage.
+  int x = 0;
+  for (; x + 6 <= NS; x += 6) {
+    step(f0, f1, wb0, tb0, wb1, tb1, x);
+    step(f1, f0, wb1, tb1, wb2, tb2, x + 1);
+    step(f0, f1, wb2, tb2, wb0, tb0, x + 2);
+    step(f1, f0, wb0, tb0, wb1, tb1, x + 3);
+    step(f0, f1, wb1, tb1, wb2, tb2, x + 4);
+    step(f1, f0, wb2, tb2, wb0, tb0, x + 5);
   }
+  const int rest = NS - x;
+  if (rest >= 1) step(f0, f1, wb0, tb0, wb1, tb1, x);
+  if (rest >= 2) step(f1, f0, wb1, tb1, wb2, tb2, x + 1);
+  if (rest >= 3) step(f0, f1, wb2, tb2, wb0, tb0, x + 2);
+  if (rest >= 4) step(f1, f0, wb0, tb0, wb1, tb1, x + 3);
+  if (rest >= 5) step(f0, f1, wb1, tb1, wb2, tb2, x + 4);
+  wait_vmem();  // out-of-range loads past the last stage land before the LDS is reused
+  __syncthreads();
+  gemm2_epilogue<WF_I8, PHASE, kWaves>(a, acc, srcl, hpart, xtot_l, wrow, sexp, it.row0, it.rows, it.slab);
 }
 
 // Per-row sums of each 128-wide K group of a bf16 matrix [rows, K] -> fp32
@@ -388,9 +591,16 @@ hipError_t launch_gemm2(const GemmArgs& a, int wf, int phase, int max_tiles, hip
     else                                                                                                   \
       launch_timed(gemm2_kernel<W, PHASE_DOWN, gemm2_waves(W)>, grid, block, 0, stream, tm, a, n_slabs);    \
     break;
+  // the int8 pipeline addresses its operands with 32-bit buffer offsets
+  if (wf == WF_I8 && a.in_bytes <= (int64_t)kI8Skip && (int64_t)a.N * a.K <= (int64_t)kI8Skip) {
+    if (phase == PHASE_GATE_UP)
+      launch_timed(gemm2_i8_kernel<PHASE_GATE_UP>, grid, block, 0, stream, tm, a, n_slabs);
+    else
+      launch_timed(gemm2_i8_kernel<PHASE_DOWN>, grid, block, 0, stream, tm, a, n_slabs);
+    return hipGetLastError();
+  }
   switch (wf) {
     NKT_G2(WF_BF16)
-    NKT_G2(WF_I8)
     NKT_G2(WF_I4)
     default:
       return hipErrorInvalidValue;

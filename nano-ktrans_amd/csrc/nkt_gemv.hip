@@ -73,24 +73,6 @@ __device__ __forceinline__ void load_w(WSlot<WF, NT>& r, const uint8_t* wexp, co
   }
 }
 
-// Direct-to-LDS loads (global_load_lds): lane l's 16 (4) bytes from src land
-// at dst + 16 l (dst + 4 l); dst must be the same in every lane.  Waited for
-// with the vector-memory counter.
-__device__ __forceinline__ void load16_to_lds(const void* src, uint8_t* dst) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
-}
-__device__ __forceinline__ void load4_to_lds(const void* src, uint8_t* dst) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
-}
-
-// Waits for every vector-memory load of this wave (direct-to-LDS ones
-// included) before the LDS is read.
-__device__ __forceinline__ void wait_vmem() {
-  __asm__ volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-  __asm__ volatile("" ::: "memory");
-}
-
 // B operand of group g, one load per MFMA step: lane l holds
 // x[row of column l%16][128g + 32s + 8(l/16) .. +7] in x[s].
 __device__ __forceinline__ void load_x_full(u32x4 (&x)[4], const uint8_t* xrow, int g) {

@@ -46,6 +46,7 @@ struct GemmArgs {
   float* hsum;             // prefill gate_up: group sums of the stored h [positions, I/128]
   const int32_t* tile_src; // decode gate_up: [max_tiles][kTileSrcCols] input row of each tile column
   int out_cols;            // decode down, > 0: store bf16 [rows, out_cols] (columns < out_cols)
+  int64_t in_bytes;        // extent of in: its rows x K x activation size
 };
 
 enum GemmPhase : int { PHASE_GATE_UP = 0, PHASE_DOWN = 1 };
@@ -107,7 +108,7 @@ bool gemv_supported(int wf, int phase, int N, int K, int I);
 hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream,
                        const KernelTimer* tm = nullptr);
 
-// Prefill form of K3 (tiles of 128 positions, bf16 / int8 / int4 weights).
+// Prefill form of K3 (tiles of 64 positions, bf16 / int8 / int4 weights).
 bool gemm2_supported(int wf, int phase, int N, int K, int I);
 hipError_t launch_gemm2(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream,
                         const KernelTimer* tm = nullptr);
