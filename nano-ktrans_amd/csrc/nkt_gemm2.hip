@@ -358,28 +358,30 @@ __global__ void __launch_bounds__(64 * kWaves, 2) gemm2_kernel(GemmArgs a, int n
 }
 
 // ---------------------------------------------------------------------------
-// int8 weights, three-stage direct-to-LDS pipeline.  Same tile, waves, work
-// order, MFMA sequence and epilogue as gemm2_kernel<WF_I8, ...> (so the
-// results are the same bit for bit), but both operands reach LDS by
-// direct-to-LDS loads (global_load_lds_dwordx4), no register staging, and K
-// advances in 64-wide stages through three LDS buffers, so two stages load
-// while one computes:
-//   * weights: each wave loads and reads only its own 4 row tiles, one 1 KiB
-//     block (16 rows x 64 K, lane l's MFMA fragments at 16 l) per row tile;
-//   * tokens: 64 positions x 128 B per stage, written by 8 loads of 8
-//     positions (2 per wave); lane l carries position 8 i + l / 8 into LDS
-//     slot l % 8 of that position's row, fetched from source chunk
-//     (l % 8) ^ ((position / 2) % 8): the MFMA operand reads of 16
-//     consecutive positions then cover all 64 LDS banks;
-//   * per stage a wave waits for its own loads of that stage (the next
-//     stage's 6 may stay in flight) and the workgroup meets at one
-//     LDS-only barrier, after which the buffer read two stages ago is
-//     refilled.
-// Six separate LDS objects: the compiler tells a direct-to-LDS load into one
-// buffer from reads of another and waits only where they alias.
+// int8 weights, three-stage pipeline.  Same tile, waves, work order, MFMA
+// sequence and epilogue as gemm2_kernel<WF_I8, ...> (so the results are the
+// same bit for bit); K advances in 64-wide stages:
+//   * weights: each wave's own 4 row tiles, one 1 KiB block (16 rows x 64 K,
+//     lane l's MFMA fragments at 16 l) per row tile, loaded by buffer loads
+//     straight into a ring of three register stages (the weights are private
+//     to the wave, so they never touch LDS);
+//   * tokens: 64 positions x 128 B per stage reach one of three LDS buffers
+//     by direct-to-LDS buffer loads (8 loads of 8 positions, 2 per wave);
+//     lane l carries position 8 i + l / 8 into LDS slot l % 8 of that
+//     position's row, fetched from source chunk (l % 8) ^ ((position / 2) % 8):
+//     the MFMA operand reads of 16 consecutive positions cover all 64 LDS
+//     banks;
+//   * step x: wait for this wave's loads of stage x + 1's tokens and stage
+//     x's weights, meet at one LDS-only barrier, start stage x + 3's tokens
+//     (into the buffer stage x was read from) and stage x + 2's weights,
+//     read stage x + 1's token fragments from LDS, run stage x's MFMAs.
+// Three separate LDS objects: the compiler tells a direct-to-LDS load into
+// one buffer from reads of another and waits only where they alias.  Loads
+// past the last stage use an out-of-range buffer offset: they read nothing
+// and keep the per-step load count (6) fixed, so the wait is always "all
+// but the newest 6".
 // ---------------------------------------------------------------------------
 constexpr int kI8Stage = 64;                   // K per stage
-constexpr int kI8WaveBytes = 4 * 1024;         // one wave's 4 weight blocks per stage
 constexpr int kI8TokBytes = kBM * kI8Stage * 2;
 constexpr uint32_t kI8Skip = 0xFFFFFF00u;     // a buffer offset past every range the kernel is given
 
@@ -387,9 +389,6 @@ template <int PHASE>
 __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slabs) {
   constexpr int kWaves = 4;
   constexpr int kRT = 4;
-  __shared__ __attribute__((aligned(1024))) uint8_t wb0[kWaves * kI8WaveBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t wb1[kWaves * kI8WaveBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t wb2[kWaves * kI8WaveBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t tb0[kI8TokBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t tb1[kI8TokBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t tb2[kI8TokBytes];
@@ -407,7 +406,7 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
   const uint16_t* sexp = a.scales + (int64_t)it.expert * a.s_expert_elems;
   const int NS = a.K / kI8Stage;  // stages = 1 KiB blocks per 16-row block
   // buffer resources over this expert's weights and the activation rows; a
-  // load at offset kI8Skip is out of range: it reads nothing and writes zeros
+  // load at offset kI8Skip is out of range: it reads nothing (zeros)
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(a.w + (int64_t)it.expert * a.w_expert_bytes), (short)0, a.N * a.K, 0x00020000);
   const __amdgpu_buffer_rsrc_t tres = __builtin_amdgcn_make_buffer_rsrc((void*)a.in, (short)0, a.in_bytes, 0x00020000);
@@ -428,21 +427,22 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
     const int chunk = (lane & 7) ^ ((p >> 1) & 7);
     tsrc[j] = (uint32_t)srcl[p] * (uint32_t)a.K * 2u + chunk * 16u;
   }
-  // this wave's slices of the buffers
-  const int wofs = wave * kI8WaveBytes;
-  const int tofs = wave * 2048;
+  const int tofs = wave * 2048;  // this wave's slice of a token buffer
 
-  // the 6 loads of stage st (st >= NS: out of range, no memory traffic)
-  auto issue = [&](int st, uint8_t* wb, uint8_t* tb) {
+  // stage st's 2 token loads into tb (st >= NS: out of range, no traffic)
+  auto issue_tok = [&](int st, uint8_t* tb) {
     const bool live = st < NS;
-#pragma unroll
-    for (int r = 0; r < kRT; ++r)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, (__attribute__((address_space(3))) void*)(wb + wofs + r * 1024),
-                                               16, live ? wsrc[r] + st * 1024u : kI8Skip, 0, 0, 0);
 #pragma unroll
     for (int j = 0; j < 2; ++j)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(tres, (__attribute__((address_space(3))) void*)(tb + tofs + j * 1024),
                                                16, live ? tsrc[j] + st * (kI8Stage * 2u) : kI8Skip, 0, 0, 0);
+  };
+  // stage st's 4 weight blocks into registers
+  auto issue_w = [&](int st, u32x4 (&w)[kRT]) {
+    const bool live = st < NS;
+#pragma unroll
+    for (int r = 0; r < kRT; ++r)
+      w[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, live ? wsrc[r] + st * 1024u : kI8Skip, 0, 0));
   };
 
   f32x4 acc[kRT][kCT];
@@ -451,79 +451,74 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
 #pragma unroll
     for (int c = 0; c < kCT; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // one stage's MFMA operands: this wave's 4 weight fragments (both 32-wide
-  // K steps) and the 2 x 4 token fragments
-  struct Frags {
-    u32x4 w[kRT];
-    u32x4 b[2][kCT];
-  };
-  auto read_frags = [&](Frags& f, const uint8_t* wb, const uint8_t* tb) {
-#pragma unroll
-    for (int r = 0; r < kRT; ++r) f.w[r] = *(const u32x4*)(wb + wofs + r * 1024 + lane * 16);
+  // one stage's token fragments (2 K steps x 4 column tiles)
+  typedef u32x4 TokFrags[2][kCT];
+  auto read_tok = [&](TokFrags& f, const uint8_t* tb) {
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int c = 0; c < kCT; ++c) {
         const int p = c * 16 + (lane & 15);
         const int chunk = 4 * s + (lane >> 4);
-        f.b[s][c] = *(const u32x4*)(tb + p * (kI8Stage * 2) + ((chunk ^ ((p >> 1) & 7)) * 16));
+        f[s][c] = *(const u32x4*)(tb + p * (kI8Stage * 2) + ((chunk ^ ((p >> 1) & 7)) * 16));
       }
   };
-  auto mma = [&](const Frags& f) {
+  auto mma = [&](const u32x4 (&w)[kRT], const TokFrags& f) {
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       u32x4 ad[kRT];
 #pragma unroll
-      for (int r = 0; r < kRT; ++r) ad[r] = dq_i8(f.w[r][2 * s], f.w[r][2 * s + 1]);
+      for (int r = 0; r < kRT; ++r) ad[r] = dq_i8(w[r][2 * s], w[r][2 * s + 1]);
 #pragma unroll
       for (int c = 0; c < kCT; ++c)
 #pragma unroll
-        for (int r = 0; r < kRT; ++r) acc[r][c] = mfma_bf16(ad[r], f.b[s][c], acc[r][c]);
+        for (int r = 0; r < kRT; ++r) acc[r][c] = mfma_bf16(ad[r], f[s][c], acc[r][c]);
     }
   };
 
-  // Step x: stage x + 1's loads landed (this wave's: all but the newest 6,
-  // the loads of stage x + 2; then every wave's at the barrier, where every
-  // wave has also finished reading stage x from LDS); stage x + 3 starts
-  // loading into stage x's buffer; stage x + 1's fragments are read while
-  // stage x's MFMAs run.
-  Frags f0, f1;
-  auto step = [&](Frags& cur, Frags& nxt, uint8_t* wb_x, uint8_t* tb_x, const uint8_t* wb_n, const uint8_t* tb_n,
-                  int x) {
+  TokFrags f0, f1;
+  u32x4 w0[kRT], w1[kRT], w2[kRT];
+  // issue order: T0, T1, W0, T2, W1, then per step x: T(x + 3), W(x + 2);
+  // at step x the newest 6 loads are T(x + 2) and W(x + 1), so waiting for
+  // all but 6 covers T(x + 1) and W(x)
+  auto step = [&](TokFrags& cur, TokFrags& nxt, const u32x4 (&wcur)[kRT], u32x4 (&wnew)[kRT], uint8_t* tb_x,
+                  const uint8_t* tb_n, int x) {
     __asm__ volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6)
     lds_barrier();
-    issue(x + 3, wb_x, tb_x);
-    read_frags(nxt, wb_n, tb_n);
-    mma(cur);
+    issue_tok(x + 3, tb_x);
+    issue_w(x + 2, wnew);
+    read_tok(nxt, tb_n);
+    mma(wcur, cur);
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  issue(0, wb0, tb0);
-  issue(1, wb1, tb1);
-  issue(2, wb2, tb2);
+  issue_tok(0, tb0);
+  issue_tok(1, tb1);
+  issue_w(0, w0);
+  issue_tok(2, tb2);
+  issue_w(1, w1);
   __asm__ volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0x0F7C);  // vmcnt(12): stage 0 landed
+  __builtin_amdgcn_s_waitcnt(0x0F7C);  // vmcnt(12): T0 landed
   lds_barrier();
-  read_frags(f0, wb0, tb0);
-  // six steps per iteration return the fragments and buffers to their
-  // starting roles; the last NS % 6 steps follow.  Every step issues 6
-  // loads, so "all but the newest 6" always means the next stage.
+  read_tok(f0, tb0);
+  // six steps per iteration return fragments, weight registers and buffers
+  // to their starting roles; the last NS % 6 steps follow
   int x = 0;
   for (; x + 6 <= NS; x += 6) {
-    step(f0, f1, wb0, tb0, wb1, tb1, x);
-    step(f1, f0, wb1, tb1, wb2, tb2, x + 1);
-    step(f0, f1, wb2, tb2, wb0, tb0, x + 2);
-    step(f1, f0, wb0, tb0, wb1, tb1, x + 3);
-    step(f0, f1, wb1, tb1, wb2, tb2, x + 4);
-    step(f1, f0, wb2, tb2, wb0, tb0, x + 5);
+    step(f0, f1, w0, w2, tb0, tb1, x);
+    step(f1, f0, w1, w0, tb1, tb2, x + 1);
+    step(f0, f1, w2, w1, tb2, tb0, x + 2);
+    step(f1, f0, w0, w2, tb0, tb1, x + 3);
+    step(f0, f1, w1, w0, tb1, tb2, x + 4);
+    step(f1, f0, w2, w1, tb2, tb0, x + 5);
   }
   const int rest = NS - x;
-  if (rest >= 1) step(f0, f1, wb0, tb0, wb1, tb1, x);
-  if (rest >= 2) step(f1, f0, wb1, tb1, wb2, tb2, x + 1);
-  if (rest >= 3) step(f0, f1, wb2, tb2, wb0, tb0, x + 2);
-  if (rest >= 4) step(f1, f0, wb0, tb0, wb1, tb1, x + 3);
-  if (rest >= 5) step(f0, f1, wb1, tb1, wb2, tb2, x + 4);
+  if (rest >= 1) step(f0, f1, w0, w2, tb0, tb1, x);
+  if (rest >= 2) step(f1, f0, w1, w0, tb1, tb2, x + 1);
+  if (rest >= 3) step(f0, f1, w2, w1, tb2, tb0, x + 2);
+  if (rest >= 4) step(f1, f0, w0, w2, tb0, tb1, x + 3);
+  if (rest >= 5) step(f0, f1, w1, w0, tb1, tb2, x + 4);
   wait_vmem();  // out-of-range loads past the last stage land before the LDS is reused
   __syncthreads();
   gemm2_epilogue<WF_I8, PHASE, kWaves>(a, acc, srcl, hpart, xtot_l, wrow, sexp, it.row0, it.rows, it.slab);
