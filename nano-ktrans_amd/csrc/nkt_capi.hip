@@ -28,7 +28,9 @@ constexpr int kWsHsum = NKT_WS_NUM_REGIONS + 3;    // fp32 [T*k, I/128] group su
 constexpr int kWsShHsum = NKT_WS_NUM_REGIONS + 4;  // fp32 [T, I_s/128] group sums of the shared h
 constexpr int kWsHist = NKT_WS_NUM_REGIONS + 5;   // int32 [blocks, E] per-block expert histograms
 constexpr int kWsTileSrc = NKT_WS_NUM_REGIONS + 6; // int32 [max_tiles, 16] decode tiles' input rows
-constexpr int kWsAll = NKT_WS_NUM_REGIONS + 7;
+constexpr int kWsX16 = NKT_WS_NUM_REGIONS + 7;     // fp16 [T, H] scaled copy of x (int8 prefill gate_up)
+constexpr int kWsXInv = NKT_WS_NUM_REGIONS + 8;    // fp32 [T] 1 / scale of each row of that copy
+constexpr int kWsAll = NKT_WS_NUM_REGIONS + 9;
 
 void set_err(char* err, size_t len, const char* fmt, ...) {
   if (!err || len == 0) return;
@@ -112,6 +114,10 @@ bool prefill_form_ok(const Handle* h, bool shared) {
 
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// int8 weights with bf16 activations: the prefill gate_up runs on the fp16
+// matrix cores from a power-of-two-scaled fp16 copy of x (H <= 4096)
+bool int8_f16_input(const Handle* h) { return h->wf == WF_I8 && h->act_bf16 && h->H <= 4096; }
+
 WsLayout ws_layout(const Handle* h, int T) {
   WsLayout L;
   const size_t P = (size_t)T * h->k;
@@ -147,6 +153,9 @@ WsLayout ws_layout(const Handle* h, int T) {
   sz[kWsShHsum] = h->Is > 0 ? (size_t)T * (h->Is / 128) * 4 : 0;
   sz[kWsHist] = (size_t)group_hist_blocks((int)P) * h->E * 4;
   sz[kWsTileSrc] = L.bm == kTileSrcCols ? (size_t)L.max_tiles * kTileSrcCols * 4 : 0;
+  const bool x16 = int8_f16_input(h);
+  sz[kWsX16] = x16 ? (size_t)T * h->H * 2 : 0;
+  sz[kWsXInv] = x16 ? (size_t)T * 4 : 0;
   size_t o = 0;
   for (int i = 0; i < kWsAll; ++i) {
     L.off[i] = o;
@@ -249,6 +258,10 @@ GemmArgs expert_args(const Handle* h, int phase, bool shared, const void* in, vo
   }
   const int64_t in_rows = (!shared && phase == PHASE_GATE_UP) ? T : a.num_rows;
   a.in_bytes = in_rows * K * (h->act_bf16 ? 2 : 4);
+  if (phase == PHASE_GATE_UP && int8_f16_input(h)) {
+    a.in16 = ws_ptr<uint16_t>(ws, L, kWsX16);
+    a.xinv = ws_ptr<float>(ws, L, kWsXInv);
+  }
   return a;
 }
 
@@ -329,12 +342,20 @@ hipError_t launch_expert_gemm(const Handle* h, const GemmArgs& a, int phase, int
                               hipStream_t st, const KernelTimer* tm = nullptr) {
   if (bm == 16 && gemv_supported(h->wf, phase, a.N, a.K, a.I)) return launch_gemv(a, h->wf, phase, tiles, st, tm);
   if (bm == kPrefillTileM && gemm2_supported(h->wf, phase, a.N, a.K, a.I)) {
+    GemmArgs b = a;
     if (phase == PHASE_GATE_UP && (h->wf == WF_I4 || h->wf == WF_I8)) {
-      const hipError_t e = launch_group_sums(a.in, (a.perm ? a.num_rows / a.topk : a.num_rows), a.K,
-                                             const_cast<float*>(a.xsum), st);
+      const int rows_in = a.perm ? a.num_rows / a.topk : a.num_rows;
+      hipError_t e;
+      if (a.in16 && a.xinv && gemm2_i8_pipeline(a, h->wf)) {
+        e = launch_prep_f16(a.in, rows_in, a.K, const_cast<float*>(a.xsum), a.in16, a.xinv, st);
+        b.in = a.in16;
+      } else {
+        e = launch_group_sums(a.in, rows_in, a.K, const_cast<float*>(a.xsum), st);
+        b.xinv = nullptr;
+      }
       if (e != hipSuccess) return e;
     }
-    return launch_gemm2(a, h->wf, phase, tiles, st, tm);
+    return launch_gemm2(b, h->wf, phase, tiles, st, tm);
   }
   return launch_gemm(a, h->wf, phase, bm, tiles, st, tm);
 }

@@ -200,6 +200,13 @@ __device__ __forceinline__ u32x4 dq_i8(uint32_t w0, uint32_t w1) {
   return a;
 }
 
+// int8 for the fp16 matrix cores: stored byte u -> fp16 1024 + u (bits
+// 0x6400 | u, exact), one byte permute per pair; same element order as dq_i8.
+__device__ __forceinline__ u32x4 dq_i8_f16(uint32_t w0, uint32_t w1) {
+  return u32x4{__builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u),
+               __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u), __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u)};
+}
+
 __device__ __forceinline__ f32x4 bf16x4_to_f32(u32x2 v) {
   return f32x4{__uint_as_float(v[0] << 16), __uint_as_float(v[0] & 0xffff0000u),
                __uint_as_float(v[1] << 16), __uint_as_float(v[1] & 0xffff0000u)};
@@ -246,6 +253,12 @@ __device__ __forceinline__ void wait_vmem() {
 __device__ __forceinline__ f32x4 mfma_bf16(u32x4 a, u32x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x4 mfma_f16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                 0, 0);
 }
 
 __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {

@@ -96,9 +96,12 @@ __device__ __forceinline__ void gemm2_sources(const GemmArgs& a, const TileItem&
 // Epilogue of the prefill form (shared by its kernels): int8 code offset,
 // per-row scales, then gate_up SwiGLU -> bf16 h (+ h's group sums) or down
 // fp32 y.  acc[r][c]: this wave's row tile r x column tile c.
-template <int WF, int PHASE, int kWaves>
+// XS (int8 gate_up on the fp16 matrix cores): acc holds sum (1024 + u) x / s
+// for the input rows scaled by s; it is rescaled per position and the code
+// offset is 1152 (1024 + 128).
+template <int WF, int PHASE, int kWaves, bool XS = false>
 __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[16 / kWaves][kCT], const int* srcl,
-                                               float (*hpart)[kBM], float* xtot_l, const int* wrow,
+                                               float (*hpart)[kBM], float* xtot_l, float* xinv_l, const int* wrow,
                                                const uint16_t* sexp, int row0, int rows, int slab) {
   constexpr int kRT = 16 / kWaves;
   const int tid = threadIdx.x;
@@ -113,13 +116,20 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[1
       float t = 0.f;
       for (int g = 0; g < G; ++g) t += xr[g];
       xtot_l[tid] = t;
+      if (XS) xinv_l[tid] = a.xinv[srcl[tid]];
     }
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < kCT; ++c) {
-      const float cv = -128.0f * xtot_l[c * 16 + (lane & 15)];
+      const float cv = (XS ? -1152.0f : -128.0f) * xtot_l[c * 16 + (lane & 15)];
+      const float xi = XS ? xinv_l[c * 16 + (lane & 15)] : 1.0f;
 #pragma unroll
-      for (int r = 0; r < kRT; ++r) acc[r][c] += f32x4{cv, cv, cv, cv};
+      for (int r = 0; r < kRT; ++r) {
+        if (XS)
+          acc[r][c] = acc[r][c] * xi + f32x4{cv, cv, cv, cv};
+        else
+          acc[r][c] += f32x4{cv, cv, cv, cv};
+      }
     }
   }
   if (PHASE == PHASE_GATE_UP) {
@@ -354,7 +364,7 @@ __global__ void __launch_bounds__(64 * kWaves, 2) gemm2_kernel(GemmArgs a, int n
   }
   __syncthreads();
 
-  gemm2_epilogue<WF, PHASE, kWaves>(a, acc, srcl, hpart, xtot_l, wrow, sexp, row0, rows, slab);
+  gemm2_epilogue<WF, PHASE, kWaves>(a, acc, srcl, hpart, xtot_l, xtot_l, wrow, sexp, row0, rows, slab);
 }
 
 // ---------------------------------------------------------------------------
@@ -385,7 +395,7 @@ constexpr int kI8Stage = 64;                   // K per stage
 constexpr int kI8TokBytes = kBM * kI8Stage * 2;
 constexpr uint32_t kI8Skip = 0xFFFFFF00u;     // a buffer offset past every range the kernel is given
 
-template <int PHASE>
+template <int PHASE, bool F16>
 __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slabs) {
   constexpr int kWaves = 4;
   constexpr int kRT = 4;
@@ -395,6 +405,7 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
   __shared__ int srcl[kBM];
   __shared__ float hpart[kWaves][kBM];
   __shared__ float xtot_l[kBM];
+  __shared__ float xinv_l[kBM];
 
   TileItem it;
   if (!gemm2_item(a, n_slabs, it)) return;
@@ -468,11 +479,12 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
     for (int s = 0; s < 2; ++s) {
       u32x4 ad[kRT];
 #pragma unroll
-      for (int r = 0; r < kRT; ++r) ad[r] = dq_i8(w[r][2 * s], w[r][2 * s + 1]);
+      for (int r = 0; r < kRT; ++r) ad[r] = F16 ? dq_i8_f16(w[r][2 * s], w[r][2 * s + 1]) : dq_i8(w[r][2 * s], w[r][2 * s + 1]);
 #pragma unroll
       for (int c = 0; c < kCT; ++c)
 #pragma unroll
-        for (int r = 0; r < kRT; ++r) acc[r][c] = mfma_bf16(ad[r], f[s][c], acc[r][c]);
+        for (int r = 0; r < kRT; ++r)
+          acc[r][c] = F16 ? mfma_f16(ad[r], f[s][c], acc[r][c]) : mfma_bf16(ad[r], f[s][c], acc[r][c]);
     }
   };
 
@@ -521,7 +533,7 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
   if (rest >= 5) step(f0, f1, w1, w0, tb1, tb2, x + 4);
   wait_vmem();  // out-of-range loads past the last stage land before the LDS is reused
   __syncthreads();
-  gemm2_epilogue<WF_I8, PHASE, kWaves>(a, acc, srcl, hpart, xtot_l, wrow, sexp, it.row0, it.rows, it.slab);
+  gemm2_epilogue<WF_I8, PHASE, kWaves, F16>(a, acc, srcl, hpart, xtot_l, xinv_l, wrow, sexp, it.row0, it.rows, it.slab);
 }
 
 // Per-row sums of each 128-wide K group of a bf16 matrix [rows, K] -> fp32
@@ -553,10 +565,93 @@ __global__ void __launch_bounds__(256) group_sums_kernel(const uint16_t* __restr
   }
 }
 
+// the int8 pipeline addresses its operands with 32-bit buffer offsets
+bool gemm2_i8_pipeline(const GemmArgs& a, int wf) {
+  return wf == WF_I8 && a.in_bytes <= (int64_t)kI8Skip && (int64_t)a.N * a.K <= (int64_t)kI8Skip;
+}
+
 bool gemm2_supported(int wf, int phase, int N, int K, int I) {
   if (wf != WF_BF16 && wf != WF_I8 && wf != WF_I4) return false;
   if (K % 128 != 0) return false;
   return phase == PHASE_GATE_UP ? (I % 128 == 0) : (N % 256 == 0);
+}
+
+// Input of the int8 gate_up on the fp16 matrix cores, one wave per row: the
+// group sums exactly as group_sums_kernel, and the row times s = 2^(15 - E)
+// rounded to fp16, where the row's largest |x| is f 2^E with f in [0.5, 1)
+// (s = 1 for an all-zero or non-finite row).  The scaled maximum lies in
+// [2^14, 2^15), and every bf16 value down to 2^-32 of it is exact in fp16
+// (normal down to 2^-14, subnormal with 8 significant bits down to 2^-17).
+// xinv = 1 / s.  Lane l holds 8 values of group 4c + l / 16 per chunk c.
+template <int NCH>
+__global__ void __launch_bounds__(256) prep_f16_kernel(const uint16_t* __restrict__ x, int rows, int K,
+                                                       float* __restrict__ sums, uint16_t* __restrict__ x16,
+                                                       float* __restrict__ xinv) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const uint16_t* xr = x + (int64_t)row * K;
+  const int G = K / 128;
+  u32x4 v[NCH];
+  float m = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int g = 4 * c + (lane >> 4);
+    v[c] = u32x4{0u, 0u, 0u, 0u};
+    if (g < G) v[c] = *(const u32x4*)(xr + g * 128 + (lane & 15) * 8);
+    float s = 0.f;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const float lo = __uint_as_float(v[c][h] << 16), hi = __uint_as_float(v[c][h] & 0xffff0000u);
+      s += lo;
+      s += hi;
+      m = fmaxf(m, fmaxf(fabsf(lo), fabsf(hi)));
+    }
+    s += __shfl_xor(s, 8);
+    s += __shfl_xor(s, 4);
+    s += __shfl_xor(s, 2);
+    s += __shfl_xor(s, 1);
+    if ((lane & 15) == 0 && g < G) sums[(int64_t)row * G + g] = s;
+  }
+  m = wave_max(m);
+  int e = 0;
+  if (m > 0.f && m <= 3.402823466e38f) {
+    int E;
+    frexpf(m, &E);
+    e = min(max(15 - E, -126), 126);
+  }
+  const float sc = __builtin_ldexpf(1.0f, e);
+  uint16_t* xo = x16 + (int64_t)row * K;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int g = 4 * c + (lane >> 4);
+    if (g >= G) continue;
+    u32x4 o;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const _Float16 lo = (_Float16)(__uint_as_float(v[c][h] << 16) * sc);
+      const _Float16 hi = (_Float16)(__uint_as_float(v[c][h] & 0xffff0000u) * sc);
+      o[h] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+    }
+    *(u32x4*)(xo + g * 128 + (lane & 15) * 8) = o;
+  }
+  if (lane == 0) xinv[row] = __builtin_ldexpf(1.0f, -e);
+}
+
+hipError_t launch_prep_f16(const void* x, int rows, int K, float* sums, uint16_t* x16, float* xinv,
+                           hipStream_t stream) {
+  if (rows <= 0) return hipSuccess;
+  if (K % 128 != 0 || K > 4096) return hipErrorInvalidValue;
+  const dim3 grid((rows + 3) / 4), block(256);
+  const uint16_t* xb = (const uint16_t*)x;
+  switch ((K + 511) / 512) {
+    case 1: hipLaunchKernelGGL(prep_f16_kernel<1>, grid, block, 0, stream, xb, rows, K, sums, x16, xinv); break;
+    case 2: hipLaunchKernelGGL(prep_f16_kernel<2>, grid, block, 0, stream, xb, rows, K, sums, x16, xinv); break;
+    case 3:
+    case 4: hipLaunchKernelGGL(prep_f16_kernel<4>, grid, block, 0, stream, xb, rows, K, sums, x16, xinv); break;
+    default: hipLaunchKernelGGL(prep_f16_kernel<8>, grid, block, 0, stream, xb, rows, K, sums, x16, xinv); break;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_group_sums(const void* x, int rows, int K, float* out, hipStream_t stream) {
@@ -586,12 +681,13 @@ hipError_t launch_gemm2(const GemmArgs& a, int wf, int phase, int max_tiles, hip
     else                                                                                                   \
       launch_timed(gemm2_kernel<W, PHASE_DOWN, gemm2_waves(W)>, grid, block, 0, stream, tm, a, n_slabs);    \
     break;
-  // the int8 pipeline addresses its operands with 32-bit buffer offsets
-  if (wf == WF_I8 && a.in_bytes <= (int64_t)kI8Skip && (int64_t)a.N * a.K <= (int64_t)kI8Skip) {
-    if (phase == PHASE_GATE_UP)
-      launch_timed(gemm2_i8_kernel<PHASE_GATE_UP>, grid, block, 0, stream, tm, a, n_slabs);
+  if (gemm2_i8_pipeline(a, wf)) {
+    if (phase == PHASE_GATE_UP && a.xinv)
+      launch_timed(gemm2_i8_kernel<PHASE_GATE_UP, true>, grid, block, 0, stream, tm, a, n_slabs);
+    else if (phase == PHASE_GATE_UP)
+      launch_timed(gemm2_i8_kernel<PHASE_GATE_UP, false>, grid, block, 0, stream, tm, a, n_slabs);
     else
-      launch_timed(gemm2_i8_kernel<PHASE_DOWN>, grid, block, 0, stream, tm, a, n_slabs);
+      launch_timed(gemm2_i8_kernel<PHASE_DOWN, false>, grid, block, 0, stream, tm, a, n_slabs);
     return hipGetLastError();
   }
   switch (wf) {

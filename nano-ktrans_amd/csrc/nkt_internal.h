@@ -47,6 +47,10 @@ struct GemmArgs {
   const int32_t* tile_src; // decode gate_up: [max_tiles][kTileSrcCols] input row of each tile column
   int out_cols;            // decode down, > 0: store bf16 [rows, out_cols] (columns < out_cols)
   int64_t in_bytes;        // extent of in: its rows x K x activation size
+  // prefill int8 gate_up on the fp16 matrix cores: destination of the
+  // power-of-two-scaled fp16 copy of in, and per input row 1 / scale
+  uint16_t* in16;
+  float* xinv;
 };
 
 enum GemmPhase : int { PHASE_GATE_UP = 0, PHASE_DOWN = 1 };
@@ -114,6 +118,13 @@ hipError_t launch_gemm2(const GemmArgs& a, int wf, int phase, int max_tiles, hip
                         const KernelTimer* tm = nullptr);
 // fp32 sums of every 128-wide K group of the rows of a bf16 matrix [rows, K]
 hipError_t launch_group_sums(const void* x, int rows, int K, float* out, hipStream_t stream);
+// the same sums, plus the fp16 copy of each row scaled by a power of two
+// (x16, same layout) and 1 / scale per row (xinv); K <= 4096
+hipError_t launch_prep_f16(const void* x, int rows, int K, float* sums, uint16_t* x16, float* xinv,
+                           hipStream_t stream);
+// whether launch_gemm2 runs a on the int8 pipeline kernel (which then takes
+// gate_up's input as the fp16 copy when a.xinv is set)
+bool gemm2_i8_pipeline(const GemmArgs& a, int wf);
 
 // Repack [N, K] into the block layout; rows >= n_valid (bf16 only) are zero
 // and not read (n_valid < 0: all N rows).

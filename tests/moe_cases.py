@@ -7,6 +7,8 @@ Shapes and seeds:
   mixtral_int4       H=4096 E=8   k=2 I=14336 bf16 act, int4 g128, top-k on logits then softmax, seed 2
   qwen15_int8_shared H=2048 E=60  k=4 I=1408  shared I=5632 + sigmoid gate, int8 per-channel,
                      softmax without renorm, seed 3
+  small_int8_shared  H=256  E=8   k=2 I=128   shared I=128, int8 per-channel, softmax+renorm, seed 4
+                     (prefill-form K loops of 4 and 2 stages)
 Activations ~N(0,1); router and expert weights ~N(0, 0.02); router logits are
 x . router^T in fp32, then cast to the activation dtype.
 """
@@ -52,6 +54,9 @@ CONFIGS = {
     "mixtral_int4": MoEConfig("mixtral_int4", 4096, 8, 2, 14336, 0, False, True, "bf16", "int4_g128", 2),
     "qwen15_int8_shared": MoEConfig("qwen15_int8_shared", 2048, 60, 4, 1408, 5632, True, False, "bf16",
                                     "int8_per_channel", 3),
+    # K of 256 / 128: the prefill form's K loop is only its last, partial round
+    "small_int8_shared": MoEConfig("small_int8_shared", 256, 8, 2, 128, 128, True, True, "bf16",
+                                   "int8_per_channel", 4),
 }
 
 

@@ -135,6 +135,13 @@ def test_mixtral_int4_cut_intermediate_prefill(gpu_device):
     _check(layer, native, 300)
 
 
+@pytest.mark.parametrize("T", [40, 600])
+def test_small_int8_short_k(gpu_device, T):
+    announce(f"forward small_int8_shared T={T}")
+    layer, native = _layer("small_int8_shared")
+    _check(layer, native, T)
+
+
 @pytest.mark.parametrize("T", [1, 16, 200])
 def test_qwen15_shared_full(gpu_device, T):
     announce(f"forward qwen15_int8_shared full T={T}")
