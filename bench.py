@@ -285,7 +285,9 @@ def kernel_form(w, T):
     avg = T * w.k / w.E
     if avg <= 12:
         return "gemv_kernel"
-    return "gemm2_kernel" if w.wfmt != "f32" else "gemm_kernel"
+    if w.wfmt == "f32":
+        return "gemm_kernel"
+    return "gemm2_i8_kernel" if w.wfmt == "int8_per_channel" else "gemm2_kernel"
 
 
 def bench_workload(w, T, layers, router, steps, warmup, device):
