@@ -56,10 +56,12 @@ __device__ __forceinline__ void wave_lds_sync() {
 // Route one token with the whole wavefront.  sv/si: this wave's 16-entry LDS
 // scratch (selected values / ids in slot order).  Returns, in lanes < k, the
 // slot's expert id and weight; lanes >= k return id -1.
+// selmask (nullable, LDS): the token's selected experts as a bit mask, bit
+// e of 32-bit word e / 32, written by lane 0.
 template <int VPL, bool BF16>
 __device__ __forceinline__ void route_token(const void* __restrict__ logits, int t, int E, int k,
                                             unsigned flags, float* sv, int* si, int* out_id,
-                                            float* out_w) {
+                                            float* out_w, uint32_t* selmask = nullptr) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   float v[VPL];
@@ -138,6 +140,10 @@ __device__ __forceinline__ void route_token(const void* __restrict__ logits, int
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const uint64_t m = ballot64(sel[j]);
+    if (selmask && lane == 0) {
+      selmask[2 * j] = (uint32_t)m;
+      selmask[2 * j + 1] = (uint32_t)(m >> 32);
+    }
     if (sel[j]) {
       const int c = before + lanes_below(m);
       sv[c] = v[j];
@@ -217,155 +223,114 @@ __global__ void __launch_bounds__(256) route_kernel(const void* __restrict__ log
 }
 
 // ---------------------------------------------------------------------------
-// K2 for small batches: one workgroup of 16 waves groups the P = T*k pairs
-// (P <= kFusedRouteMaxPairs) whose expert ids sit in LDS.  Thread t owns
-// (expert e, part q) = (t / NP, t % NP): the pairs are cut into NP equal
-// consecutive parts and the thread counts the pairs of its part that go to
-// its expert.  An expert's NP counts sit in neighbouring lanes, so its total
-// takes a few DPP adds; one workgroup prefix sum over the threads, in
-// (expert, part) order, of count | tiles << 16 then gives every thread the
-// first position of its pairs inside the expert's segment and every expert
-// its first tile.  A second walk over the part writes perm / inv / tile
-// sources in pair order (stable in token order, independent of scheduling);
-// the expert's lanes write its tile records.  Two workgroup barriers in all.
+// K2 for small batches (T <= 64), one wave, from the selection masks K1
+// leaves in LDS (token t's experts as bits of selmask[t]).  A token picks an
+// expert at most once, so expert e's pairs are the set bits of a 64-bit
+// token mask M_e (bit t: token t picked e); lane l owns the VPL consecutive
+// experts VPL l .. VPL l + VPL - 1:
+//   * M_e by transposing the token masks (T words read per lane, one bit
+//     field extract and insert per token and expert);
+//   * count_e = popcount(M_e), tiles_e = ceil(count_e / bm) (0 when e is not
+//     HBM-resident); one wave scan of count | tiles << 16 in expert order
+//     gives every expert its first position and first tile;
+//   * expert lanes write counts, offsets, tile records and the tiles'
+//     source columns (the set bits of M_e in ascending order);
+//   * pair p = t k + slot with expert e lands at position
+//     off_e + popcount(M_e & (2^t - 1)): tokens ascend within an expert, as
+//     the reference's stable grouping orders them.
 // ---------------------------------------------------------------------------
-constexpr int kGroupWaves = 16;
+constexpr int kGroupWaves = 16;  // waves of the fused route + group workgroup
 constexpr int kGroupThreads = 64 * kGroupWaves;
 
-// parts per expert: NP lanes of one expert share a 16-lane row
-__host__ __device__ constexpr int group_parts(int E) {
-  int epad = 1;
-  while (epad < E) epad <<= 1;
-  const int np = kGroupThreads / epad;
-  return np < 16 ? np : 16;
-}
-
-// Sum over the aligned group of NP (1, 2, 4, 8 or 16) neighbouring lanes,
-// in every lane of the group.
-__device__ __forceinline__ int group_lane_sum(int v, int np) {
-  if (np >= 2) v += (int)dpp_u32<0xB1>((uint32_t)v);   // quad_perm [1,0,3,2]: lane ^ 1
-  if (np >= 4) v += (int)dpp_u32<0x4E>((uint32_t)v);   // quad_perm [2,3,0,1]: lane ^ 2
-  if (np >= 8) v += (int)dpp_u32<0x141>((uint32_t)v);  // row_half_mirror: the other quad
-  if (np >= 16) v += (int)dpp_u32<0x140>((uint32_t)v); // row_mirror: the other half row
-  return v;
-}
-
-// Bit i of the result: pair p + i (i < n <= 64) goes to expert e.
-__device__ __forceinline__ uint64_t pair_match_mask(const int32_t* ids, int p, int n, int e) {
-  uint32_t lo = 0, hi = 0;
-  for (int i = 0; i < n; i += 4) {
-    const int4 g = *(const int4*)(ids + p + i);
-    const uint32_t b = (uint32_t)(g.x == e) | ((uint32_t)(g.y == e) << 1) | ((uint32_t)(g.z == e) << 2) |
-                       ((uint32_t)(g.w == e) << 3);
-    if (i < 32)
-      lo |= b << i;
-    else
-      hi |= b << (i - 32);
-  }
-  const uint64_t m = ((uint64_t)hi << 32) | lo;
-  return n >= 64 ? m : m & ((1ull << n) - 1);
-}
-
-// ids: LDS, 16-byte aligned, at least P rounded up to 4 entries readable.
-// res_ok: this thread's expert is HBM-resident (loaded by the caller early).
-// bm: a power of two (kTileSrcCols when tile_src is given).
-__device__ __forceinline__ void group_small(const int32_t* ids, int T, int k, int E, int bm,
-                                            int max_tiles, bool res_ok, int32_t* __restrict__ counts,
+// selmask: [T][8] u32 words (LDS); ids: the P = T k expert ids (LDS);
+// mlo/mhi/offl: LDS scratch of at least E entries; res: this lane's experts
+// are HBM-resident (bit i for expert VPL lane + i).  Runs in one wave.
+template <int VPL>
+__device__ __forceinline__ void group_masks(const uint32_t (*selmask)[8], const int32_t* ids, int T, int k, int E,
+                                            int bm, int max_tiles, unsigned res, int32_t* __restrict__ counts,
                                             int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
                                             int32_t* __restrict__ inv, int32_t* __restrict__ tiles,
                                             int32_t* __restrict__ n_tiles, int32_t* __restrict__ tile_src,
-                                            int32_t* wave_tot) {
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
+                                            uint32_t* mlo, uint32_t* mhi, int32_t* offl) {
+  const int lane = threadIdx.x & 63;
   const int P = T * k;
-  const int np = group_parts(E);  // a power of two
-  const int lg_np = __builtin_ctz(np);
-  const int e = tid >> lg_np;
-  const int q = tid & (np - 1);
-  const bool own = e < E;
-  const int chunk = (((P + np - 1) >> lg_np) + 3) & ~3;
-  const int pb = min(P, q * chunk);
-  const int pe = min(P, pb + chunk);
-
-  // pass 1: pairs of this part that go to e, as bit masks of 64-pair windows
-  // (the first window's mask is kept for pass 2)
-  int cnt = 0;
-  uint64_t m_first = 0;
-  if (own) {
-    for (int p = pb; p < pe; p += 64) {
-      const uint64_t m = pair_match_mask(ids, p, min(64, pe - p), e);
-      if (p == pb) m_first = m;
-      cnt += __popcll(m);
-    }
-  }
-  const int tot = group_lane_sum(cnt, np);
-  const int nt = (own && res_ok) ? (tot + bm - 1) >> __builtin_ctz(bm) : 0;  // non-resident: no tiles
-
-  // workgroup exclusive prefix of (pairs | tiles << 16) in (expert, part) order
-  const int val = own ? (cnt | ((q == 0 ? nt : 0) << 16)) : 0;
-  const int incl = wave_inclusive_scan(val);
-  if (lane == 63) wave_tot[wave] = incl;
-  __syncthreads();
-  int base = 0, total = 0;
+  const int lg_bm = __builtin_ctz(bm);
+  // token masks of this lane's experts
+  uint32_t lo[VPL], hi[VPL];
 #pragma unroll
-  for (int w = 0; w < kGroupWaves; ++w) {
-    const int x = wave_tot[w];
-    base += (w < wave) ? x : 0;
-    total += x;
+  for (int i = 0; i < VPL; ++i) lo[i] = hi[i] = 0u;
+  for (int t = 0; t < T; ++t) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int e = VPL * lane + i;
+      const uint32_t b = (selmask[t][(e >> 5) & 7] >> (e & 31)) & 1u;
+      if (t < 32)
+        lo[i] |= b << t;
+      else
+        hi[i] |= b << (t - 32);
+    }
   }
-  const int excl = base + incl - val;
-  const int pos0 = excl & 0xffff;                      // first position of this part's pairs
-  const int off_e = __shfl(pos0, lane & ~(np - 1));    // the expert's first position
-  const int toff_e = (excl >> 16) - (q > 0 ? nt : 0);  // the expert's first tile
-  const int n_pairs = total & 0xffff;
-  const int n_tile_all = total >> 16;
+  int cnt[VPL], nt[VPL];
+  int lane_val = 0;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int e = VPL * lane + i;
+    const bool own = e < E;
+    if (!own) lo[i] = hi[i] = 0u;
+    cnt[i] = __popc(lo[i]) + __popc(hi[i]);
+    nt[i] = (own && ((res >> i) & 1u)) ? (cnt[i] + bm - 1) >> lg_bm : 0;
+    lane_val += cnt[i] | (nt[i] << 16);
+  }
+  const int incl = wave_inclusive_scan(lane_val);
+  const int n_tile_all = __builtin_amdgcn_readlane(incl, 63) >> 16;
+  int run = incl - lane_val;  // this lane's first (position | tile << 16)
 
-  // pass 2: positions in pair order, one iteration per matching pair; the
-  // token of pair p is p / k = (p * ceil(2^32 / k)) >> 32 (exact for p < 2^16)
-  if (cnt > 0) {
-    const uint64_t kmagic = ((1ull << 32) + (uint64_t)k - 1) / (uint64_t)k;
-    int pos = pos0;
-    for (int p = pb; p < pe; p += 64) {
-      uint64_t m = (p == pb) ? m_first : pair_match_mask(ids, p, min(64, pe - p), e);
-      while (m) {
-        const int pp = p + __builtin_ctzll(m);
-        m &= m - 1;
-        perm[pos] = pp;
-        inv[pp] = pos;
-        if (tile_src && nt > 0) {
-          const int rel = pos - off_e;
-          const int ti = toff_e + rel / kTileSrcCols;
-          if (ti < max_tiles) tile_src[ti * kTileSrcCols + rel % kTileSrcCols] = (int)(((uint64_t)pp * kmagic) >> 32);
-        }
-        ++pos;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int e = VPL * lane + i;
+    const int off = run & 0xffff, toff = run >> 16;
+    run += cnt[i] | (nt[i] << 16);
+    if (e >= E) continue;
+    counts[e] = cnt[i];
+    offsets[e] = off;
+    mlo[e] = lo[i];
+    mhi[e] = hi[i];
+    offl[e] = off;
+    for (int m = 0; m < nt[i]; ++m) {
+      const int ti = toff + m;
+      if (ti < max_tiles) *(int4*)(tiles + 4 * ti) = int4{e, off + m * bm, min(bm, cnt[i] - m * bm), 0};
+    }
+    if (tile_src && nt[i] > 0) {
+      // column r of the expert's tiles = its r-th token; unused columns 0
+      uint64_t mm = ((uint64_t)hi[i] << 32) | lo[i];
+      for (int r = 0; mm; ++r) {
+        const int ti = toff + (r >> lg_bm);
+        if (ti < max_tiles) tile_src[ti * kTileSrcCols + (r & (kTileSrcCols - 1))] = __builtin_ctzll(mm);
+        mm &= mm - 1;
       }
+      const int ti = toff + nt[i] - 1;
+      if (ti < max_tiles)
+        for (int c = cnt[i] - (nt[i] - 1) * bm; c < kTileSrcCols; ++c) tile_src[ti * kTileSrcCols + c] = 0;
     }
   }
-
-  // the expert's tile records (expert, first position, rows); its lanes pad
-  // the unused source columns of every tile
-  if (own) {
-    if (q == 0) {
-      counts[e] = tot;
-      offsets[e] = off_e;
-    }
-    for (int m = 0; m < nt; ++m) {
-      const int ti = toff_e + m;
-      if (ti >= max_tiles) break;
-      const int rows = min(bm, tot - m * bm);
-      if (q == 0) *(int4*)(tiles + 4 * ti) = int4{e, off_e + m * bm, rows, 0};
-      if (tile_src)
-        for (int c = q; c < kTileSrcCols; c += np)
-          if (c >= rows) tile_src[ti * kTileSrcCols + c] = 0;
-    }
-  }
-  if (tid == 0) {
-    offsets[E] = n_pairs;
+  if (lane == 0) {
+    offsets[E] = P;
     n_tiles[0] = min(n_tile_all, max_tiles);
   }
   // records past the last tile say "no rows" (the decode form reads every record up to max_tiles)
-  for (int ti = n_tile_all + tid; ti < max_tiles; ti += kGroupThreads) *(int4*)(tiles + 4 * ti) = int4{0, 0, 0, 0};
+  for (int ti = n_tile_all + lane; ti < max_tiles; ti += 64) *(int4*)(tiles + 4 * ti) = int4{0, 0, 0, 0};
+  wave_lds_sync();
+  // positions of the pairs; the token of pair p is p / k = (p ceil(2^32 / k)) >> 32
+  const uint64_t kmagic = ((1ull << 32) + (uint64_t)k - 1) / (uint64_t)k;
+  for (int p = lane; p < P; p += 64) {
+    const int e = ids[p];
+    const int t = (int)(((uint64_t)p * kmagic) >> 32);
+    const uint32_t below_lo = t >= 32 ? 0xffffffffu : ((1u << t) - 1u);
+    const uint32_t below_hi = t <= 32 ? 0u : ((1u << (t - 32)) - 1u);
+    const int pos = offl[e] + __popc(mlo[e] & below_lo) + __popc(mhi[e] & below_hi);
+    perm[pos] = p;
+    inv[p] = pos;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -555,19 +520,27 @@ __global__ void __launch_bounds__(kGroupThreads) route_group_kernel(
     int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ inv,
     int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles, int32_t* __restrict__ tile_src,
     const uint8_t* __restrict__ resident) {
-  __shared__ __attribute__((aligned(16))) int32_t ids_s[kFusedRouteMaxPairs];
-  __shared__ int32_t wave_tot[kGroupWaves];
+  __shared__ int32_t ids_s[kFusedRouteMaxPairs];
+  __shared__ uint32_t selmask[kFusedRouteMaxTokens][8];
+  __shared__ uint32_t mlo[kMaxExperts], mhi[kMaxExperts];
+  __shared__ int32_t offl[kMaxExperts];
   __shared__ float sv[kGroupWaves][kMaxTopK];
   __shared__ int si[kGroupWaves][kMaxTopK];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  // the grouping thread's residency flag, read before routing so its latency hides
-  const int ge = threadIdx.x / group_parts(E);
-  const bool res_ok = !resident || (ge < E && resident[ge]);
+  // the grouping lane's residency flags, read before routing so their latency hides
+  unsigned res = 0;
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int e = VPL * lane + i;
+      res |= (unsigned)(!resident || (e < E && resident[e])) << i;
+    }
+  }
   for (int t = wave; t < T; t += kGroupWaves) {
     int id;
     float w;
-    route_token<VPL, BF16>(logits, t, E, k, flags, sv[wave], si[wave], &id, &w);
+    route_token<VPL, BF16>(logits, t, E, k, flags, sv[wave], si[wave], &id, &w, selmask[t]);
     if (lane < k) {
       ids_s[t * k + lane] = id;
       ids_out[(int64_t)t * k + lane] = id;
@@ -575,8 +548,9 @@ __global__ void __launch_bounds__(kGroupThreads) route_group_kernel(
     }
   }
   __syncthreads();
-  group_small(ids_s, T, k, E, bm, max_tiles, res_ok, counts, offsets, perm, inv, tiles, n_tiles, tile_src,
-              wave_tot);
+  if (wave != 0) return;
+  group_masks<VPL>(selmask, ids_s, T, k, E, bm, max_tiles, res, counts, offsets, perm, inv, tiles, n_tiles,
+                   tile_src, mlo, mhi, offl);
 }
 
 #define NKT_VPL_SWITCH(E, CASE) \
