@@ -81,6 +81,36 @@ def test_qwen3_int8_cut_experts(gpu_device, T):
     _check(layer, native, T)
 
 
+def test_qwen3_int8_prefill_row_scales(gpu_device):
+    """The int8 prefill gate_up multiplies power-of-two-scaled fp16 copies of
+    the token rows: rows scaled by 2^-40 .. 2^40, a zero row and rows whose
+    entries span 2^20 must each match the oracle to the bf16 tolerance of
+    their own magnitude (routing from the unscaled rows)."""
+    announce("forward qwen3_int8 E=32 T=320 scaled rows")
+    layer, native = _layer("qwen3_int8", E=32)
+    T = 320
+    x, logits = build_inputs(layer, T, seed=11, device="cuda")
+    xf = x.float()
+    exps = torch.tensor([-40, -20, 0, 20, 40], dtype=torch.float32, device="cuda")
+    scale = torch.pow(2.0, exps[torch.arange(T, device="cuda") % 5])
+    xf = xf * scale[:, None]
+    xf[7] = 0.0
+    xf[9, ::97] *= 2.0 ** 20  # one row spanning 2^20 (plus the N(0,1) spread)
+    xs = xf.to(torch.bfloat16)
+    out = native.forward(xs, logits)
+    torch.cuda.synchronize()
+    ref = oracle_forward(layer, xs, logits)
+    got = out.float().cpu().numpy().astype(np.float64)
+    assert np.all(got[7] == 0.0)
+    for t in range(T):
+        if t == 7:
+            continue
+        r = ref[t].astype(np.float64)
+        rel = np.linalg.norm(got[t] - r) / np.linalg.norm(r)
+        assert rel <= 1e-2, f"row {t}: rel-L2 {rel}"
+        assert np.max(np.abs(got[t] - r)) <= 2e-2 * np.max(np.abs(r)), f"row {t}: max-abs"
+
+
 @pytest.mark.parametrize("T", [16, 100, 256])
 def test_qwen3_shape_bf16_weights(gpu_device, T):
     """Dense bf16 experts at the Qwen3 shape (E cut to 16): T=16 decode form,
