@@ -570,10 +570,181 @@ bool gemm2_i8_pipeline(const GemmArgs& a, int wf) {
   return wf == WF_I8 && a.in_bytes <= (int64_t)kI8Skip && (int64_t)a.N * a.K <= (int64_t)kI8Skip;
 }
 
+// the int4 pipeline addresses weights, scales, group sums and activations
+// with 32-bit buffer offsets (bf16 activations)
+bool gemm2_i4_pipeline(const GemmArgs& a, int wf) {
+  if (wf != WF_I4 || !a.act_bf16 || a.in_bytes <= 0) return false;
+  const int64_t rows_in = a.in_bytes / ((int64_t)a.K * 2);
+  return a.in_bytes <= (int64_t)kI8Skip && a.w_expert_bytes <= (int64_t)kI8Skip &&
+         a.s_expert_elems * 2 <= (int64_t)kI8Skip && rows_in * (a.K / 128) * 4 <= (int64_t)kI8Skip;
+}
+
 bool gemm2_supported(int wf, int phase, int N, int K, int I) {
   if (wf != WF_BF16 && wf != WF_I8 && wf != WF_I4) return false;
   if (K % 128 != 0) return false;
   return phase == PHASE_GATE_UP ? (I % 128 == 0) : (N % 256 == 0);
+}
+
+// ---------------------------------------------------------------------------
+// int4 g128 weights, three-stage pipeline.  Same tile, waves (8, two 16-row
+// tiles each), work order, MFMA and scaling sequence and epilogue as
+// gemm2_kernel<WF_I4, ...> (so the results are the same bit for bit); K
+// advances one 128-wide scale group per stage:
+//   * tokens: 64 positions x 256 B per stage reach one of three LDS buffers
+//     by direct-to-LDS buffer loads (16 loads of 4 positions, 2 per wave);
+//     lane l carries position 4 i + l / 16 into slot l % 16 of that
+//     position's row, fetched from chunk (l % 16) ^ (position % 16), so the
+//     MFMA operand reads of 16 consecutive positions cover all 64 banks;
+//   * each wave's two 1 KiB weight blocks go by buffer loads straight into a
+//     three-deep register ring; their bf16 scales (lanes 0-15, 4 bytes
+//     each) and the 64 positions' activation group sums (4 bytes per lane)
+//     reach the wave's own slice of a small LDS buffer by direct-to-LDS
+//     loads;
+//   * step x: wait for this wave's loads of stage x (all but the newest 6,
+//     the loads of stage x + 1), one LDS-only barrier (every wave is also
+//     done reading stage x - 1's buffers), start stage x + 2's loads into
+//     those buffers and that ring slot, then stage x: per column tile (the
+//     next tile's operands read from LDS meanwhile) four MFMAs per row tile
+//     into a temporary that starts at the code offset, scaled into the
+//     accumulator.
+// Loads past the last stage take an out-of-range buffer offset (no
+// traffic), so every step issues the same 6.  Six LDS objects: the compiler
+// tells a direct-to-LDS load into one from reads of another.
+// ---------------------------------------------------------------------------
+constexpr int kI4TokBytes = kBM * 256;
+constexpr int kI4SxBytes = 8 * 512;  // per wave: 256 B scales (64 used), 256 B group sums
+
+template <int PHASE>
+__global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slabs) {
+  constexpr int kWaves = 8;
+  constexpr int kRT = 2;
+  __shared__ __attribute__((aligned(1024))) uint8_t tb0[kI4TokBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t tb1[kI4TokBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t tb2[kI4TokBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t sx0[kI4SxBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t sx1[kI4SxBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t sx2[kI4SxBytes];
+  __shared__ int srcl[kBM];
+  __shared__ float hpart[kWaves][kBM];
+  __shared__ float xtot_l[kBM];
+
+  TileItem it;
+  if (!gemm2_item(a, n_slabs, it)) return;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  gemm2_sources(a, it, srcl);
+  __syncthreads();
+
+  const uint16_t* sexp = a.scales + (int64_t)it.expert * a.s_expert_elems;
+  const int G = a.K / 128;  // stages = scale groups = 1 KiB blocks per 16-row block
+  const int rows_in = (int)(a.in_bytes / ((int64_t)a.K * 2));
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.w + (int64_t)it.expert * a.w_expert_bytes), (short)0, (int)a.w_expert_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t sres =
+      __builtin_amdgcn_make_buffer_rsrc((void*)sexp, (short)0, (int)(a.s_expert_elems * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t xres =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.xsum, (short)0, rows_in * G * 4, 0x00020000);
+  const __amdgpu_buffer_rsrc_t tres = __builtin_amdgcn_make_buffer_rsrc((void*)a.in, (short)0, (int)a.in_bytes, 0x00020000);
+  int wrow[kRT];
+  uint32_t wsrc[kRT];
+#pragma unroll
+  for (int r = 0; r < kRT; ++r) {
+    if (PHASE == PHASE_GATE_UP)
+      wrow[r] = (r == 0 ? 0 : a.I) + it.slab * 128 + wave * 16;
+    else
+      wrow[r] = it.slab * 256 + wave * 32 + r * 16;
+    wsrc[r] = (uint32_t)(wrow[r] >> 4) * (uint32_t)G * 1024u + lane * 16u;
+  }
+  // scale lane (lanes 16-63 repeat lanes 0-15): row tile (l % 16) / 8, 4-byte piece l % 8
+  const int sl = lane & 15;
+  const uint32_t ssrc = ((uint32_t)(wrow[sl >> 3] >> 4) * (uint32_t)G * 16u) * 2u + (sl & 7) * 4u;
+  const uint32_t xsrc = (uint32_t)srcl[lane] * (uint32_t)G * 4u;
+  uint32_t tsrc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int p = 8 * wave + 4 * j + (lane >> 4);
+    const int chunk = (lane & 15) ^ (p & 15);
+    tsrc[j] = (uint32_t)srcl[p] * (uint32_t)a.K * 2u + chunk * 16u;
+  }
+  const int tofs = wave * 2048;  // this wave's slice of a token buffer
+  const int sofs = wave * 512;   // and of a scale / group-sum buffer
+
+  // stage st's 6 loads (st >= G: out of range, no traffic)
+  auto issue = [&](int st, uint8_t* tb, uint8_t* sx, u32x4 (&w)[kRT]) {
+    const bool live = st < G;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(tres, (__attribute__((address_space(3))) void*)(tb + tofs + j * 1024),
+                                               16, live ? tsrc[j] + st * 256u : kI8Skip, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(sres, (__attribute__((address_space(3))) void*)(sx + sofs), 4,
+                                             live ? ssrc + st * 32u : kI8Skip, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(xres, (__attribute__((address_space(3))) void*)(sx + sofs + 256), 4,
+                                             live ? xsrc + st * 4u : kI8Skip, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < kRT; ++r)
+      w[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, live ? wsrc[r] + st * 1024u : kI8Skip, 0, 0));
+  };
+
+  f32x4 acc[kRT][kCT];
+#pragma unroll
+  for (int r = 0; r < kRT; ++r)
+#pragma unroll
+    for (int c = 0; c < kCT; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto read_b = [&](u32x4 (&f)[4], const uint8_t* tb, int c) {
+    const int p = c * 16 + (lane & 15);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) f[s] = *(const u32x4*)(tb + p * 256 + (((4 * s + (lane >> 4)) ^ (p & 15)) * 16));
+  };
+  auto compute = [&](const u32x4 (&w)[kRT], const uint8_t* tb, const uint8_t* sx) {
+    u32x4 ad[kRT][4];
+    f32x4 sc[kRT];
+#pragma unroll
+    for (int r = 0; r < kRT; ++r) {
+      sc[r] = bf16x4_to_f32(*(const u32x2*)(sx + sofs + r * 32 + (lane >> 4) * 8));
+#pragma unroll
+      for (int s = 0; s < 4; ++s) ad[r][s] = dq_i4(w[r][s]);
+    }
+    u32x4 bf[2][4];
+    read_b(bf[0], tb, 0);
+#pragma unroll
+    for (int c = 0; c < kCT; ++c) {
+      if (c + 1 < kCT) read_b(bf[(c + 1) & 1], tb, c + 1);
+      const float cv = -136.0f * *(const float*)(sx + sofs + 256 + (c * 16 + (lane & 15)) * 4);
+#pragma unroll
+      for (int r = 0; r < kRT; ++r) {
+        f32x4 tmp = f32x4{cv, cv, cv, cv};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) tmp = mfma_bf16(ad[r][s], bf[c & 1][s], tmp);
+        acc[r][c] += sc[r] * tmp;
+      }
+    }
+  };
+
+  u32x4 w0[kRT], w1[kRT], w2[kRT];
+  auto step = [&](const u32x4 (&wcur)[kRT], u32x4 (&wn2)[kRT], const uint8_t* tb_x, const uint8_t* sx_x,
+                  uint8_t* tb_n2, uint8_t* sx_n2, int x) {
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6): stage x landed (stage x + 1's 6 may fly)
+    lds_barrier();
+    issue(x + 2, tb_n2, sx_n2, wn2);
+    compute(wcur, tb_x, sx_x);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  issue(0, tb0, sx0, w0);
+  issue(1, tb1, sx1, w1);
+  // three steps per iteration return ring slots and buffers to their roles
+  int x = 0;
+  for (; x + 3 <= G; x += 3) {
+    step(w0, w2, tb0, sx0, tb2, sx2, x);
+    step(w1, w0, tb1, sx1, tb0, sx0, x + 1);
+    step(w2, w1, tb2, sx2, tb1, sx1, x + 2);
+  }
+  if (x < G) step(w0, w2, tb0, sx0, tb2, sx2, x);
+  if (x + 1 < G) step(w1, w0, tb1, sx1, tb0, sx0, x + 1);
+  wait_vmem();  // out-of-range loads past the last stage land before the LDS is reused
+  __syncthreads();
+  gemm2_epilogue<WF_I4, PHASE, kWaves>(a, acc, srcl, hpart, xtot_l, xtot_l, wrow, sexp, it.row0, it.rows, it.slab);
 }
 
 // Input of the int8 gate_up on the fp16 matrix cores, one wave per row: the
@@ -688,6 +859,13 @@ hipError_t launch_gemm2(const GemmArgs& a, int wf, int phase, int max_tiles, hip
       launch_timed(gemm2_i8_kernel<PHASE_GATE_UP, false>, grid, block, 0, stream, tm, a, n_slabs);
     else
       launch_timed(gemm2_i8_kernel<PHASE_DOWN, false>, grid, block, 0, stream, tm, a, n_slabs);
+    return hipGetLastError();
+  }
+  if (gemm2_i4_pipeline(a, wf)) {
+    if (phase == PHASE_GATE_UP)
+      launch_timed(gemm2_i4_kernel<PHASE_GATE_UP>, grid, block, 0, stream, tm, a, n_slabs);
+    else
+      launch_timed(gemm2_i4_kernel<PHASE_DOWN>, grid, block, 0, stream, tm, a, n_slabs);
     return hipGetLastError();
   }
   switch (wf) {

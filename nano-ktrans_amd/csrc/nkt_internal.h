@@ -125,6 +125,8 @@ hipError_t launch_prep_f16(const void* x, int rows, int K, float* sums, uint16_t
 // whether launch_gemm2 runs a on the int8 pipeline kernel (which then takes
 // gate_up's input as the fp16 copy when a.xinv is set)
 bool gemm2_i8_pipeline(const GemmArgs& a, int wf);
+// whether launch_gemm2 runs a on the int4 pipeline kernel
+bool gemm2_i4_pipeline(const GemmArgs& a, int wf);
 
 // Repack [N, K] into the block layout; rows >= n_valid (bf16 only) are zero
 // and not read (n_valid < 0: all N rows).
