@@ -176,6 +176,39 @@ __device__ __forceinline__ int wave_inclusive_scan(int v) {
 //         for columns 2s', 2s'+1 pairs (n = stored nibble = q + 8).
 //   int8: two u32 hold 8 bytes (stored q + 128) -> 8 bf16 values 0..255.
 // ---------------------------------------------------------------------------
+// int4 dequantisation with v_and_or_b32: (w >> 4j) & 0x000F000F | 0x43004300
+// in one instruction after the shift (the mask comes from an SGPR, the bf16
+// exponent bits from a VGPR: one constant-bus read per instruction).
+struct DqConst {
+  uint32_t mask;  // SGPR: 0x000F000F
+  uint32_t bits;  // VGPR: 0x43004300
+};
+
+__device__ __forceinline__ DqConst dq_const() {
+  DqConst k;
+  __asm__ volatile("s_mov_b32 %0, 0xf000f" : "=s"(k.mask));
+  __asm__ volatile("v_mov_b32 %0, 0x43004300" : "=v"(k.bits));
+  return k;
+}
+
+// (w >> SH) & mask | bits; the shift sits inside the same statement so that
+// nothing of the dequantisation can move away from the constants' block
+template <int SH>
+__device__ __forceinline__ uint32_t dq_word(uint32_t w, const DqConst& k) {
+  uint32_t r;
+  if (SH == 0)
+    __asm__("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(k.mask), "v"(k.bits));
+  else
+    __asm__("v_lshrrev_b32 %0, %4, %1\n\tv_and_or_b32 %0, %0, %2, %3"
+            : "=&v"(r)
+            : "v"(w), "s"(k.mask), "v"(k.bits), "i"(SH));
+  return r;
+}
+
+__device__ __forceinline__ u32x4 dq_i4_k(uint32_t w, const DqConst& k) {
+  return u32x4{dq_word<0>(w, k), dq_word<4>(w, k), dq_word<8>(w, k), dq_word<12>(w, k)};
+}
+
 __device__ __forceinline__ u32x4 dq_i4(uint32_t w) {
   u32x4 a;
   a[0] = (w & 0x000F000Fu) | 0x43004300u;

@@ -49,17 +49,25 @@ struct ARegs {
 
 // One workgroup's work item: (token tile, weight slab) and the tile record.
 // XCD-aware work order: workgroup b runs on XCD b % 8, so XCD x takes the
-// x-th contiguous eighth of the (tile-major, slab-minor) item list.  The
-// slabs of one token tile and the tiles of one expert then run side by side
-// on one XCD and share its L2 (token rows and weight slabs are read from HBM
-// about once instead of once per XCD).  (The 1-D grid is a multiple of 8 and
-// at least 8 * per_xcd, so every item below n_items has exactly one
-// workgroup.)  Returns false for a workgroup without an item.
+// x-th contiguous eighth of the item list, and the items one XCD runs side
+// by side share its L2.  The list runs over groups of sg slabs, tile-major
+// inside a group.  For small experts (one group of all slabs) the slabs of
+// one token tile and the tiles of one expert run together: token rows and
+// weight slabs are read from HBM about once.  For experts larger than the
+// L2 (sg = 4: Mixtral's 58.7 MB gate_up, Qwen1.5's shared expert) a group
+// of 4 slabs runs over the expert's tiles, so a slab's weights are fetched
+// once per group instead of once per tile; a last, smaller group takes the
+// remaining slabs.  (The 1-D grid is a multiple of 8 and at least
+// 8 * per_xcd, so every item below n_items has exactly one workgroup.)
+// Returns false for a workgroup without an item.
+// slabs per group: all of them unless one expert's weights pass 4 MiB
+int slab_group(int n_slabs, int64_t expert_bytes) { return expert_bytes > (4 << 20) ? min(4, n_slabs) : n_slabs; }
+
 struct TileItem {
   int expert, row0, rows, slab;
 };
 
-__device__ __forceinline__ bool gemm2_item(const GemmArgs& a, int n_slabs, TileItem& it) {
+__device__ __forceinline__ bool gemm2_item(const GemmArgs& a, int n_slabs, int sg, TileItem& it) {
   const int n_tiles = a.n_tiles ? a.n_tiles[0] : (a.num_rows + kBM - 1) / kBM;
   const int n_items = n_tiles * n_slabs;
   const int b = blockIdx.x;
@@ -68,8 +76,19 @@ __device__ __forceinline__ bool gemm2_item(const GemmArgs& a, int n_slabs, TileI
   if (j >= per_xcd) return false;
   const int item = (b % kXcds) * per_xcd + j;
   if (item >= n_items) return false;
-  const int tile = item / n_slabs;
-  it.slab = item - tile * n_slabs;
+  const int full = (n_slabs / sg) * n_tiles * sg;  // items in full groups
+  int tile;
+  if (item < full) {
+    const int g = item / (n_tiles * sg);
+    const int rem = item - g * n_tiles * sg;
+    tile = rem / sg;
+    it.slab = g * sg + (rem - tile * sg);
+  } else {
+    const int last = n_slabs % sg;  // slabs of the last group
+    const int rem = item - full;
+    tile = rem / last;
+    it.slab = (n_slabs / sg) * sg + (rem - tile * last);
+  }
   if (a.n_tiles) {
     const int4 rec = *(const int4*)(a.tiles + 4 * tile);
     it.expert = rec.x;
@@ -195,7 +214,7 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[1
 }
 
 template <int WF, int PHASE, int kWaves>
-__global__ void __launch_bounds__(64 * kWaves, 2) gemm2_kernel(GemmArgs a, int n_slabs) {
+__global__ void __launch_bounds__(64 * kWaves, 2) gemm2_kernel(GemmArgs a, int n_slabs, int sg) {
   constexpr int kRT = 16 / kWaves;  // 16-row weight tiles per wave
   constexpr int NBLK = 128 / block_k(WF);
   // two separate LDS objects (not one array) so the compiler can tell a
@@ -209,7 +228,7 @@ __global__ void __launch_bounds__(64 * kWaves, 2) gemm2_kernel(GemmArgs a, int n
   __shared__ float xtot_l[kBM];
 
   TileItem it;
-  if (!gemm2_item(a, n_slabs, it)) return;
+  if (!gemm2_item(a, n_slabs, sg, it)) return;
   const int expert = it.expert, row0 = it.row0, rows = it.rows, slab = it.slab;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -396,7 +415,7 @@ constexpr int kI8TokBytes = kBM * kI8Stage * 2;
 constexpr uint32_t kI8Skip = 0xFFFFFF00u;     // a buffer offset past every range the kernel is given
 
 template <int PHASE, bool F16>
-__global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slabs) {
+__global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slabs, int sg) {
   constexpr int kWaves = 4;
   constexpr int kRT = 4;
   __shared__ __attribute__((aligned(1024))) uint8_t tb0[kI8TokBytes];
@@ -408,7 +427,7 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
   __shared__ float xinv_l[kBM];
 
   TileItem it;
-  if (!gemm2_item(a, n_slabs, it)) return;
+  if (!gemm2_item(a, n_slabs, sg, it)) return;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   gemm2_sources(a, it, srcl);
@@ -615,7 +634,7 @@ constexpr int kI4TokBytes = kBM * 256;
 constexpr int kI4SxBytes = 8 * 512;  // per wave: 256 B scales (64 used), 256 B group sums
 
 template <int PHASE>
-__global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slabs) {
+__global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slabs, int sg) {
   constexpr int kWaves = 8;
   constexpr int kRT = 2;
   __shared__ __attribute__((aligned(1024))) uint8_t tb0[kI4TokBytes];
@@ -629,7 +648,7 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
   __shared__ float xtot_l[kBM];
 
   TileItem it;
-  if (!gemm2_item(a, n_slabs, it)) return;
+  if (!gemm2_item(a, n_slabs, sg, it)) return;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   gemm2_sources(a, it, srcl);
@@ -844,28 +863,29 @@ hipError_t launch_gemm2(const GemmArgs& a, int wf, int phase, int max_tiles, hip
   if (max_tiles <= 0) return hipSuccess;
   const int n_slabs = phase == PHASE_GATE_UP ? a.I / 128 : a.N / 256;
   const int64_t items = (int64_t)n_slabs * max_tiles;
+  const int sg = slab_group(n_slabs, a.w_expert_bytes);
   dim3 grid((unsigned)((items + kXcds - 1) / kXcds * kXcds)), block(64 * gemm2_waves(wf));
 #define NKT_G2(W)                                                                                          \
   case W:                                                                                                  \
     if (phase == PHASE_GATE_UP)                                                                            \
-      launch_timed(gemm2_kernel<W, PHASE_GATE_UP, gemm2_waves(W)>, grid, block, 0, stream, tm, a, n_slabs); \
+      launch_timed(gemm2_kernel<W, PHASE_GATE_UP, gemm2_waves(W)>, grid, block, 0, stream, tm, a, n_slabs, sg); \
     else                                                                                                   \
-      launch_timed(gemm2_kernel<W, PHASE_DOWN, gemm2_waves(W)>, grid, block, 0, stream, tm, a, n_slabs);    \
+      launch_timed(gemm2_kernel<W, PHASE_DOWN, gemm2_waves(W)>, grid, block, 0, stream, tm, a, n_slabs, sg);    \
     break;
   if (gemm2_i8_pipeline(a, wf)) {
     if (phase == PHASE_GATE_UP && a.xinv)
-      launch_timed(gemm2_i8_kernel<PHASE_GATE_UP, true>, grid, block, 0, stream, tm, a, n_slabs);
+      launch_timed(gemm2_i8_kernel<PHASE_GATE_UP, true>, grid, block, 0, stream, tm, a, n_slabs, sg);
     else if (phase == PHASE_GATE_UP)
-      launch_timed(gemm2_i8_kernel<PHASE_GATE_UP, false>, grid, block, 0, stream, tm, a, n_slabs);
+      launch_timed(gemm2_i8_kernel<PHASE_GATE_UP, false>, grid, block, 0, stream, tm, a, n_slabs, sg);
     else
-      launch_timed(gemm2_i8_kernel<PHASE_DOWN, false>, grid, block, 0, stream, tm, a, n_slabs);
+      launch_timed(gemm2_i8_kernel<PHASE_DOWN, false>, grid, block, 0, stream, tm, a, n_slabs, sg);
     return hipGetLastError();
   }
   if (gemm2_i4_pipeline(a, wf)) {
     if (phase == PHASE_GATE_UP)
-      launch_timed(gemm2_i4_kernel<PHASE_GATE_UP>, grid, block, 0, stream, tm, a, n_slabs);
+      launch_timed(gemm2_i4_kernel<PHASE_GATE_UP>, grid, block, 0, stream, tm, a, n_slabs, sg);
     else
-      launch_timed(gemm2_i4_kernel<PHASE_DOWN>, grid, block, 0, stream, tm, a, n_slabs);
+      launch_timed(gemm2_i4_kernel<PHASE_DOWN>, grid, block, 0, stream, tm, a, n_slabs, sg);
     return hipGetLastError();
   }
   switch (wf) {
