@@ -622,10 +622,10 @@ bool gemm2_supported(int wf, int phase, int N, int K, int I) {
 //   * step x: wait for this wave's loads of stage x (all but the newest 6,
 //     the loads of stage x + 1), one LDS-only barrier (every wave is also
 //     done reading stage x - 1's buffers), start stage x + 2's loads into
-//     those buffers and that ring slot, then stage x: per column tile (the
-//     next tile's operands read from LDS meanwhile) four MFMAs per row tile
-//     into a temporary that starts at the code offset, scaled into the
-//     accumulator.
+//     those buffers and that ring slot, then stage x: four MFMAs per (row
+//     tile, column tile) into a temporary that starts at the code offset,
+//     the 8 temporaries advancing together, then scaled into the
+//     accumulators.
 // Loads past the last stage take an out-of-range buffer offset (no
 // traffic), so every step issues the same 6.  Six LDS objects: the compiler
 // tells a direct-to-LDS load into one from reads of another.
@@ -710,12 +710,16 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
 #pragma unroll
     for (int c = 0; c < kCT; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  auto read_b = [&](u32x4 (&f)[4], const uint8_t* tb, int c) {
-    const int p = c * 16 + (lane & 15);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) f[s] = *(const u32x4*)(tb + p * 256 + (((4 * s + (lane >> 4)) ^ (p & 15)) * 16));
-  };
+  // all 8 (row tile, column tile) temporaries advance one K step at a time,
+  // so no MFMA waits on the one before it
   auto compute = [&](const u32x4 (&w)[kRT], const uint8_t* tb, const uint8_t* sx) {
+    u32x4 bf[kCT][4];
+#pragma unroll
+    for (int c = 0; c < kCT; ++c) {
+      const int p = c * 16 + (lane & 15);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) bf[c][s] = *(const u32x4*)(tb + p * 256 + (((4 * s + (lane >> 4)) ^ (p & 15)) * 16));
+    }
     u32x4 ad[kRT][4];
     f32x4 sc[kRT];
 #pragma unroll
@@ -724,20 +728,23 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
 #pragma unroll
       for (int s = 0; s < 4; ++s) ad[r][s] = dq_i4(w[r][s]);
     }
-    u32x4 bf[2][4];
-    read_b(bf[0], tb, 0);
+    f32x4 tmp[kRT][kCT];
 #pragma unroll
     for (int c = 0; c < kCT; ++c) {
-      if (c + 1 < kCT) read_b(bf[(c + 1) & 1], tb, c + 1);
       const float cv = -136.0f * *(const float*)(sx + sofs + 256 + (c * 16 + (lane & 15)) * 4);
 #pragma unroll
-      for (int r = 0; r < kRT; ++r) {
-        f32x4 tmp = f32x4{cv, cv, cv, cv};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) tmp = mfma_bf16(ad[r][s], bf[c & 1][s], tmp);
-        acc[r][c] += sc[r] * tmp;
-      }
+      for (int r = 0; r < kRT; ++r) tmp[r][c] = f32x4{cv, cv, cv, cv};
     }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int c = 0; c < kCT; ++c)
+#pragma unroll
+        for (int r = 0; r < kRT; ++r) tmp[r][c] = mfma_bf16(ad[r][s], bf[c][s], tmp[r][c]);
+#pragma unroll
+    for (int c = 0; c < kCT; ++c)
+#pragma unroll
+      for (int r = 0; r < kRT; ++r) acc[r][c] += sc[r] * tmp[r][c];
   };
 
   u32x4 w0[kRT], w1[kRT], w2[kRT];
