@@ -105,6 +105,9 @@ struct WsLayout {
 
 constexpr int kSharedDecodeMaxTokens = 256;
 
+// NKT_WS_Y row order: pair (t k + slot) for the decode form, else position
+bool y_pair_order(const WsLayout& L) { return L.bm == kTileSrcCols; }
+
 // the prefill form covers both projections of the routed (or shared) experts
 bool prefill_form_ok(const Handle* h, bool shared) {
   const int I = shared ? h->Is : h->I;
@@ -258,6 +261,9 @@ GemmArgs expert_args(const Handle* h, int phase, bool shared, const void* in, vo
   }
   const int64_t in_rows = (!shared && phase == PHASE_GATE_UP) ? T : a.num_rows;
   a.in_bytes = in_rows * K * (h->act_bf16 ? 2 : 4);
+  // the decode form writes y in pair order (the combine then issues all its
+  // loads at once); the prefill form keeps position order (contiguous rows)
+  if (!shared && phase == PHASE_DOWN && y_pair_order(L)) a.out_rows = ws_ptr<int32_t>(ws, L, NKT_WS_PERM);
   if (phase == PHASE_GATE_UP && int8_f16_input(h)) {
     a.in16 = ws_ptr<uint16_t>(ws, L, kWsX16);
     a.xinv = ws_ptr<float>(ws, L, kWsXInv);
@@ -420,7 +426,7 @@ int do_combine(Handle* h, int T, void* out, void* ws, const WsLayout& L, hipStre
   const bool sh = h->Is > 0;
   if (!check_hip(launch_combine(ws_ptr<float>(ws, L, NKT_WS_Y), ws_ptr<int32_t>(ws, L, NKT_WS_TOPK_IDS),
                                 ws_ptr<float>(ws, L, NKT_WS_TOPK_WEIGHTS),
-                                ws_ptr<int32_t>(ws, L, NKT_WS_INV),
+                                y_pair_order(L) ? nullptr : ws_ptr<int32_t>(ws, L, NKT_WS_INV),
                                 sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_Y) : nullptr,
                                 sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE) : nullptr, h->resident,
                                 extra, residual, T, h->k, h->H, out, h->act_bf16, st),

@@ -37,72 +37,57 @@ __global__ void __launch_bounds__(256) shared_gate_kernel(const void* __restrict
 }
 
 // One workgroup per (token, 1024-column slice); one thread per 4 columns.
+// y holds the k expert rows of token t at rows t k .. t k + k - 1 (pair
+// order; inv == nullptr) or at rows inv[t k + j] (position order); in pair
+// order every load is issued at once.  The terms are added in ascending
+// expert id through the thread's own LDS slots.
 template <int K>
 __global__ void __launch_bounds__(256) combine_kernel(
     const float* __restrict__ y, const int32_t* __restrict__ ids, const float* __restrict__ w,
-    const int32_t* __restrict__ inv, const float* __restrict__ y_shared,
-    const float* __restrict__ shared_gate, const uint8_t* __restrict__ resident,
+    const int32_t* __restrict__ inv, const float* __restrict__ y_shared, const float* __restrict__ shared_gate, const uint8_t* __restrict__ resident,
     const void* __restrict__ extra, const void* __restrict__ residual, int num_tokens, int H,
     void* __restrict__ out, int out_bf16) {
+  __shared__ f32x4 terms[K][256];
   const int t = blockIdx.x;
   const int c = blockIdx.y * blockDim.x + threadIdx.x;  // float4 column index
-  // order the token's slots by expert id: rank[j] = #{i : id_i < id_j}
-  // (ids of one token are distinct), then gather by rank with static indices
-  int sid[K], spos[K], rank[K];
-  float sw[K];
-  bool sres[K];
-#pragma unroll
-  for (int j = 0; j < K; ++j) {
-    sid[j] = ids[(int64_t)t * K + j];
-    sres[j] = resident ? resident[sid[j]] != 0 : true;
-    // positions index y [T*K, H]; keep a corrupt entry from reading outside it
-    spos[j] = min(max(inv[(int64_t)t * K + j], 0), num_tokens * K - 1);
-    sw[j] = w[(int64_t)t * K + j];
-  }
-#pragma unroll
-  for (int j = 0; j < K; ++j) {
-    int r = 0;
-#pragma unroll
-    for (int i = 0; i < K; ++i) r += (sid[i] < sid[j]) ? 1 : 0;
-    rank[j] = r;
-  }
-  int order_pos[K];
-  float order_w[K];
-  bool order_res[K];
-#pragma unroll
-  for (int r = 0; r < K; ++r) {
-    int p = 0;
-    float wt = 0.f;
-    bool rs = true;
-#pragma unroll
-    for (int j = 0; j < K; ++j) {
-      if (rank[j] == r) {
-        p = spos[j];
-        wt = sw[j];
-        rs = sres[j];
-      }
-    }
-    order_pos[r] = p;
-    order_w[r] = wt;
-    order_res[r] = rs;
-  }
   if (4 * c >= H) return;
-  // every load first, then the fixed-order sum
+  // every load first: the k rows, the gated shared row, ids and weights
   f32x4 v[K];
 #pragma unroll
-  for (int j = 0; j < K; ++j) v[j] = *(const f32x4*)(y + (int64_t)order_pos[j] * H + 4 * c);
+  for (int j = 0; j < K; ++j) {
+    // a corrupt position never reads outside y
+    const int64_t row = inv ? min(max(inv[(int64_t)t * K + j], 0), num_tokens * K - 1) : (int64_t)t * K + j;
+    v[j] = *(const f32x4*)(y + row * H + 4 * c);
+  }
   f32x4 vs = f32x4{0.f, 0.f, 0.f, 0.f};
   float sg = 0.f;
   if (y_shared) {
     vs = *(const f32x4*)(y_shared + (int64_t)t * H + 4 * c);
     sg = shared_gate[t];
   }
-  // slots of experts that are not resident have no y row this call: their
-  // (stale) values are selected away, never multiplied
-  const f32x4 zero = f32x4{0.f, 0.f, 0.f, 0.f};
-  f32x4 acc = order_res[0] ? order_w[0] * v[0] : zero;
+  int sid[K];
+  float sw[K];
+  bool sres[K];
 #pragma unroll
-  for (int j = 1; j < K; ++j) acc += order_res[j] ? order_w[j] * v[j] : zero;
+  for (int j = 0; j < K; ++j) {
+    sid[j] = ids[(int64_t)t * K + j];
+    sw[j] = w[(int64_t)t * K + j];
+    sres[j] = resident ? resident[sid[j]] != 0 : true;
+  }
+  // slot j's term goes to place rank_j = #{i : id_i < id_j} (ids of one token
+  // are distinct); slots of experts that are not resident have no y row this
+  // call: their (stale) values are selected away, never multiplied
+  const f32x4 zero = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    int r = 0;
+#pragma unroll
+    for (int i = 0; i < K; ++i) r += (sid[i] < sid[j]) ? 1 : 0;
+    terms[r][threadIdx.x] = sres[j] ? sw[j] * v[j] : zero;
+  }
+  f32x4 acc = terms[0][threadIdx.x];
+#pragma unroll
+  for (int r = 1; r < K; ++r) acc += terms[r][threadIdx.x];
   if (extra) {
     if (out_bf16) {
       const u32x2 e = *(const u32x2*)((const uint16_t*)extra + (int64_t)t * H + 4 * c);
@@ -181,8 +166,7 @@ hipError_t launch_shared_gate(const void* x, const void* gate_w, int act_bf16, i
   return hipGetLastError();
 }
 
-hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, const int32_t* inv,
-                          const float* y_shared, const float* shared_gate, const uint8_t* resident,
+hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, const int32_t* inv, const float* y_shared, const float* shared_gate, const uint8_t* resident,
                           const void* extra, const void* residual, int T, int k, int H, void* out,
                           int out_bf16, hipStream_t stream) {
   if (T <= 0) return hipSuccess;

@@ -331,7 +331,8 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(GemmArgs a) {
       for (int c = 0; c < CT; ++c) {
         const int t = c * 16 + col;
         if (t < rows) {
-          const int64_t o = (int64_t)(row0 + t) * a.N + orow0 + 16 * r + rq;
+          const int64_t yrow = a.out_rows ? a.out_rows[row0 + t] : row0 + t;
+          const int64_t o = yrow * a.N + orow0 + 16 * r + rq;
           *(f32x4*)((float*)a.out + o) = acc[r][c];
         }
       }

@@ -103,12 +103,14 @@ __device__ __forceinline__ bool gemm2_item(const GemmArgs& a, int n_slabs, int s
 }
 
 // Source row of each tile position (positions past the tile's rows repeat
-// the first), into LDS; the caller's barrier publishes it.
-__device__ __forceinline__ void gemm2_sources(const GemmArgs& a, const TileItem& it, int* srcl) {
+// the first) and its output row (down: the pair, so y is in pair order),
+// into LDS; the caller's barrier publishes them.
+__device__ __forceinline__ void gemm2_sources(const GemmArgs& a, const TileItem& it, int* srcl, int* orow_l) {
   const int tid = threadIdx.x;
   if (tid < kBM) {
     const int p = it.row0 + (tid < it.rows ? tid : 0);
     srcl[tid] = a.perm ? a.perm[p] / a.topk : p;
+    orow_l[tid] = a.out_rows ? a.out_rows[p] : p;
   }
 }
 
@@ -120,6 +122,7 @@ __device__ __forceinline__ void gemm2_sources(const GemmArgs& a, const TileItem&
 // offset is 1152 (1024 + 128).
 template <int WF, int PHASE, int kWaves, bool XS = false>
 __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[16 / kWaves][kCT], const int* srcl,
+                                               const int* orow_l,
                                                float (*hpart)[kBM], float* xtot_l, float* xinv_l, const int* wrow,
                                                const uint16_t* sexp, int row0, int rows, int slab) {
   constexpr int kRT = 16 / kWaves;
@@ -207,7 +210,7 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[1
         const int pl = c * 16 + (lane & 15);
         f32x4 v = acc[r][c];
         if (WF == WF_I8) v *= sr;
-        if (pl < rows) *(f32x4*)((float*)a.out + (int64_t)(row0 + pl) * a.N + wrow[r] + rq) = v;
+        if (pl < rows) *(f32x4*)((float*)a.out + (int64_t)orow_l[pl] * a.N + wrow[r] + rq) = v;
       }
     }
   }
@@ -224,6 +227,7 @@ __global__ void __launch_bounds__(64 * kWaves, 2) gemm2_kernel(GemmArgs a, int n
   __shared__ float xsl0[256];  // int4: group sums of the tile rows (each wave loads all; [0, kBM) used)
   __shared__ float xsl1[256];
   __shared__ int srcl[kBM];
+  __shared__ int orow_l[kBM];
   __shared__ float hpart[kWaves][kBM];
   __shared__ float xtot_l[kBM];
 
@@ -235,7 +239,7 @@ __global__ void __launch_bounds__(64 * kWaves, 2) gemm2_kernel(GemmArgs a, int n
   const int wave = tid >> 6;
   const int G = a.K / 128;
   const int NKB = a.K / block_k(WF);
-  gemm2_sources(a, it, srcl);
+  gemm2_sources(a, it, srcl, orow_l);
   __syncthreads();
 
   // ---- this wave's weight rows ------------------------------------------
@@ -383,7 +387,7 @@ __global__ void __launch_bounds__(64 * kWaves, 2) gemm2_kernel(GemmArgs a, int n
   }
   __syncthreads();
 
-  gemm2_epilogue<WF, PHASE, kWaves>(a, acc, srcl, hpart, xtot_l, xtot_l, wrow, sexp, row0, rows, slab);
+  gemm2_epilogue<WF, PHASE, kWaves>(a, acc, srcl, orow_l, hpart, xtot_l, xtot_l, wrow, sexp, row0, rows, slab);
 }
 
 // ---------------------------------------------------------------------------
@@ -422,6 +426,7 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
   __shared__ __attribute__((aligned(1024))) uint8_t tb1[kI8TokBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t tb2[kI8TokBytes];
   __shared__ int srcl[kBM];
+  __shared__ int orow_l[kBM];
   __shared__ float hpart[kWaves][kBM];
   __shared__ float xtot_l[kBM];
   __shared__ float xinv_l[kBM];
@@ -430,7 +435,7 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
   if (!gemm2_item(a, n_slabs, sg, it)) return;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  gemm2_sources(a, it, srcl);
+  gemm2_sources(a, it, srcl, orow_l);
   __syncthreads();
 
   const uint16_t* sexp = a.scales + (int64_t)it.expert * a.s_expert_elems;
@@ -552,7 +557,7 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
   if (rest >= 5) step(f0, f1, w1, w0, tb1, tb2, x + 4);
   wait_vmem();  // out-of-range loads past the last stage land before the LDS is reused
   __syncthreads();
-  gemm2_epilogue<WF_I8, PHASE, kWaves, F16>(a, acc, srcl, hpart, xtot_l, xinv_l, wrow, sexp, it.row0, it.rows, it.slab);
+  gemm2_epilogue<WF_I8, PHASE, kWaves, F16>(a, acc, srcl, orow_l, hpart, xtot_l, xinv_l, wrow, sexp, it.row0, it.rows, it.slab);
 }
 
 // Per-row sums of each 128-wide K group of a bf16 matrix [rows, K] -> fp32
@@ -644,6 +649,7 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
   __shared__ __attribute__((aligned(1024))) uint8_t sx1[kI4SxBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t sx2[kI4SxBytes];
   __shared__ int srcl[kBM];
+  __shared__ int orow_l[kBM];
   __shared__ float hpart[kWaves][kBM];
   __shared__ float xtot_l[kBM];
 
@@ -651,7 +657,7 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
   if (!gemm2_item(a, n_slabs, sg, it)) return;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  gemm2_sources(a, it, srcl);
+  gemm2_sources(a, it, srcl, orow_l);
   __syncthreads();
 
   const uint16_t* sexp = a.scales + (int64_t)it.expert * a.s_expert_elems;
@@ -770,7 +776,7 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
   if (x + 1 < G) step(w1, w0, tb1, sx1, tb0, sx0, x + 1);
   wait_vmem();  // out-of-range loads past the last stage land before the LDS is reused
   __syncthreads();
-  gemm2_epilogue<WF_I4, PHASE, kWaves>(a, acc, srcl, hpart, xtot_l, xtot_l, wrow, sexp, it.row0, it.rows, it.slab);
+  gemm2_epilogue<WF_I4, PHASE, kWaves>(a, acc, srcl, orow_l, hpart, xtot_l, xtot_l, wrow, sexp, it.row0, it.rows, it.slab);
 }
 
 // Input of the int8 gate_up on the fp16 matrix cores, one wave per row: the

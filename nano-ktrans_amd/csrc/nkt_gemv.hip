@@ -227,9 +227,11 @@ __device__ __forceinline__ void mma_group(const WSlot<WF, NT>& r, const u32x4 (&
 
 // Output rows orow0 .. orow0 + 16 RT of the tile's positions: SwiGLU into h
 // (gate_up) or y / bf16 logits (down); int8 row scales applied here.
+// yrow: the output row of this lane's position (down).
 template <int WF, int PHASE, int RT>
 __device__ __forceinline__ void gemv_epilogue(const GemmArgs& a, const f32x4 (&acc)[PHASE == PHASE_GATE_UP ? 2 * RT : RT],
-                                              int rows, int row0, int orow0, const uint16_t* sexp, uint32_t lane) {
+                                              int rows, int row0, int orow0, const uint16_t* sexp, uint32_t lane,
+                                              int yrow) {
   const int t_out = lane & 15;
   if (t_out >= rows) return;
   const int64_t pos = row0 + t_out;
@@ -259,7 +261,7 @@ __device__ __forceinline__ void gemv_epilogue(const GemmArgs& a, const f32x4 (&a
           if (orow + v < a.out_cols)
             ((uint16_t*)a.out)[pos * a.out_cols + orow + v] = (uint16_t)f32_to_bf16_bits(s0[v]);
       } else {
-        *(f32x4*)((float*)a.out + pos * a.N + orow) = s0;
+        *(f32x4*)((float*)a.out + (int64_t)yrow * a.N + orow) = s0;
       }
     }
   }
@@ -322,6 +324,9 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
     rows = min(16, a.num_rows - row0);
   }
   if (rows <= 0) return;
+  // down: the output row of this lane's position, loaded before the K loop
+  int yrow = row0 + (lane & 15);
+  if (PHASE == PHASE_DOWN && a.out_rows && (int)(lane & 15) < rows) yrow = a.out_rows[yrow];
   if (!a.tile_src) {  // rows read in place
     src = row0 + (col < rows ? col : 0);
     srcq = row0 + ((col & 3) < rows ? (col & 3) : 0);
@@ -481,7 +486,7 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
     }
   }
   if (!rs_ok) return;
-  gemv_epilogue<WF, PHASE, RT>(a, acc, rows, row0, orow0, sexp, lane);
+  gemv_epilogue<WF, PHASE, RT>(a, acc, rows, row0, orow0, sexp, lane, yrow);
 }
 
 // ---------------------------------------------------------------------------

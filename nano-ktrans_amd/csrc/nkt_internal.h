@@ -51,6 +51,9 @@ struct GemmArgs {
   // power-of-two-scaled fp16 copy of in, and per input row 1 / scale
   uint16_t* in16;
   float* xinv;
+  // down of the routed experts: output row of each position (its pair
+  // t k + slot), so y comes out in pair order; nullptr: the position
+  const int32_t* out_rows;
 };
 
 enum GemmPhase : int { PHASE_GATE_UP = 0, PHASE_DOWN = 1 };
@@ -136,10 +139,11 @@ hipError_t launch_pack(int wf, const void* src, const void* src_scales, int N, i
 hipError_t launch_shared_gate(const void* x, const void* gate_w, int act_bf16, int T, int H,
                               float* gate_out, hipStream_t stream);
 
-hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, const int32_t* inv,
-                          const float* y_shared, const float* shared_gate, const uint8_t* resident,
-                          const void* extra, const void* residual, int T, int k, int H, void* out,
-                          int out_bf16, hipStream_t stream);
+// y: the k expert rows of token t at rows t k .. t k + k - 1 (pair order,
+// inv == nullptr) or at rows inv[t k + j] (position order)
+hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, const int32_t* inv, const float* y_shared,
+                          const float* shared_gate, const uint8_t* resident, const void* extra, const void* residual,
+                          int T, int k, int H, void* out, int out_bf16, hipStream_t stream);
 
 // bf16 RMSNorm rows of x [T, H] with weight w [H] (decoder-block form)
 hipError_t launch_rmsnorm(const void* x, const void* w, float eps, int T, int H, void* out, hipStream_t stream);
