@@ -39,6 +39,7 @@ namespace nkt {
 // 16-row output tiles per wave
 constexpr int kGemvRtGateUp = 1;
 constexpr int kGemvRtDown = 2;
+constexpr int kGemvFewWaves = 256;  // down launches with fewer (row set, tile) items take one row tile per wave
 
 namespace {
 
@@ -563,6 +564,10 @@ template <int WF>
 hipError_t launch_gemv_wf(const GemmArgs& a, int phase, int max_tiles, hipStream_t stream,
                           const KernelTimer* tm) {
   if (phase == PHASE_GATE_UP) return launch_gemv_rt<WF, PHASE_GATE_UP, kGemvRtGateUp>(a, max_tiles, stream, tm);
+  // few tiles (the shared expert: one): one row tile per wave doubles the
+  // waves streaming the weights
+  if ((int64_t)(a.N / (kGemvRtDown * 16)) * max_tiles < kGemvFewWaves && a.N % 16 == 0)
+    return launch_gemv_rt<WF, PHASE_DOWN, 1>(a, max_tiles, stream, tm);
   return launch_gemv_rt<WF, PHASE_DOWN, kGemvRtDown>(a, max_tiles, stream, tm);
 }
 
