@@ -26,11 +26,13 @@ enum WeightFormat : int { WF_F32 = 0, WF_BF16 = 1, WF_I8 = 2, WF_I4 = 3 };
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
+// round to nearest even; NaN stays NaN (quiet bit set); both results are
+// formed and one selected (no branch)
 __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u | 0x00400000u) >> 16;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t quiet = (u | 0x00400000u) >> 16;
+  return (u & 0x7fffffffu) > 0x7f800000u ? quiet : rounded;
 }
 
 __device__ __forceinline__ float bf16_round(float f) {
@@ -52,12 +54,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float route_expf(float x) {
 #pragma clang fp contract(off)
-  if (x != x) return x;
-  if (x > 89.0f) return __builtin_huge_valf();
-  if (x < -110.0f) x = -110.0f;
-  const float t = x * 0x1.715476p+0f;
+  // every case is computed and one selected (no divergent branches); the
+  // argument is kept finite where its result is selected away
+  const bool nan = x != x;
+  const bool big = x > 89.0f;
+  float xc = x < -110.0f ? -110.0f : x;
+  xc = (nan || big) ? 0.0f : xc;
+  const float t = xc * 0x1.715476p+0f;
   const float n = __builtin_rintf(t);
-  float r = __builtin_fmaf(-n, 0x1.62e430p-1f, x);
+  float r = __builtin_fmaf(-n, 0x1.62e430p-1f, xc);
   r = __builtin_fmaf(-n, -0x1.05c610p-29f, r);
   float p = 0x1.a01a02p-13f;
   p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);
@@ -68,10 +73,13 @@ __device__ __forceinline__ float route_expf(float x) {
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
   const int ni = (int)n;
-  if (ni > 127) return (p * __uint_as_float(254u << 23)) * 2.0f;
-  if (ni >= -126) return p * __uint_as_float((uint32_t)(ni + 127) << 23);
-  return (p * __uint_as_float((uint32_t)(ni + 127 + 64) << 23)) *
-         __uint_as_float((uint32_t)(127 - 64) << 23);
+  const float hi = (p * __uint_as_float(254u << 23)) * 2.0f;                       // ni > 127
+  const float mid = p * __uint_as_float((uint32_t)(ni + 127) << 23);               // -126 <= ni <= 127
+  const float lo = (p * __uint_as_float((uint32_t)(ni + 127 + 64) << 23)) *        // ni < -126
+                   __uint_as_float((uint32_t)(127 - 64) << 23);
+  float y = ni > 127 ? hi : (ni >= -126 ? mid : lo);
+  y = big ? __builtin_huge_valf() : y;
+  return nan ? x : y;
 }
 
 // ---------------------------------------------------------------------------
