@@ -291,6 +291,7 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
                               ? (kStageX + kStageS > kRed ? kStageX + kStageS : kRed)
                               : 16;
   __shared__ __attribute__((aligned(16))) uint8_t lds[S * P][kRegion];
+  __shared__ uint32_t arrived[P];  // K parts of each row set that have stored their sums
 
   const int tile = blockIdx.y;
   const uint32_t lane = threadIdx.x & 63;
@@ -325,6 +326,15 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
     rows = min(16, a.num_rows - row0);
   }
   if (rows <= 0) return;
+  // split-K reduction by the last of a row set's waves to arrive (the others
+  // end at once): measured faster for six or more K parts of the down
+  // projection and of int4 gate_up (Mixtral), slower for fewer parts and
+  // for int8 gate_up, which keep the workgroup barrier
+  constexpr bool kLastReduces = S >= 6 && (PHASE == PHASE_DOWN || WF == WF_I4);
+  if (kLastReduces) {
+    if (threadIdx.x < P) arrived[threadIdx.x] = 0u;
+    __syncthreads();
+  }
   // down: the output row of this lane's position, loaded before the K loop
   int yrow = row0 + (lane & 15);
   if (PHASE == PHASE_DOWN && a.out_rows && (int)(lane & 15) < rows) yrow = a.out_rows[yrow];
@@ -471,7 +481,7 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
     }
   }
 
-  if (S > 1) {
+  if (S > 1 && !kLastReduces) {
     // each wave's partial sums go to its own region (its staged data is
     // consumed), the K part 0 wave adds the S parts in order
 #pragma unroll
@@ -483,6 +493,28 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
       f32x4 s = *(const f32x4*)(lds[wave] + t * 1024 + lane * 16);
 #pragma unroll
       for (int k = 1; k < S; ++k) s += *(const f32x4*)(lds[wave + k] + t * 1024 + lane * 16);
+      acc[t] = s;
+    }
+  }
+  if (kLastReduces) {
+    // each wave's partial sums go to its own region (its staged data is
+    // consumed); the last of the row set's S waves to arrive (an LDS counter:
+    // LDS operations of a wave complete in order, so every earlier arrival's
+    // sums are visible to it) adds the S parts in K-part order, the others
+    // end at once and free their registers
+#pragma unroll
+    for (int t = 0; t < NT; ++t) *(f32x4*)(lds[wave] + t * 1024 + lane * 16) = acc[t];
+    const int rs_local = wave / S;
+    uint32_t prior = 0;
+    if (lane == 0) prior = __hip_atomic_fetch_add(&arrived[rs_local], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+    prior = __builtin_amdgcn_readfirstlane(prior);
+    if (prior != (uint32_t)(S - 1)) return;
+    const int base = rs_local * S;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      f32x4 s = *(const f32x4*)(lds[base] + t * 1024 + lane * 16);
+#pragma unroll
+      for (int k = 1; k < S; ++k) s += *(const f32x4*)(lds[base + k] + t * 1024 + lane * 16);
       acc[t] = s;
     }
   }
