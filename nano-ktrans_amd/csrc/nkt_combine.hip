@@ -137,6 +137,8 @@ __global__ void __launch_bounds__(256) combine_kernel(
 // x * rsqrt(mean(x^2) + eps), rounded to bf16, then times the bf16 weight,
 // rounded again.  Lane l holds the 8-column chunks l, l + 64, ...; the sum of
 // squares adds a lane's chunks in order, then a fixed butterfly.
+constexpr int kNormMaxChunks = 8;  // rows up to 4096 wide stay in registers
+
 __global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* __restrict__ x,
                                                       const uint16_t* __restrict__ w, float eps, int T,
                                                       int H, uint16_t* __restrict__ out) {
@@ -144,6 +146,45 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* __restrict
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const uint16_t* xr = x + (int64_t)t * H;
+  uint16_t* orow = out + (int64_t)t * H;
+  if (H <= kNormMaxChunks * 512) {
+    // the row and the weight in registers, every load issued at once; the
+    // same summation order as below (chunks past H add +0)
+    u32x4 v[kNormMaxChunks], g[kNormMaxChunks];
+#pragma unroll
+    for (int ch = 0; ch < kNormMaxChunks; ++ch) {
+      const int c = lane * 8 + ch * 512;
+      v[ch] = c < H ? *(const u32x4*)(xr + c) : u32x4{0u, 0u, 0u, 0u};
+      g[ch] = c < H ? *(const u32x4*)(w + c) : u32x4{0u, 0u, 0u, 0u};
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int ch = 0; ch < kNormMaxChunks; ++ch) {
+      if (lane * 8 + ch * 512 >= H) continue;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const float a = __uint_as_float(v[ch][h] << 16), b = __uint_as_float(v[ch][h] & 0xffff0000u);
+        ss += a * a;
+        ss += b * b;
+      }
+    }
+    ss = wave_sum_butterfly(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)H + eps);
+#pragma unroll
+    for (int ch = 0; ch < kNormMaxChunks; ++ch) {
+      const int c = lane * 8 + ch * 512;
+      if (c >= H) continue;
+      u32x4 o;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const float a = bf16_round(__uint_as_float(v[ch][h] << 16) * inv);
+        const float b = bf16_round(__uint_as_float(v[ch][h] & 0xffff0000u) * inv);
+        o[h] = pack_bf16x2(a * __uint_as_float(g[ch][h] << 16), b * __uint_as_float(g[ch][h] & 0xffff0000u));
+      }
+      *(u32x4*)(orow + c) = o;
+    }
+    return;
+  }
   float ss = 0.f;
   for (int c = lane * 8; c < H; c += 512) {
     const u32x4 v = *(const u32x4*)(xr + c);
@@ -166,7 +207,7 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* __restrict
       const float b = bf16_round(__uint_as_float(v[h] & 0xffff0000u) * inv);
       o[h] = pack_bf16x2(a * __uint_as_float(g[h] << 16), b * __uint_as_float(g[h] & 0xffff0000u));
     }
-    *(u32x4*)(out + (int64_t)t * H + c) = o;
+    *(u32x4*)(orow + c) = o;
   }
 }
 
