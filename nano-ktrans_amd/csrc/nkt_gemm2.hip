@@ -1,16 +1,24 @@
-// K3, prefill form: grouped SwiGLU expert GEMM for tiles of up to 128
-// positions of one expert (prefill-sized groups), on the bf16 matrix cores.
+// K3, prefill form: grouped SwiGLU expert GEMM for tiles of up to 64
+// positions of one expert (prefill-sized groups), on the matrix cores.
 //
 // Replaces, for large batches, the per-routed-expert loop of
 // nano_ktrans/layers/hybrid_moe.py:3501-3533 (SparseExpertMLP /
 // PackedSparseExpertMLP.forward, nano_ktrans/layers/expert_mlp.py:20-41) and
 // the quantized loop of nano_ktrans/kernels/cpu_moe.py:419-450.
 //
-// Workgroup = 4 or 8 waves, tile = 64 positions x 256 weight rows, two
-// workgroups per CU.  gate_up: the 256 rows are 128 gate rows and the 128
-// matching up rows (a wave holds gate and up rows for the same h columns, so
-// SwiGLU is wave-local); down: 256 output rows split over the waves.  K
-// advances one 128-wide group per step:
+// Three kernels share the work order, tile record and epilogue:
+//   * gemm2_i8_kernel (int8): 4 waves, three-stage pipeline of 64-wide K
+//     stages (tokens direct-to-LDS, weights in a register ring), gate_up on
+//     the fp16 matrix cores;
+//   * gemm2_i4_kernel (int4 g128): 8 waves, three-stage pipeline of 128-wide
+//     K stages (tokens, scales and group sums direct-to-LDS, weights in a
+//     register ring);
+//   * gemm2_kernel (bf16 weights, and int8 / int4 operands past the
+//     pipelines' 32-bit buffer offsets): the register-staged form below.
+// Tile = 64 positions x 256 weight rows.  gate_up: the 256 rows are 128 gate
+// rows and the 128 matching up rows (a wave holds gate and up rows for the
+// same h columns, so SwiGLU is wave-local); down: 256 output rows split over
+// the waves.  In gemm2_kernel K advances one 128-wide group per step:
 //   * the token tile (64 positions x 128 K, bf16, gathered through the
 //     permutation for gate_up) is staged in LDS, double-buffered: the next
 //     group's rows load into registers while this group computes;
@@ -18,13 +26,14 @@
 //     16-byte load per lane per 1 KiB block), one group ahead;
 //   * per group a wave runs 4 (or 2) row tiles x 4 column tiles x 4 K steps of
 //     v_mfma_f32_16x16x32_bf16, dequantising each weight fragment once.
-// Codes enter the matrix core as exact bf16 integers with an offset (int4:
-// 136 + q, int8: 128 + q); the offset times the group's activation sum
-// (precomputed per source row and group, fp32) is removed per group for
-// int4, whose group scale then multiplies the group's fp32 partial; for int8
-// the offset times the row's total sum is removed once and the per-row scale
-// multiplies the total.  gate_up also writes the per-position group
-// sums of the bf16 h it stores, which the down projection consumes.
+// Codes enter the matrix core as exact integers with an offset (int4: bf16
+// 136 + q, int8: bf16 128 + q, or fp16 1152 + q in the int8 gate_up); the
+// offset times the group's activation sum (precomputed per source row and
+// group, fp32) is removed per group for int4, whose group scale then
+// multiplies the group's fp32 partial; for int8 the offset times the row's
+// total sum is removed once and the per-row scale multiplies the total.
+// gate_up also writes the per-position group sums of the bf16 h it stores,
+// which the down projection consumes.
 #include "nkt_common.h"
 #include "nkt_internal.h"
 

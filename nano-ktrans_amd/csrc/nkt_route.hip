@@ -19,8 +19,9 @@
 // cross-lane shuffles sit on the selection's critical path.
 //
 // Small batches run route and grouping in one launch (one workgroup of 16
-// waves); large batches use a wave-per-token route launch and a grouping
-// launch.
+// waves routes the tokens, then one wave groups them from the selection
+// masks); large batches use a wave-per-token route launch and a grouping
+// launch over many workgroups.
 #include "nkt_common.h"
 #include "nkt_internal.h"
 
