@@ -206,6 +206,35 @@ def test_stages_match_forward(gpu_device):
     assert torch.allclose(gate.cpu(), ref_gate, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("name,E,T", [("qwen15_int8_shared", None, 16), ("qwen3_int4", 32, 16)])
+def test_graph_replay_matches_eager(gpu_device, name, E, T):
+    """The layer captured in a HIP graph (the shared expert as a forked branch
+    for Qwen1.5) replays bit for bit like the eager call, replay after replay,
+    with eager calls on the same workspace in between."""
+    announce(f"graph replay {name} T={T}")
+    layer, native = _layer(name, E=E)
+    x, logits = build_inputs(layer, T, seed=21, device="cuda")
+    eager = native.forward(x, logits).clone()
+    out = torch.empty_like(eager)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        native.forward(x, logits, out=out)  # warm the workspace outside capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        native.forward(x, logits, out=out)
+    for _ in range(4):
+        out.zero_()
+        x2, l2 = build_inputs(layer, T, seed=22, device="cuda")
+        native.forward(x2, l2)  # other eager work on the same workspace
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+
+
 @pytest.mark.parametrize("name,T", [("qwen3_int4", 16), ("qwen3_int8", 512)])
 def test_timed_phases_match_untimed(gpu_device, name, T):
     """The measurement entry point runs the same kernels: bitwise-equal h and y, and
