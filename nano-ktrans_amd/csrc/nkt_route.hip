@@ -224,37 +224,45 @@ __global__ void __launch_bounds__(256) route_kernel(const void* __restrict__ log
 }
 
 // ---------------------------------------------------------------------------
-// K2 for small batches (T <= 64), one wave, from the selection masks K1
-// leaves in LDS (token t's experts as bits of selmask[t]).  A token picks an
-// expert at most once, so expert e's pairs are the set bits of a 64-bit
-// token mask M_e (bit t: token t picked e); lane l owns the VPL consecutive
-// experts VPL l .. VPL l + VPL - 1:
-//   * M_e by transposing the token masks (T words read per lane, one bit
-//     field extract and insert per token and expert);
-//   * count_e = popcount(M_e), tiles_e = ceil(count_e / bm) (0 when e is not
+// K2 for small batches (T <= 64), from the selection masks K1 leaves in LDS
+// (token t's experts as bits of selmask[t]).  A token picks an expert at most
+// once, so expert e's pairs are the set bits of a 64-bit token mask M_e
+// (bit t: token t picked e).  Two steps:
+//   * group_scan, one wave, lane l owning the VPL consecutive experts
+//     VPL l .. VPL l + VPL - 1: M_e by transposing the token masks (T words
+//     read per lane, one bit field extract and insert per token and expert);
+//     count_e = popcount(M_e), tiles_e = ceil(count_e / bm) (0 when e is not
 //     HBM-resident); one wave scan of count | tiles << 16 in expert order
-//     gives every expert its first position and first tile;
-//   * expert lanes write counts, offsets, tile records and the tiles'
-//     source columns (the set bits of M_e in ascending order);
-//   * pair p = t k + slot with expert e lands at position
+//     gives every expert its first position and first tile; M_e, the first
+//     position and first tile, the count and the tile -> expert map go to LDS;
+//   * group_write, the whole workgroup, one output element per thread:
+//     counts, offsets, tile records; column r of an expert's tiles = its r-th
+//     token = the r-th set bit of M_e (a six-step popcount select); pair
+//     p = t k + slot with expert e lands at position
 //     off_e + popcount(M_e & (2^t - 1)): tokens ascend within an expert, as
 //     the reference's stable grouping orders them.
 // ---------------------------------------------------------------------------
 constexpr int kGroupWaves = 16;  // waves of the fused route + group workgroup
 constexpr int kGroupThreads = 64 * kGroupWaves;
+// tiles of the fused grouping: sum of ceil(count_e / bm) <= P / bm + min(P, E)
+constexpr int kFusedMaxTiles = kFusedRouteMaxPairs + kMaxExperts;
 
-// selmask: [T][8] u32 words (LDS); ids: the P = T k expert ids (LDS);
-// mlo/mhi/offl: LDS scratch of at least E entries; res: this lane's experts
-// are HBM-resident (bit i for expert VPL lane + i).  Runs in one wave.
+// LDS the two grouping steps share
+struct GroupLds {
+  uint32_t mlo[kMaxExperts], mhi[kMaxExperts];  // M_e
+  int32_t off[kMaxExperts];                     // first position of expert e
+  int32_t toff[kMaxExperts];                    // first tile of expert e
+  int32_t cnt[kMaxExperts];                     // count_e
+  int32_t tmap[kFusedMaxTiles];                 // tile -> expert
+  int32_t n_tile_all;
+};
+
+// selmask: [T][8] u32 words (LDS); res: this lane's experts are HBM-resident
+// (bit i for expert VPL lane + i).  Runs in one wave.
 template <int VPL>
-__device__ __forceinline__ void group_masks(const uint32_t (*selmask)[8], const int32_t* ids, int T, int k, int E,
-                                            int bm, int max_tiles, unsigned res, int32_t* __restrict__ counts,
-                                            int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
-                                            int32_t* __restrict__ inv, int32_t* __restrict__ tiles,
-                                            int32_t* __restrict__ n_tiles, int32_t* __restrict__ tile_src,
-                                            uint32_t* mlo, uint32_t* mhi, int32_t* offl) {
+__device__ __forceinline__ void group_scan(const uint32_t (*selmask)[8], int T, int E, int bm, unsigned res,
+                                           GroupLds& g) {
   const int lane = threadIdx.x & 63;
-  const int P = T * k;
   const int lg_bm = __builtin_ctz(bm);
   // token masks of this lane's experts
   uint32_t lo[VPL], hi[VPL];
@@ -283,52 +291,85 @@ __device__ __forceinline__ void group_masks(const uint32_t (*selmask)[8], const 
     lane_val += cnt[i] | (nt[i] << 16);
   }
   const int incl = wave_inclusive_scan(lane_val);
-  const int n_tile_all = __builtin_amdgcn_readlane(incl, 63) >> 16;
   int run = incl - lane_val;  // this lane's first (position | tile << 16)
-
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
     const int e = VPL * lane + i;
     const int off = run & 0xffff, toff = run >> 16;
     run += cnt[i] | (nt[i] << 16);
     if (e >= E) continue;
-    counts[e] = cnt[i];
-    offsets[e] = off;
-    mlo[e] = lo[i];
-    mhi[e] = hi[i];
-    offl[e] = off;
-    for (int m = 0; m < nt[i]; ++m) {
-      const int ti = toff + m;
-      if (ti < max_tiles) *(int4*)(tiles + 4 * ti) = int4{e, off + m * bm, min(bm, cnt[i] - m * bm), 0};
-    }
-    if (tile_src && nt[i] > 0) {
-      // column r of the expert's tiles = its r-th token; unused columns 0
-      uint64_t mm = ((uint64_t)hi[i] << 32) | lo[i];
-      for (int r = 0; mm; ++r) {
-        const int ti = toff + (r >> lg_bm);
-        if (ti < max_tiles) tile_src[ti * kTileSrcCols + (r & (kTileSrcCols - 1))] = __builtin_ctzll(mm);
-        mm &= mm - 1;
-      }
-      const int ti = toff + nt[i] - 1;
-      if (ti < max_tiles)
-        for (int c = cnt[i] - (nt[i] - 1) * bm; c < kTileSrcCols; ++c) tile_src[ti * kTileSrcCols + c] = 0;
-    }
+    g.mlo[e] = lo[i];
+    g.mhi[e] = hi[i];
+    g.off[e] = off;
+    g.toff[e] = toff;
+    g.cnt[e] = cnt[i];
+    for (int m = 0; m < nt[i]; ++m) g.tmap[toff + m] = e;
   }
-  if (lane == 0) {
+  if (lane == 0) g.n_tile_all = __builtin_amdgcn_readlane(incl, 63) >> 16;
+}
+
+// the position (0..63) of the r-th (from 0) set bit of m; r < popcount(m)
+__device__ __forceinline__ int nth_set_bit(uint64_t m, int r) {
+  int pos = 0;
+#pragma unroll
+  for (int w = 32; w >= 1; w >>= 1) {
+    const int c = __popcll(m & ((1ull << w) - 1ull));
+    const bool up = r >= c;
+    r -= up ? c : 0;
+    m = up ? (m >> w) : m;
+    pos += up ? w : 0;
+  }
+  return pos;
+}
+
+// ids: the P = T k expert ids (LDS).  Every thread of the workgroup, after a
+// barrier that follows group_scan.
+__device__ __forceinline__ void group_write(const GroupLds& g, const int32_t* ids, int T, int k, int E, int bm,
+                                            int max_tiles, int32_t* __restrict__ counts,
+                                            int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
+                                            int32_t* __restrict__ inv, int32_t* __restrict__ tiles,
+                                            int32_t* __restrict__ n_tiles, int32_t* __restrict__ tile_src) {
+  const int tid = threadIdx.x;
+  const int P = T * k;
+  const int n_tile_all = g.n_tile_all;
+  const int nt_out = min(n_tile_all, max_tiles);
+  for (int e = tid; e < E; e += kGroupThreads) {
+    counts[e] = g.cnt[e];
+    offsets[e] = g.off[e];
+  }
+  if (tid == 0) {
     offsets[E] = P;
-    n_tiles[0] = min(n_tile_all, max_tiles);
+    n_tiles[0] = nt_out;
   }
-  // records past the last tile say "no rows" (the decode form reads every record up to max_tiles)
-  for (int ti = n_tile_all + lane; ti < max_tiles; ti += 64) *(int4*)(tiles + 4 * ti) = int4{0, 0, 0, 0};
-  wave_lds_sync();
+  // tile records; records past the last tile say "no rows" (the decode form
+  // reads every record up to max_tiles)
+  for (int ti = tid; ti < max_tiles; ti += kGroupThreads) {
+    int4 rec = int4{0, 0, 0, 0};
+    if (ti < n_tile_all) {
+      const int e = g.tmap[ti];
+      const int m = ti - g.toff[e];
+      rec = int4{e, g.off[e] + m * bm, min(bm, g.cnt[e] - m * bm), 0};
+    }
+    *(int4*)(tiles + 4 * ti) = rec;
+  }
+  if (tile_src) {
+    // column c of tile ti: the expert's token of rank (ti - first tile) * 16 + c, unused columns 0
+    for (int i = tid; i < nt_out * kTileSrcCols; i += kGroupThreads) {
+      const int ti = i / kTileSrcCols;
+      const int e = g.tmap[ti];
+      const int r = (ti - g.toff[e]) * kTileSrcCols + (i & (kTileSrcCols - 1));
+      const uint64_t mm = ((uint64_t)g.mhi[e] << 32) | g.mlo[e];
+      tile_src[i] = r < g.cnt[e] ? nth_set_bit(mm, r) : 0;
+    }
+  }
   // positions of the pairs; the token of pair p is p / k = (p ceil(2^32 / k)) >> 32
   const uint64_t kmagic = ((1ull << 32) + (uint64_t)k - 1) / (uint64_t)k;
-  for (int p = lane; p < P; p += 64) {
+  for (int p = tid; p < P; p += kGroupThreads) {
     const int e = ids[p];
     const int t = (int)(((uint64_t)p * kmagic) >> 32);
     const uint32_t below_lo = t >= 32 ? 0xffffffffu : ((1u << t) - 1u);
     const uint32_t below_hi = t <= 32 ? 0u : ((1u << (t - 32)) - 1u);
-    const int pos = offl[e] + __popc(mlo[e] & below_lo) + __popc(mhi[e] & below_hi);
+    const int pos = g.off[e] + __popc(g.mlo[e] & below_lo) + __popc(g.mhi[e] & below_hi);
     perm[pos] = p;
     inv[p] = pos;
   }
@@ -523,8 +564,7 @@ __global__ void __launch_bounds__(kGroupThreads) route_group_kernel(
     const uint8_t* __restrict__ resident) {
   __shared__ int32_t ids_s[kFusedRouteMaxPairs];
   __shared__ uint32_t selmask[kFusedRouteMaxTokens][8];
-  __shared__ uint32_t mlo[kMaxExperts], mhi[kMaxExperts];
-  __shared__ int32_t offl[kMaxExperts];
+  __shared__ GroupLds g;
   __shared__ float sv[kGroupWaves][kMaxTopK];
   __shared__ int si[kGroupWaves][kMaxTopK];
   const int wave = threadIdx.x >> 6;
@@ -549,9 +589,9 @@ __global__ void __launch_bounds__(kGroupThreads) route_group_kernel(
     }
   }
   __syncthreads();
-  if (wave != 0) return;
-  group_masks<VPL>(selmask, ids_s, T, k, E, bm, max_tiles, res, counts, offsets, perm, inv, tiles, n_tiles,
-                   tile_src, mlo, mhi, offl);
+  if (wave == 0) group_scan<VPL>(selmask, T, E, bm, res, g);
+  __syncthreads();
+  group_write(g, ids_s, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, tile_src);
 }
 
 #define NKT_VPL_SWITCH(E, CASE) \
