@@ -287,7 +287,8 @@ def kernel_form(w, T):
         return "gemv_kernel"
     if w.wfmt == "f32":
         return "gemm_kernel"
-    return "gemm2_i8_kernel" if w.wfmt == "int8_per_channel" else "gemm2_kernel"
+    # int8 and int4 (bf16 activations, buffers under 4 GiB: every bench shape) have pipelined kernels
+    return {"int8_per_channel": "gemm2_i8_kernel", "int4_g128": "gemm2_i4_kernel"}.get(w.wfmt, "gemm2_kernel")
 
 
 def bench_workload(w, T, layers, router, steps, warmup, device):
