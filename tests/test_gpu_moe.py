@@ -37,9 +37,11 @@ def _layer(name, E=None, I=None, device="cuda"):
     return _LAYERS[key]
 
 
-def _check(layer, native, T, seed=7):
+def _check(layer, native, T, seed=7, bias=None):
     cfg = layer.cfg
     x, logits = build_inputs(layer, T, seed=seed, device="cuda")
+    if bias is not None:  # skew the routing: bias [E] added to every token's logits
+        logits = (logits.float() + bias.to(logits.device)).to(logits.dtype)
     out = native.forward(x, logits)
     torch.cuda.synchronize()
     ref, parts = oracle_forward(layer, x, logits, return_parts=True)
@@ -65,6 +67,19 @@ def test_qwen3_int4_cut_experts(gpu_device, T):
     announce(f"forward qwen3_int4 E=32 T={T}")
     layer, native = _layer("qwen3_int4", E=32)
     _check(layer, native, T)
+
+
+@pytest.mark.parametrize("T", [40, 48, 64])
+def test_qwen3_int4_decode_form_multi_tile_experts(gpu_device, T):
+    """Four experts picked by every token.  T = 40, 48: the decode form
+    (T k <= 12 E): each hot expert holds T positions in ceil(T / 16) tiles, so
+    the tile records past an expert's first tile and its tiles' source columns
+    of rank >= 16 are used; T = 64 is past that form (prefill tiles)."""
+    announce(f"forward qwen3_int4 E=32 T={T} skewed")
+    layer, native = _layer("qwen3_int4", E=32)
+    bias = torch.zeros(32)
+    bias[[3, 11, 20, 31]] = 30.0
+    _check(layer, native, T, seed=9, bias=bias)
 
 
 @pytest.mark.parametrize("T", [1, 16])

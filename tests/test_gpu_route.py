@@ -94,6 +94,19 @@ def test_route_ties_and_edges(gpu_device, E, k, softmax, renorm, act_dtype):
         _check_route(native, logits, k, softmax, renorm, act_dtype == torch.bfloat16)
 
 
+@pytest.mark.parametrize("E,k", [(256, 16), (128, 16), (60, 4), (8, 2)])
+@pytest.mark.parametrize("T", [63, 64, 65])
+def test_route_fused_limits(gpu_device, E, k, T):
+    """The one-workgroup route + group at its limits (T = 64 tokens, T k up to
+    1024 pairs, E up to 256) and the first size past it, on tie-heavy logits."""
+    announce(f"route fused limits E={E} k={k} T={T}")
+    rng = np.random.default_rng(E + 7 * k + T)
+    native = _router_only(E, k, True, True, torch.bfloat16, gpu_device)
+    for c in (np.round(rng.standard_normal((T, E)) * 2) / 2, rng.standard_normal((T, E))):
+        logits = torch.from_numpy(c.astype(np.float32)).to(torch.bfloat16).to(gpu_device)
+        _check_route(native, logits, k, True, True, True)
+
+
 def test_route_repeatable(gpu_device):
     announce("route repeatable")
     native = _router_only(128, 8, True, True, torch.bfloat16, gpu_device)
