@@ -651,8 +651,12 @@ int nkt_moe_bind_weights(void* handle, const void* const* ptrs, char* err, size_
 
 int nkt_moe_workspace_bytes(void* handle, int num_tokens, size_t* bytes, char* err, size_t err_len) {
   Handle* h = (Handle*)handle;
-  if (!h || !bytes || num_tokens < 0 || num_tokens > h->max_tokens) {
-    set_err(err, err_len, "bad arguments");
+  if (!h || !bytes) {
+    set_err(err, err_len, "null handle or output pointer");
+    return NKT_ERR;
+  }
+  if (num_tokens < 0 || num_tokens > h->max_tokens) {
+    set_err(err, err_len, "num_tokens=%d outside [0, max_tokens=%d]", num_tokens, h->max_tokens);
     return NKT_ERR;
   }
   *bytes = ws_layout(h, num_tokens).total;
@@ -662,9 +666,16 @@ int nkt_moe_workspace_bytes(void* handle, int num_tokens, size_t* bytes, char* e
 int nkt_moe_workspace_region(void* handle, int num_tokens, int region, size_t* offset, char* err,
                              size_t err_len) {
   Handle* h = (Handle*)handle;
-  if (!h || !offset || num_tokens < 0 || num_tokens > h->max_tokens || region < 0 ||
-      region >= NKT_WS_NUM_REGIONS) {
-    set_err(err, err_len, "bad arguments");
+  if (!h || !offset) {
+    set_err(err, err_len, "null handle or output pointer");
+    return NKT_ERR;
+  }
+  if (num_tokens < 0 || num_tokens > h->max_tokens) {
+    set_err(err, err_len, "num_tokens=%d outside [0, max_tokens=%d]", num_tokens, h->max_tokens);
+    return NKT_ERR;
+  }
+  if (region < 0 || region >= NKT_WS_NUM_REGIONS) {
+    set_err(err, err_len, "region=%d outside [0, %d)", region, NKT_WS_NUM_REGIONS);
     return NKT_ERR;
   }
   *offset = ws_layout(h, num_tokens).off[region];

@@ -82,6 +82,22 @@ def test_qwen3_int4_decode_form_multi_tile_experts(gpu_device, T):
     _check(layer, native, T, seed=9, bias=bias)
 
 
+@pytest.mark.parametrize("max_tokens", [1, 48])
+def test_empty_and_max_token_batches(gpu_device, max_tokens):
+    """An empty batch returns an empty output without a launch; a batch of
+    exactly max_tokens matches the oracle; one token more is rejected."""
+    from nano_ktrans_amd import _native as N
+
+    announce(f"empty / max_tokens={max_tokens} small_int8_shared")
+    layer = build_layer(CONFIGS["small_int8_shared"], device="cuda")
+    native = native_layer(layer, torch.device("cuda"), max_tokens=max_tokens)
+    x, logits = build_inputs(layer, max_tokens + 1, seed=13, device="cuda")
+    assert native.forward(x[:0], logits[:0]).shape == (0, layer.cfg.H)
+    _check(layer, native, max_tokens, seed=13)
+    with pytest.raises(N.NativeError, match="max_tokens"):
+        native.forward(x, logits)
+
+
 @pytest.mark.parametrize("T", [1, 16])
 def test_qwen3_int4_full(gpu_device, T):
     announce(f"forward qwen3_int4 full T={T}")
