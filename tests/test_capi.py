@@ -104,6 +104,12 @@ def test_calls_validate_before_touching_the_gpu():
     assert b"workspace" in eb.value
     assert lib.nkt_moe_route(h, None, 65, None, 0, None, eb, 256) == -1
     assert b"max_tokens" in eb.value
+    nbytes, off = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    assert lib.nkt_moe_workspace_bytes(h, 65, ctypes.byref(nbytes), eb, 256) == -1
+    assert b"max_tokens=64" in eb.value
+    assert lib.nkt_moe_workspace_bytes(h, 64, ctypes.byref(nbytes), eb, 256) == 0 and nbytes.value > 0
+    assert lib.nkt_moe_workspace_region(h, 1, N.WS_NORMED + 1, ctypes.byref(off), eb, 256) == -1
+    assert b"region" in eb.value
     assert lib.nkt_moe_pack_weight(h, 1, 0, None, None, None, None, None, eb, 256) == -1
     assert lib.nkt_moe_pack_weight(h, 0, 9, None, None, None, None, None, eb, 256) == -1
     assert lib.nkt_moe_shared(h, None, 1, None, 0, None, eb, 256) == -1
