@@ -318,25 +318,30 @@ int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, 
 
 // Router GEMV (decode-form GEMM over dense 16-token tiles, bf16 gate rows)
 // into the bf16 logits region, then K1 + K2 on those logits.
-int do_route_hidden(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipStream_t st, char* err,
-                    size_t len) {
+bool check_route_hidden(const Handle* h, const void* x, char* err, size_t len) {
   if (!x) {
     set_err(err, len, "null hidden_states");
-    return NKT_ERR;
+    return false;
   }
   if (!h->act_bf16) {
     set_err(err, len, "the fused router needs bf16 activations");
-    return NKT_ERR;
+    return false;
   }
   if (!h->w[NKT_SLOT_ROUTER]) {
     set_err(err, len, "router weight not bound (NKT_SLOT_ROUTER)");
-    return NKT_ERR;
+    return false;
   }
-  const int Ep = router_rows(h);
-  if (!gemv_supported(WF_BF16, PHASE_DOWN, Ep, h->H, 0)) {
+  if (!gemv_supported(WF_BF16, PHASE_DOWN, router_rows(h), h->H, 0)) {
     set_err(err, len, "hidden size %d unsupported by the router GEMM", h->H);
-    return NKT_ERR;
+    return false;
   }
+  return true;
+}
+
+int do_route_hidden(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipStream_t st, char* err,
+                    size_t len) {
+  if (!check_route_hidden(h, x, err, len)) return NKT_ERR;
+  const int Ep = router_rows(h);
   GemmArgs r;
   memset(&r, 0, sizeof(r));
   r.w = (const uint8_t*)h->w[NKT_SLOT_ROUTER];
@@ -484,9 +489,20 @@ bool shared_side_ready(Handle* h, int T, const WsLayout& L, hipStream_t st) {
 // everything the caller queued on st (its input is ready) and joins back
 // before the combine: it overlaps the routing and the routed experts, and a
 // graph captured on st holds it as a parallel branch.
+// The caller has checked the routing input (logits, or x and the router);
+// every other argument and weight slot is checked here before the fork, so
+// that a rejected call leaves no fork behind.  After the fork the join is
+// recorded and waited for on every path, errors included: the caller's
+// stream never runs ahead of the side stream's reads of x and the workspace,
+// and a graph being captured on st stays joined.
 template <typename Route>
 int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayout& L, hipStream_t st, char* err,
               size_t len, Route route, const void* residual = nullptr) {
+  if (!x || !out) {
+    set_err(err, len, "null hidden_states or output");
+    return NKT_ERR;
+  }
+  if (!check_weights(h, h->Is > 0, err, len)) return NKT_ERR;
   std::unique_lock<std::mutex> lk(h->side_mu, std::defer_lock);
   const bool side = shared_side_ready(h, T, L, st);
   if (side) {
@@ -494,13 +510,26 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
     if (!check_hip(hipEventRecord(h->fork_ev, st), "fork event", err, len) ||
         !check_hip(hipStreamWaitEvent(h->side, h->fork_ev, 0), "fork wait", err, len))
       return NKT_ERR;
-    if (do_shared(h, x, T, ws, L, h->side, err, len) != NKT_OK) return NKT_ERR;
-    if (!check_hip(hipEventRecord(h->join_ev, h->side), "join event", err, len)) return NKT_ERR;
+    const int rs = do_shared(h, x, T, ws, L, h->side, err, len);
+    const hipError_t je = hipEventRecord(h->join_ev, h->side);
+    if (je != hipSuccess) {
+      if (rs == NKT_OK) check_hip(je, "join event", err, len);
+      (void)hipStreamSynchronize(h->side);  // no event to wait on: drain the branch instead
+      return NKT_ERR;
+    }
+    if (rs != NKT_OK) {
+      (void)hipStreamWaitEvent(st, h->join_ev, 0);
+      return NKT_ERR;
+    }
   }
-  if (route() != NKT_OK) return NKT_ERR;
-  if (do_experts(h, x, T, ws, L, st, err, len) != NKT_OK) return NKT_ERR;
-  if (!side && h->Is > 0 && do_shared(h, x, T, ws, L, st, err, len) != NKT_OK) return NKT_ERR;
-  if (side && !check_hip(hipStreamWaitEvent(st, h->join_ev, 0), "join wait", err, len)) return NKT_ERR;
+  int rc = route();
+  if (rc == NKT_OK) rc = do_experts(h, x, T, ws, L, st, err, len);
+  if (rc == NKT_OK && !side && h->Is > 0) rc = do_shared(h, x, T, ws, L, st, err, len);
+  if (side) {
+    const hipError_t we = hipStreamWaitEvent(st, h->join_ev, 0);
+    if (rc == NKT_OK && !check_hip(we, "join wait", err, len)) rc = NKT_ERR;
+  }
+  if (rc != NKT_OK) return rc;
   return do_combine(h, T, out, ws, L, st, err, len, nullptr, residual);
 }
 
@@ -778,6 +807,10 @@ int nkt_moe_forward(void* handle, const void* hidden_states, const void* router_
   Handle* h = (Handle*)handle;
   if (!check_call(h, num_tokens, workspace, workspace_bytes, err, err_len)) return NKT_ERR;
   if (num_tokens == 0) return NKT_OK;
+  if (!router_logits) {
+    set_err(err, err_len, "null router_logits");
+    return NKT_ERR;
+  }
   const WsLayout L = ws_layout(h, num_tokens);
   hipStream_t st = (hipStream_t)stream;
   return run_layer(h, hidden_states, num_tokens, out, workspace, L, st, err, err_len,
@@ -798,6 +831,7 @@ int nkt_moe_forward_hidden(void* handle, const void* hidden_states, int num_toke
   Handle* h = (Handle*)handle;
   if (!check_call(h, num_tokens, workspace, workspace_bytes, err, err_len)) return NKT_ERR;
   if (num_tokens == 0) return NKT_OK;
+  if (!check_route_hidden(h, hidden_states, err, err_len)) return NKT_ERR;
   const WsLayout L = ws_layout(h, num_tokens);
   hipStream_t st = (hipStream_t)stream;
   return run_layer(h, hidden_states, num_tokens, out, workspace, L, st, err, err_len,
@@ -825,6 +859,7 @@ int nkt_moe_forward_block(void* handle, const void* hidden_states, const void* n
   const WsLayout L = ws_layout(h, num_tokens);
   hipStream_t st = (hipStream_t)stream;
   void* x = ws_ptr<void>(workspace, L, NKT_WS_NORMED);
+  if (!check_route_hidden(h, x, err, err_len) || !check_weights(h, h->Is > 0, err, err_len)) return NKT_ERR;
   if (!check_hip(launch_rmsnorm(hidden_states, norm_weight, eps, num_tokens, h->H, x, st), "rmsnorm kernel", err,
                  err_len))
     return NKT_ERR;

@@ -108,6 +108,10 @@ class ExpertWeightLoader:
     def has_key(self, key: str) -> bool:
         return key in self._key_to_file
 
+    def load_tensor(self, key: str) -> torch.Tensor:
+        """One tensor by its checkpoint key (contiguous, on the CPU)."""
+        return self._load_tensor(key)
+
     def _load_tensor(self, key: str) -> torch.Tensor:
         file_path = self._key_to_file.get(key)
         if file_path is None:

@@ -138,7 +138,7 @@ class HybridMoE(nn.Module):
         self.shared_expert_gate = shared_expert_gate
         # optional router nn.Linear(H, E, bias=False) (the decoder layer's self.gate,
         # nano_ktrans/models/mixtral.py:127): with it, forward(x) without
-        # router_logits runs the router GEMV fused into the routing launch
+        # router_logits runs the router GEMV inside the expert path (the library)
         self.gate = gate
         self.max_tokens = max_tokens
         mask = [bool(m) for m in gpu_experts_mask.reshape(-1).tolist()] if gpu_experts_mask is not None \
@@ -234,7 +234,7 @@ class HybridMoE(nn.Module):
     def forward(self, hidden_states: torch.Tensor, router_logits: Optional[torch.Tensor] = None) -> torch.Tensor:
         """The reference forward (hidden_states, router_logits).  router_logits=None
         (with gate= given at construction, bf16 activations) computes the logits
-        inside the expert path: the router GEMV fused with routing."""
+        inside the expert path: the library runs the router GEMV, then routing."""
         self.forward_calls += 1
         self.last_phase = "prefill" if get_context().is_prefill else "decode"
         native = self._ensure(hidden_states)

@@ -98,6 +98,7 @@ class NativeMoE:
                 self.slots[slot] = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         self._bind()
         self._ws: Optional[torch.Tensor] = None
+        self._ws_streams: set = set()
 
     def __del__(self):
         h = getattr(self, "handle", None)
@@ -204,9 +205,21 @@ class NativeMoE:
         return nbytes.value
 
     def workspace(self, num_tokens: int) -> torch.Tensor:
+        """The workspace for num_tokens tokens, grown when too small.  Every
+        stream a call enqueued on is remembered: before a smaller buffer is
+        dropped it is marked in use on each of them (record_stream), so the
+        caching allocator does not hand its memory out while kernels queued
+        there may still read or write it.  (The library's own side stream
+        joins back into the caller's stream before each call returns.)"""
         need = self.workspace_bytes(num_tokens)
+        stream = torch.cuda.current_stream(self.device)
         if self._ws is None or self._ws.numel() < need:
+            if self._ws is not None:
+                for s in self._ws_streams:
+                    self._ws.record_stream(s)
             self._ws = torch.empty(max(need, 256), dtype=torch.uint8, device=self.device)
+            self._ws_streams = set()
+        self._ws_streams.add(stream)
         return self._ws
 
     def region(self, num_tokens: int, region: int, dtype: torch.dtype, shape) -> torch.Tensor:

@@ -305,20 +305,27 @@ def _lin(x: np.ndarray, w) -> np.ndarray:
     return x.astype(np.float32) @ np.asarray(w, dtype=np.float32).T
 
 
-def expert_forward(x: np.ndarray, ex: Expert) -> np.ndarray:
-    """down(silu(gate(x)) * up(x)) in fp32."""
+def expert_forward(x: np.ndarray, ex: Expert, h_bf16: bool = False) -> np.ndarray:
+    """down(silu(gate(x)) * up(x)) in fp32.  h_bf16: the SwiGLU output h is
+    rounded to bf16 before the down projection, as a bf16 module stores it
+    (nano_ktrans/layers/expert_mlp.py:20-23 in bf16: act_fn(w1 x) * w3 x is a
+    bf16 tensor)."""
     g = _lin(x, ex.gate)
     u = _lin(x, ex.up)
-    return _lin(silu(g) * u, ex.down)
+    h = silu(g) * u
+    if h_bf16:
+        h = bf16_round(h)
+    return _lin(h, ex.down)
 
 
 def moe_forward(x: np.ndarray, logits: np.ndarray, experts: List[Expert], top_k: int,
                 use_softmax: bool, renorm: bool, bf16: bool,
                 shared: Optional[Expert] = None, shared_gate: Optional[np.ndarray] = None,
-                return_parts: bool = False):
+                return_parts: bool = False, h_bf16: bool = False):
     """MoE layer output in fp32 before the final cast (cast with ``bf16_round`` for bf16).
 
-    x [T, H] and logits [T, E] hold the activation-dtype values as float32."""
+    x [T, H] and logits [T, E] hold the activation-dtype values as float32.
+    h_bf16: every expert's SwiGLU output rounded to bf16 (``expert_forward``)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     T, H = x.shape
     E = len(experts)
@@ -331,7 +338,7 @@ def moe_forward(x: np.ndarray, logits: np.ndarray, experts: List[Expert], top_k:
             continue
         pairs = perm[offsets[e]:offsets[e + 1]]
         toks = pairs // top_k
-        y = expert_forward(x[toks], experts[e])
+        y = expert_forward(x[toks], experts[e], h_bf16)
         y_pairs[pairs] = y
         out[toks] += y * w.reshape(-1)[pairs][:, None]
     gate_vals = None
@@ -339,7 +346,7 @@ def moe_forward(x: np.ndarray, logits: np.ndarray, experts: List[Expert], top_k:
     if shared is not None:
         gl = x @ np.asarray(shared_gate, dtype=np.float32).reshape(-1)
         gate_vals = (np.float32(1.0) / (np.float32(1.0) + np.exp(-gl.astype(np.float32)))).astype(np.float32)
-        y_shared = expert_forward(x, shared)
+        y_shared = expert_forward(x, shared, h_bf16)
         out += gate_vals[:, None] * y_shared
     if return_parts:
         return out, dict(ids=ids, weights=w, counts=counts, offsets=offsets, perm=perm, inv=inv,

@@ -131,7 +131,8 @@ def _to_oracle(w):
     return w.cpu().numpy().astype(np.float32)
 
 
-def oracle_forward(layer: Layer, x: torch.Tensor, logits: torch.Tensor, return_parts: bool = False):
+def oracle_forward(layer: Layer, x: torch.Tensor, logits: torch.Tensor, return_parts: bool = False,
+                   h_bf16: bool = False):
     cfg = layer.cfg
     experts = [O.Expert(_to_oracle(e["gate"]), _to_oracle(e["up"]), _to_oracle(e["down"])) for e in layer.experts]
     shared = None
@@ -142,7 +143,7 @@ def oracle_forward(layer: Layer, x: torch.Tensor, logits: torch.Tensor, return_p
         x.float().cpu().numpy(), logits.float().cpu().numpy(), experts, cfg.k, cfg.softmax, cfg.renorm,
         cfg.act == "bf16", shared=shared,
         shared_gate=None if layer.shared_gate is None else layer.shared_gate.cpu().numpy(),
-        return_parts=return_parts)
+        return_parts=return_parts, h_bf16=h_bf16)
 
 
 def native_layer(layer: Layer, device, max_tokens: int = 8192):

@@ -302,3 +302,113 @@ def test_fused_decoder_block(gpu_device, T):
          "down": _bf16(experts[str(e)].w2.weight)} for e in range(E)])
     moe_ref = oracle_forward(layer, torch.from_numpy(xg), logits.cpu())
     _check(out, h.float().cpu().numpy() + moe_ref)
+
+
+def test_safetensors_qwen3_packed_dense(gpu_device, tmp_path):
+    """Qwen3 checkpoint with packed dense experts: ``gate_up_proj.weight``
+    [2I, H] split into gate (first I rows) and up by the loader
+    (nano_ktrans/kernels/weight_loader.py:355-392), every expert read from disk."""
+    from safetensors.torch import save_file
+
+    announce("HybridMoE from safetensors: qwen3 packed gate_up (dense bf16)")
+    E, k, H, I, T = 16, 8, 1024, 384, 11
+    g = torch.Generator().manual_seed(21)
+    ck, weights = {}, []
+    for e in range(E):
+        gu = (torch.randn(2 * I, H, generator=g) * 0.02).to(torch.bfloat16)
+        dn = (torch.randn(H, I, generator=g) * 0.02).to(torch.bfloat16)
+        ck[f"model.layers.3.mlp.experts.{e}.gate_up_proj.weight"] = gu
+        ck[f"model.layers.3.mlp.experts.{e}.down_proj.weight"] = dn
+        weights.append({"gate": gu[:I].float(), "up": gu[I:].float(), "down": dn.float()})
+    save_file(ck, str(tmp_path / "model.safetensors"))
+    moe = HybridMoE(E, k, H, I, nn.ModuleDict(), torch.zeros(E, dtype=torch.bool), 3, str(tmp_path),
+                    router_use_softmax=True, normalize_topk_prob=True, experts_are_packed=True,
+                    expert_key_template=QWEN3_MOE_SPEC.expert_key_template,
+                    expert_proj_names=QWEN3_MOE_SPEC.expert_proj_names)
+    x, logits = _inputs(T, H, E, seed=22)
+    out = moe(x.to(gpu_device), logits.to(gpu_device))
+    assert moe._native.weight_format == "bf16"
+    layer = Layer(MoEConfig("p", H, E, k, I, 0, True, True, "bf16", "bf16"), torch.zeros(E, H), weights)
+    _check(out, oracle_forward(layer, x, logits))
+
+
+def test_safetensors_qwen2_moe_with_shared_expert(gpu_device, tmp_path):
+    """Qwen2-MoE checkpoint: routed experts under ``mlp.experts.{e}.{gate,up,down}_proj``,
+    the shared expert under ``mlp.shared_expert.{gate,up,down}_proj`` and its gate
+    ``mlp.shared_expert_gate.weight`` [1, H] (nano_ktrans/models/config.py:37-49,
+    nano_ktrans/models/mixtral.py:404-426), quantized to int8 at ingest."""
+    from safetensors.torch import save_file
+
+    from nano_ktrans_amd.layers.expert_mlp import load_shared_expert_modules
+    from nano_ktrans_amd.models.config import QWEN2_MOE_SPEC
+
+    announce("HybridMoE from safetensors: qwen2-moe + shared expert (int8 at ingest)")
+    E, k, H, I, Is, T = 12, 4, 2048, 256, 512, 10
+    g = torch.Generator().manual_seed(23)
+    ck, weights = {}, []
+    for e in range(E):
+        w = {p: (torch.randn(s, generator=g) * 0.02).to(torch.bfloat16)
+             for p, s in (("gate", (I, H)), ("up", (I, H)), ("down", (H, I)))}
+        for p, t in w.items():
+            ck[QWEN2_MOE_SPEC.expert_key_template.format(layer=0, expert=e, proj=p)] = t
+        weights.append(w)
+    shared = {p: (torch.randn(s, generator=g) * 0.02).to(torch.bfloat16)
+              for p, s in (("gate", (Is, H)), ("up", (Is, H)), ("down", (H, Is)))}
+    for p, t in shared.items():
+        ck[QWEN2_MOE_SPEC.shared_expert_key_template.format(layer=0, proj=p)] = t
+    sg = (torch.randn(1, H, generator=g) * 0.02).to(torch.bfloat16)
+    ck["model.layers.0.mlp.shared_expert_gate.weight"] = sg
+    save_file(ck, str(tmp_path / "model.safetensors"))
+    sh_mod, sh_gate = load_shared_expert_modules(str(tmp_path), 0, QWEN2_MOE_SPEC, hidden_size=H,
+                                                 shared_intermediate_size=Is)
+    assert torch.equal(sh_mod.w1.weight, shared["gate"]) and torch.equal(sh_mod.w3.weight, shared["up"])
+    assert torch.equal(sh_mod.w2.weight, shared["down"]) and torch.equal(sh_gate.weight, sg)
+    moe = HybridMoE(E, k, H, I, nn.ModuleDict(), torch.zeros(E, dtype=torch.bool), 0, str(tmp_path),
+                    router_use_softmax=QWEN2_MOE_SPEC.router_use_softmax,
+                    normalize_topk_prob=QWEN2_MOE_SPEC.normalize_topk_prob,
+                    expert_key_template=QWEN2_MOE_SPEC.expert_key_template,
+                    expert_proj_names=QWEN2_MOE_SPEC.expert_proj_names, quantization="int8_per_channel",
+                    shared_expert=sh_mod.to(gpu_device), shared_expert_gate=sh_gate.to(gpu_device))
+    x, logits = _inputs(T, H, E, seed=24)
+    out = moe(x.to(gpu_device), logits.to(gpu_device))
+    q = lambda w: to_bf16_scales(quantize_symmetric_int8_per_channel(w.float()))
+    layer = Layer(MoEConfig("s", H, E, k, I, Is, True, False, "bf16", "int8_per_channel"), torch.zeros(E, H),
+                  [{p: q(w[p]) for p in ("gate", "up", "down")} for w in weights],
+                  shared={p: q(shared[p]) for p in ("gate", "up", "down")},
+                  shared_gate=sg.float().reshape(-1))
+    _check(out, oracle_forward(layer, x, logits))
+
+
+def test_safetensors_int8_per_channel_gptq(gpu_device, tmp_path):
+    """int8 checkpoint in the GPTQ on-disk layout with ``group_size: -1`` (one
+    scale per output row): qweight [in/4, out] int32 (byte j of a word = input
+    row 4w + j, stored q + 128), scales [1, out] in fp16."""
+    from safetensors.torch import save_file
+
+    announce("HybridMoE from safetensors: int8 bits=8 group_size=-1")
+    E, k, H, I, T = 8, 2, 512, 256, 13
+    g = torch.Generator().manual_seed(25)
+    ck, qlayers = {}, []
+    for e in range(E):
+        qe = {}
+        for p, s in (("gate_proj", (I, H)), ("up_proj", (I, H)), ("down_proj", (H, I))):
+            qw = to_bf16_scales(quantize_symmetric_int8_per_channel(torch.randn(s, generator=g) * 0.02))
+            pre = f"model.layers.0.mlp.experts.{e}.{p}"
+            ck[f"{pre}.qweight"] = qw.qweight.T.contiguous()
+            # bf16 scales of these magnitudes are fp16-representable (exact round trip)
+            ck[f"{pre}.scales"] = qw.scales.T.contiguous().to(torch.float16)
+            assert torch.equal(ck[f"{pre}.scales"].float(), qw.scales.T.float())
+            qe[p] = qw
+        qlayers.append({"gate": qe["gate_proj"], "up": qe["up_proj"], "down": qe["down_proj"]})
+    save_file(ck, str(tmp_path / "model.safetensors"))
+    (tmp_path / "quantize_config.json").write_text(json.dumps({"bits": 8, "group_size": -1, "sym": True}))
+    moe = HybridMoE(E, k, H, I, nn.ModuleDict(), torch.zeros(E, dtype=torch.bool), 0, str(tmp_path),
+                    router_use_softmax=True, normalize_topk_prob=True,
+                    expert_key_template=QWEN3_MOE_UNPACKED_SPEC.expert_key_template,
+                    expert_proj_names=QWEN3_MOE_UNPACKED_SPEC.expert_proj_names)
+    x, logits = _inputs(T, H, E, seed=26)
+    out = moe(x.to(gpu_device), logits.to(gpu_device))
+    assert moe._native.weight_format == "int8_per_channel"
+    layer = Layer(MoEConfig("i8", H, E, k, I, 0, True, True, "bf16", "int8_per_channel"), torch.zeros(E, H),
+                  qlayers)
+    _check(out, oracle_forward(layer, x, logits))

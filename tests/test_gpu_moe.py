@@ -314,3 +314,92 @@ def test_forward_hidden_fused_router(gpu_device, name, E, T):
     again = native.forward(x, g_logits)
     torch.cuda.synchronize()
     assert torch.equal(out, again)
+
+
+def _spread_rows(T, ids, n_edge=32, n_hot=16):
+    """Rows to check against the oracle in a large batch: the first, middle and
+    last n_edge (+1) rows -- they hold the first, middle and last positions of
+    every expert, so the first, middle and last 64-position tiles -- plus up to
+    n_hot rows routed to the most-used expert, spread over its segment."""
+    mid = T // 2 - n_edge // 2
+    rows = set(range(n_edge)) | set(range(mid, mid + n_edge)) | set(range(T - n_edge - 1, T))
+    hot = np.bincount(ids.ravel()).argmax()
+    hot_rows = np.nonzero((ids == hot).any(axis=1))[0]
+    rows |= set(hot_rows[np.linspace(0, len(hot_rows) - 1, n_hot).astype(int)].tolist())
+    return sorted(rows)
+
+
+def _check_rows_and_prefix(layer, native, T, prefix, seed):
+    """The full batch's routing and permutation bit-exact; >= 97 spread rows
+    against the oracle; rows [0, prefix) bit-identical to a batch of prefix
+    tokens (the same prefill regime: every output element sums over K in the
+    same order whatever the tile)."""
+    cfg = layer.cfg
+    x, logits = build_inputs(layer, T, seed=seed, device="cuda")
+    out = native.forward(x, logits).clone()
+    torch.cuda.synchronize()
+    ids = native.region(T, 0, torch.int32, (T, cfg.k)).cpu().numpy()
+    perm = native.region(T, 4, torch.int32, (T * cfg.k,)).cpu().numpy()
+    o_ids, _ = O.route(logits.float().cpu().numpy(), cfg.k, cfg.softmax, cfg.renorm, cfg.act == "bf16")
+    assert np.array_equal(ids, o_ids)
+    assert np.array_equal(perm, O.group(o_ids, cfg.E)[2])
+    rows = _spread_rows(T, ids)
+    assert len(rows) >= 97
+    idx = torch.tensor(rows, device="cuda")
+    ref = oracle_forward(layer, x[idx], logits[idx])
+    err_abs, err_rel = compare(out[idx].float().cpu().numpy(), ref, cfg)
+    announce(f"  {cfg.name} T={T} ({len(rows)} rows): max_abs={err_abs:.3e} rel_l2={err_rel:.3e}")
+    part = native.forward(x[:prefix].contiguous(), logits[:prefix].contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(out[:prefix], part)
+
+
+def test_mixtral_int4_full_prefill(gpu_device):
+    """Mixtral-8x7B int4 at its full shape (I=14336) and T=2048: the int4
+    prefill pipeline with down over K=14336 (112 stages) and experts of
+    58.7 MB (gate_up) / 29.4 MB (down) that run in groups of 4 weight slabs."""
+    announce("forward mixtral_int4 full T=2048 (rows) and T=1024 (prefix)")
+    layer, native = _layer("mixtral_int4")
+    _check_rows_and_prefix(layer, native, 2048, 1024, seed=31)
+
+
+def test_qwen15_shared_full_prefill(gpu_device):
+    """Qwen1.5-MoE at T=1024: the routed experts and the 23 MB shared
+    gate_up (11264 x 2048 int8) in the prefill form, the shared expert's
+    weight slabs in groups of 4."""
+    announce("forward qwen15_int8_shared full T=1024 (rows) and T=512 (prefix)")
+    layer, native = _layer("qwen15_int8_shared")
+    _check_rows_and_prefix(layer, native, 1024, 512, seed=33)
+
+
+@pytest.mark.parametrize("T", [1, 16])
+@pytest.mark.parametrize("name,E", [("qwen3_int4", None), ("qwen15_int8_shared", None)])
+def test_decode_outlier_channels(gpu_device, name, E, T):
+    """The decode form feeds codes to the matrix cores as offset integers and
+    removes offset x (group sum of x) afterwards; four activation channels
+    scaled by 256 (the outlier channels of real activations) make those group
+    sums large.  Routing from the unscaled rows."""
+    announce(f"forward {name} T={T} outlier channels")
+    layer, native = _layer(name, E=E)
+    x, logits = build_inputs(layer, T, seed=41, device="cuda")
+    xf = x.float()
+    xf[:, [5, 700, 1500, 2047]] *= 256.0
+    xs = xf.to(torch.bfloat16)
+    out = native.forward(xs, logits)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    # (1) the fp32 oracle, at the bf16 tolerance scaled to each row's size: the
+    # outputs grow with the inputs, and h is stored in bf16 on both the GPU and
+    # the reference's bf16 path (an error of 2^-9 |h| per element that an
+    # absolute bound does not scale with)
+    ref = oracle_forward(layer, xs, logits)
+    for t in range(T):
+        r = ref[t].astype(np.float64)
+        assert np.linalg.norm(got[t] - r) <= 1e-2 * np.linalg.norm(r), f"row {t}: rel-L2"
+        assert np.max(np.abs(got[t] - r)) <= 2e-2 * np.max(np.abs(r)), f"row {t}: max-abs"
+    # (2) the oracle with h rounded to bf16 like the GPU, at the absolute bf16
+    # tolerance: what is left is the accumulation of the offset codes
+    ref_h = oracle_forward(layer, xs, logits, h_bf16=True)
+    err_abs, err_rel = compare(got, ref_h, layer.cfg)
+    announce(f"  {name} T={T} outliers: max_abs={err_abs:.3e} rel_l2={err_rel:.3e} "
+             f"max|ref|={np.abs(ref).max():.2f}")

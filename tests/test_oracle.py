@@ -371,6 +371,26 @@ def test_expert_forward_is_dense_swiglu():
     assert O.rel_l2(out, _torch_swiglu64(x, g, u, d)) < 1e-6
 
 
+def test_expert_forward_bf16_h():
+    """h_bf16 rounds the SwiGLU output to bf16 before the down projection:
+    against torch's float64 SwiGLU with a torch bf16 cast of h, and the change
+    from the fp32 result stays within the rounding bound 2^-9 |h| per element."""
+    rng = np.random.default_rng(13)
+    H, I = 64, 96
+    g, u, d = (rng.standard_normal(s).astype(np.float32) * 0.3 for s in ((I, H), (I, H), (H, I)))
+    x = rng.standard_normal((5, H)).astype(np.float32)
+    ex = O.Expert(g, u, d)
+    got = O.expert_forward(x, ex, h_bf16=True)
+    x64, g64, u64, d64 = (torch.from_numpy(np.asarray(a, np.float64)) for a in (x, g, u, d))
+    h64 = torch.nn.functional.silu(x64 @ g64.T) * (x64 @ u64.T)
+    ref = (h64.to(torch.bfloat16).to(torch.float64) @ d64.T).numpy()
+    assert O.rel_l2(got, ref) < 1e-5
+    plain = O.expert_forward(x, ex)
+    bound = (np.abs(h64.numpy()) * 2.0 ** -9) @ np.abs(d.astype(np.float64)).T
+    assert np.all(np.abs(got.astype(np.float64) - plain) <= bound * 1.01 + 1e-5)
+    assert O.rel_l2(got, plain) > 1e-4  # the rounding is really applied
+
+
 def test_moe_forward_matches_independent_torch_loop():
     """C0 shape, fp32: the reference loop (softmax -> top-2 -> renorm, experts in ascending
     id, index_add_) written with torch float64 ops."""
