@@ -209,6 +209,27 @@ int nkt_moe_forward_block(void* handle, const void* hidden_states, const void* n
                           int num_tokens, void* out, void* workspace, size_t workspace_bytes, void* stream,
                           char* err, size_t err_len);
 
+/* Largest workspace (bytes, per GPU) that nkt_moe_forward_noalloc serves
+ * from the library's static scratch: compare nkt_moe_workspace_bytes. */
+#define NKT_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* nkt_moe_forward without a workspace argument and without any allocation:
+ * the workspace is a static device array of NKT_NOALLOC_SCRATCH_BYTES
+ * inside the library (one per GPU, held until the process ends), so the call
+ * makes no hipMalloc / hipFree and creates no stream (the shared expert runs
+ * on `stream`, after the routed experts).  No counterpart in the reference:
+ * it is for callers that cannot allocate -- code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc.  Fails (NKT_ERR,
+ * message in err) when nkt_moe_workspace_bytes(num_tokens) exceeds
+ * NKT_NOALLOC_SCRATCH_BYTES (decode batches of every supported shape fit;
+ * large prefill batches do not).  Every call on one GPU shares that GPU's
+ * scratch: calls that overlap on one GPU (two streams, two handles, two
+ * threads) race and must be serialised by the caller.  Nothing in the
+ * scratch has to start at zero: each call writes every region before it
+ * reads it. */
+int nkt_moe_forward_noalloc(void* handle, const void* hidden_states, const void* router_logits,
+                            int num_tokens, void* out, void* stream, char* err, size_t err_len);
+
 /* Library version string (static storage). */
 const char* nkt_moe_version(void);
 

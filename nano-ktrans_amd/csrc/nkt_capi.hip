@@ -495,16 +495,17 @@ bool shared_side_ready(Handle* h, int T, const WsLayout& L, hipStream_t st) {
 // recorded and waited for on every path, errors included: the caller's
 // stream never runs ahead of the side stream's reads of x and the workspace,
 // and a graph being captured on st stays joined.
+// allow_side false: the shared expert stays on st (no side stream is made).
 template <typename Route>
 int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayout& L, hipStream_t st, char* err,
-              size_t len, Route route, const void* residual = nullptr) {
+              size_t len, Route route, const void* residual = nullptr, bool allow_side = true) {
   if (!x || !out) {
     set_err(err, len, "null hidden_states or output");
     return NKT_ERR;
   }
   if (!check_weights(h, h->Is > 0, err, len)) return NKT_ERR;
   std::unique_lock<std::mutex> lk(h->side_mu, std::defer_lock);
-  const bool side = shared_side_ready(h, T, L, st);
+  const bool side = allow_side && shared_side_ready(h, T, L, st);
   if (side) {
     lk.lock();
     if (!check_hip(hipEventRecord(h->fork_ev, st), "fork event", err, len) ||
@@ -531,6 +532,48 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
   }
   if (rc != NKT_OK) return rc;
   return do_combine(h, T, out, ws, L, st, err, len, nullptr, residual);
+}
+
+// ---------------------------------------------------------------------------
+// Static scratch of nkt_moe_forward_noalloc: the workspace of one layer call
+// in a file-scope device array (each GPU that runs the library holds its own
+// copy until the process ends).  Host code never passes the array's name to a
+// kernel (on the host it is a stand-in symbol, not a device address): the
+// device address comes from hipGetSymbolAddress, once per device, with that
+// device current, and is kept per device.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = NKT_NOALLOC_SCRATCH_BYTES;
+constexpr int kMaxScratchDevices = 64;
+
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// The current device's scratch address, looked up on the first call there.
+void* device_scratch(char* err, size_t len) {
+  int dev = -1;
+  if (!check_hip(hipGetDevice(&dev), "hipGetDevice", err, len)) return nullptr;
+  if (dev < 0 || dev >= kMaxScratchDevices) {
+    set_err(err, len, "device %d outside the scratch table [0, %d)", dev, kMaxScratchDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (!check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)", err, len))
+      return nullptr;
+    if (!p) {
+      set_err(err, len, "hipGetSymbolAddress(scratch) returned a null address");
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
 }
 
 }  // namespace
@@ -815,6 +858,38 @@ int nkt_moe_forward(void* handle, const void* hidden_states, const void* router_
   hipStream_t st = (hipStream_t)stream;
   return run_layer(h, hidden_states, num_tokens, out, workspace, L, st, err, err_len,
                    [&] { return do_route(h, router_logits, num_tokens, workspace, L, st, err, err_len); });
+}
+
+int nkt_moe_forward_noalloc(void* handle, const void* hidden_states, const void* router_logits, int num_tokens,
+                            void* out, void* stream, char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!h) {
+    set_err(err, err_len, "null handle");
+    return NKT_ERR;
+  }
+  if (num_tokens < 0 || num_tokens > h->max_tokens) {
+    set_err(err, err_len, "num_tokens=%d outside [0, max_tokens=%d]", num_tokens, h->max_tokens);
+    return NKT_ERR;
+  }
+  if (num_tokens == 0) return NKT_OK;
+  if (!router_logits) {
+    set_err(err, err_len, "null router_logits");
+    return NKT_ERR;
+  }
+  const WsLayout L = ws_layout(h, num_tokens);
+  if (L.total > kScratchBytes) {
+    set_err(err, err_len,
+            "num_tokens=%d needs %zu bytes of workspace; the static scratch of nkt_moe_forward_noalloc holds %zu "
+            "(use nkt_moe_forward with a caller-owned workspace)",
+            num_tokens, L.total, kScratchBytes);
+    return NKT_ERR;
+  }
+  void* ws = device_scratch(err, err_len);
+  if (!ws) return NKT_ERR;
+  hipStream_t st = (hipStream_t)stream;
+  return run_layer(h, hidden_states, num_tokens, out, ws, L, st, err, err_len,
+                   [&] { return do_route(h, router_logits, num_tokens, ws, L, st, err, err_len); }, nullptr,
+                   /*allow_side=*/false);
 }
 
 int nkt_moe_route_hidden(void* handle, const void* hidden_states, int num_tokens, void* workspace,

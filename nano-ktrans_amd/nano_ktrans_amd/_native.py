@@ -74,8 +74,12 @@ EXPORTED_SYMBOLS = (
     "nkt_moe_route_hidden",
     "nkt_moe_forward_hidden",
     "nkt_moe_forward_block",
+    "nkt_moe_forward_noalloc",
     "nkt_moe_version",
 )
+
+# bytes of the static scratch behind nkt_moe_forward_noalloc (NKT_NOALLOC_SCRATCH_BYTES)
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 
 class NativeError(RuntimeError):
@@ -135,6 +139,8 @@ def lib() -> ctypes.CDLL:
     L.nkt_moe_forward_hidden.restype = i
     L.nkt_moe_forward_block.argtypes = [vp, vp, vp, ctypes.c_float, i, vp, vp, sz, vp, cp, sz]
     L.nkt_moe_forward_block.restype = i
+    L.nkt_moe_forward_noalloc.argtypes = [vp, vp, vp, i, vp, vp, cp, sz]
+    L.nkt_moe_forward_noalloc.restype = i
     L.nkt_moe_version.argtypes = []
     L.nkt_moe_version.restype = ctypes.c_char_p
     _lib = L

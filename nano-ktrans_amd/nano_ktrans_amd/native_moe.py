@@ -423,3 +423,21 @@ class NativeMoE:
                                                     ws.data_ptr(), ws.numel(), self._stream(),
                                                     self.err.buf, self.err.size), "nkt_moe_forward")
         return out
+
+    def forward_noalloc(self, hidden_states: torch.Tensor, router_logits: torch.Tensor,
+                        out: torch.Tensor) -> torch.Tensor:
+        """``forward`` through nkt_moe_forward_noalloc: the library's static
+        per-GPU scratch replaces the workspace, so the call allocates nothing
+        (``out`` is the caller's).  Calls that overlap on one GPU race."""
+        x = self._check_input(hidden_states, self.hidden_size, "hidden_states")
+        logits = self._check_input(router_logits, self.num_experts, "router_logits")
+        T = x.shape[0]
+        if logits.shape[0] != T:
+            raise ValueError(f"router_logits has {logits.shape[0]} rows, hidden_states {T}")
+        if out.dtype != self.act_dtype or tuple(out.shape) != (T, self.hidden_size) or not out.is_contiguous():
+            raise ValueError(f"out must be a contiguous [{T}, {self.hidden_size}] {self.act_dtype} tensor")
+        with torch.cuda.device(self.device):
+            self.err.check(self.lib.nkt_moe_forward_noalloc(self.handle, x.data_ptr(), logits.data_ptr(), T,
+                                                            out.data_ptr(), self._stream(), self.err.buf,
+                                                            self.err.size), "nkt_moe_forward_noalloc")
+        return out
