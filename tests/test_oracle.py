@@ -440,3 +440,27 @@ def test_moe_forward_shared_expert_closed_form():
     gate = 1.0 / (1.0 + np.exp(-(x.astype(np.float64) @ g)))
     expect = base + gate[:, None] * _torch_swiglu64(x, sh.gate, sh.up, sh.down)
     assert O.rel_l2(full, expect) < 1e-6
+
+
+def test_torch_cpu_loop_matches_oracle():
+    """oracle/cpu_loop.py (the torch restatement timed as the CPU baseline)
+    equals the numpy oracle's forward: int4 and int8 experts, and dense fp32."""
+    import cpu_loop as C
+
+    rng = np.random.default_rng(21)
+    T, H, E, k, I = 9, 256, 6, 2, 256
+    x = O.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    logits = O.bf16_round(rng.standard_normal((T, E)).astype(np.float32))
+    for kind in ("int4", "int8", "f32"):
+        def mk(n, kk):
+            w = rng.standard_normal((n, kk)).astype(np.float32) * 0.05
+            if kind == "int4":
+                return O.with_bf16_scales(O.quantize_int4(w))
+            if kind == "int8":
+                return O.with_bf16_scales(O.quantize_int8_pc(w))
+            return w
+        experts = [O.Expert(mk(I, H), mk(I, H), mk(H, I)) for _ in range(E)]
+        ref = O.moe_forward(x, logits, experts, k, True, True, True)
+        ids, w = O.route(logits, k, True, True, True)
+        got = C.moe_loop(x, ids, w, [C.to_torch_expert(e) for e in experts])
+        assert O.rel_l2(got, ref) < 1e-5, kind
