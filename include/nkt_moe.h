@@ -81,7 +81,9 @@ extern "C" {
 #define NKT_WS_SHARED_Y 10    /* fp32 [T, H]                                           */
 #define NKT_WS_ROUTER_LOGITS 11 /* bf16 [T, E] router logits of the *_hidden entry points */
 #define NKT_WS_NORMED 12        /* bf16 [T, H] RMSNorm output of nkt_moe_forward_block    */
-#define NKT_WS_NUM_REGIONS 13
+#define NKT_WS_SYNC 13          /* uint32 [32]: word 31 is the status of the last single-launch router
+                                   call, 0 unless a cross-workgroup wait gave up (a library fault) */
+#define NKT_WS_NUM_REGIONS 14
 
 /* Create a handle for one layer shape.
  * Replaces the construction of HybridMoE's expert state
@@ -113,7 +115,11 @@ int nkt_moe_pack_weight(void* handle, int slot, int expert, const void* src, con
  * NKT_NUM_SLOTS entries (NULL where a slot does not apply). */
 int nkt_moe_bind_weights(void* handle, const void* const* ptrs, char* err, size_t err_len);
 
-/* Workspace size for num_tokens tokens, and the byte offset of each region. */
+/* Workspace size for num_tokens tokens, and the byte offset of each region.
+ * The sync area -- every byte before the offset of NKT_WS_TOPK_IDS: the
+ * NKT_WS_SYNC words and the single-launch router's tagged logit words, placed
+ * first and sized independently of num_tokens -- must be zero before a
+ * workspace's first use; every call leaves it zero. */
 int nkt_moe_workspace_bytes(void* handle, int num_tokens, size_t* bytes, char* err, size_t err_len);
 int nkt_moe_workspace_region(void* handle, int num_tokens, int region, size_t* offset,
                              char* err, size_t err_len);
@@ -188,7 +194,9 @@ int nkt_moe_forward(void* handle, const void* hidden_states, const void* router_
  * accumulation, rounded to bf16 as nn.Linear(H, E, bias=False) does in bf16),
  * written to NKT_WS_ROUTER_LOGITS, then routed as by nkt_moe_route.  Fuses the
  * decoder layer's gate (nano_ktrans/models/mixtral.py:127, 212) into the
- * expert path; needs bf16 activations and a packed NKT_SLOT_ROUTER. */
+ * expert path; needs bf16 activations and a packed NKT_SLOT_ROUTER.  Up to
+ * 64 tokens (and top_k * tokens <= 1024, num_experts % 4 == 0) the GEMV,
+ * routing and grouping are one launch; larger batches take three. */
 int nkt_moe_route_hidden(void* handle, const void* hidden_states, int num_tokens, void* workspace,
                          size_t workspace_bytes, void* stream, char* err, size_t err_len);
 

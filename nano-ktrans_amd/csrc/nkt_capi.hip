@@ -3,6 +3,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <new>
 
@@ -42,7 +43,8 @@ constexpr int kWsHist = NKT_WS_NUM_REGIONS + 5;   // int32 [blocks, E] per-block
 constexpr int kWsTileSrc = NKT_WS_NUM_REGIONS + 6; // int32 [max_tiles, 16] decode tiles' input rows
 constexpr int kWsX16 = NKT_WS_NUM_REGIONS + 7;     // fp16 [T, H] scaled copy of x (int8 prefill gate_up)
 constexpr int kWsXInv = NKT_WS_NUM_REGIONS + 8;    // fp32 [T] 1 / scale of each row of that copy
-constexpr int kWsAll = NKT_WS_NUM_REGIONS + 9;
+constexpr int kWsTagged = NKT_WS_NUM_REGIONS + 9; // u64 [T, E / 2] tagged logit pairs (single-launch router)
+constexpr int kWsAll = NKT_WS_NUM_REGIONS + 10;
 
 void set_err(char* err, size_t len, const char* fmt, ...) {
   if (!err || len == 0) return;
@@ -171,8 +173,20 @@ WsLayout ws_layout(const Handle* h, int T) {
   const bool x16 = int8_f16_input(h);
   sz[kWsX16] = x16 ? (size_t)T * h->H * 2 : 0;
   sz[kWsXInv] = x16 ? (size_t)T * 4 : 0;
+  // the sync area first, at a size and place that do not depend on T: its
+  // words must be zero before a workspace's first use and every call leaves
+  // them zero, so no other region's old contents ever land there
+  sz[NKT_WS_SYNC] = 32 * 4;
+  sz[kWsTagged] = h->act_bf16 && h->E % 4 == 0
+                      ? (size_t)(h->max_tokens < kFusedRouteMaxTokens ? h->max_tokens : kFusedRouteMaxTokens) * h->E * 4
+                      : 0;
   size_t o = 0;
+  L.off[NKT_WS_SYNC] = o;
+  o += align_up(sz[NKT_WS_SYNC]);
+  L.off[kWsTagged] = o;
+  o += align_up(sz[kWsTagged]);
   for (int i = 0; i < kWsAll; ++i) {
+    if (i == NKT_WS_SYNC || i == kWsTagged) continue;
     L.off[i] = o;
     o += align_up(sz[i]);
   }
@@ -338,9 +352,35 @@ bool check_route_hidden(const Handle* h, const void* x, char* err, size_t len) {
   return true;
 }
 
+// Generation numbers of the single-launch kernels' flags: unique per call
+// across the process (never 0, the value a consumed flag is reset to).
+// The tag is a bijective hash of the counter (an odd multiplier mod 2^32), so
+// consecutive calls' tags share no low-value pattern with integer data.
+std::atomic<uint32_t> g_generation{0};
+uint32_t next_generation() {
+  uint32_t g = 0;
+  while (g == 0u) g = (++g_generation) * 0x9E3779B1u;
+  return g;
+}
+
 int do_route_hidden(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipStream_t st, char* err,
                     size_t len) {
   if (!check_route_hidden(h, x, err, len)) return NKT_ERR;
+  if (route_hidden_fused(T, h->k, h->E, h->H)) {
+    if (!check_hip(launch_route_hidden(x, h->w[NKT_SLOT_ROUTER], h->H, T, h->E, h->k, h->flags, L.bm, L.max_tiles,
+                                       ws_ptr<void>(ws, L, NKT_WS_ROUTER_LOGITS), ws_ptr<void>(ws, L, kWsTagged),
+                                       ws_ptr<uint32_t>(ws, L, NKT_WS_SYNC),
+                                       next_generation(), ws_ptr<int32_t>(ws, L, NKT_WS_TOPK_IDS),
+                                       ws_ptr<float>(ws, L, NKT_WS_TOPK_WEIGHTS), ws_ptr<int32_t>(ws, L, NKT_WS_COUNTS),
+                                       ws_ptr<int32_t>(ws, L, NKT_WS_OFFSETS), ws_ptr<int32_t>(ws, L, NKT_WS_PERM),
+                                       ws_ptr<int32_t>(ws, L, NKT_WS_INV), ws_ptr<int32_t>(ws, L, kWsTiles),
+                                       ws_ptr<int32_t>(ws, L, kWsNTiles),
+                                       L.bm == kTileSrcCols ? ws_ptr<int32_t>(ws, L, kWsTileSrc) : nullptr,
+                                       h->resident, st),
+                   "router + route + group kernel", err, len))
+      return NKT_ERR;
+    return NKT_OK;
+  }
   const int Ep = router_rows(h);
   GemmArgs r;
   memset(&r, 0, sizeof(r));

@@ -91,6 +91,21 @@ hipError_t launch_route_group(const void* logits, int act_bf16, int T, int E, in
                               int32_t* tiles, int32_t* n_tiles, int32_t* tile_src,
                               const uint8_t* resident, hipStream_t stream);
 
+// Router GEMV + K1 + K2 in one launch (bf16 activations) when
+// route_hidden_fused(T, k, E, H): gate_packed is the router weight in the
+// bf16 block layout (rows padded to 32); logits [T, E] bf16 are written as
+// well.  tagged: T E / 2 words of 8 bytes (the logit pairs with their
+// generation tags; every call leaves the tags 0); sync: 32 words of
+// workspace, word 31 the status (1 when a cross-workgroup wait gave up);
+// gen: this call's generation number (never 0).
+bool route_hidden_fused(int T, int k, int E, int H);
+hipError_t launch_route_hidden(const void* x, const void* gate_packed, int H, int T, int E, int k, unsigned flags,
+                               int bm, int max_tiles, void* logits, void* tagged, uint32_t* sync, uint32_t gen,
+                               int32_t* ids,
+                               float* w, int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
+                               int32_t* tiles, int32_t* n_tiles, int32_t* tile_src, const uint8_t* resident,
+                               hipStream_t stream);
+
 // K2 over many workgroups (large batches): hist holds group_hist_blocks(T*k) x E int32.
 int group_hist_blocks(int P);
 hipError_t launch_group_multi(const int32_t* ids, int T, int k, int E, int bm, int max_tiles, int32_t* hist,

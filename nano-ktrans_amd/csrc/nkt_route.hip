@@ -594,6 +594,144 @@ __global__ void __launch_bounds__(kGroupThreads) route_group_kernel(
   group_write(g, ids_s, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, tile_src);
 }
 
+// ---------------------------------------------------------------------------
+// Router GEMV + K1 + K2 in one launch (bf16, T <= 64): logits = x . gate^T
+// (nano_ktrans/models/mixtral.py:127, 212) computed by workgroups 1 .. NB, one
+// 16-expert row block each, then routed and grouped by workgroup 0.
+//
+// Workgroup b >= 1: its 16 waves split the K blocks of the packed gate
+// (bf16 blocks of 16 rows x 32 columns, lane l = row l % 16, columns
+// 8 (l / 16) ..), every wave multiplying its blocks by the token tiles of x on
+// the matrix cores (A = gate block, B = x columns, fp32 accumulation); the 16
+// partial tiles are added in wave order (fixed) and rounded once to bf16.
+// Each pair of logits goes out as one 64-bit device-coherent store of
+// (call generation << 32 | the two bf16 logits): the word carries its own
+// "written by this call" tag, so the reader needs no separate flag.
+//
+// Workgroup 0 is dispatched before the others (workgroups of a grid start in
+// order), so its wait cannot keep them from running.  Each of its threads
+// polls its words (device-coherent loads) until their tags hold this call's
+// generation -- a bounded wait: past kSyncSpinLimit polls it goes on anyway
+// and the status word (NKT_WS_SYNC word 31) says 1, otherwise 0 -- keeps the
+// logits, and clears the tags (a graph replay reuses the same generation;
+// nothing else writes tag 0).  Then it writes the bf16 logits region and
+// routes and groups exactly as route_group_kernel does, from LDS.
+// ---------------------------------------------------------------------------
+constexpr int kRouterRowsPerBlock = 16;
+constexpr uint32_t kSyncSpinLimit = 1u << 20;
+
+struct RouteHiddenLds {
+  int32_t ids_s[kFusedRouteMaxPairs];
+  uint32_t selmask[kFusedRouteMaxTokens][8];
+  GroupLds g;
+  float sv[kGroupWaves][kMaxTopK];
+  int si[kGroupWaves][kMaxTopK];
+  uint32_t logits[kFusedRouteMaxTokens * kMaxExperts / 2];  // bf16 pairs [T][E]
+};
+
+template <int VPL>
+__global__ void __launch_bounds__(kGroupThreads) route_hidden_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ gate, int H, int T, int E, int k, unsigned flags,
+    int bm, int max_tiles, uint16_t* __restrict__ logits, uint64_t* __restrict__ tagged, uint32_t* __restrict__ sync,
+    uint32_t gen, int32_t* __restrict__ ids_out, float* __restrict__ w_out, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ inv,
+    int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles, int32_t* __restrict__ tile_src,
+    const uint8_t* __restrict__ resident) {
+  constexpr int kRedBytes = kGroupWaves * 4 * 1024;  // partial tiles: [wave][column tile][64 lanes x 16 B]
+  constexpr int kLdsBytes = sizeof(RouteHiddenLds) > kRedBytes ? sizeof(RouteHiddenLds) : kRedBytes;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kLdsBytes];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+
+  if (blockIdx.x > 0) {
+    // ---- logits of experts 16 (b - 1) .. + 15 for every token ------------
+    const int rb = blockIdx.x - 1;
+    const int NKB = H / 32;
+    const int CT = (T + 15) / 16;
+    const int col = lane & 15;
+    const uint8_t* ablk = gate + (size_t)rb * NKB * 1024 + lane * 16;
+    const uint16_t* xcol[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const int t = ct * 16 + col;
+      xcol[ct] = x + (size_t)(t < T ? t : 0) * H + 8 * (lane >> 4);
+    }
+    f32x4 acc[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kb = wave; kb < NKB; kb += kGroupWaves) {
+      const u32x4 a = *(const u32x4*)(ablk + (size_t)kb * 1024);
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+        if (ct < CT) acc[ct] = mfma_bf16(a, *(const u32x4*)(xcol[ct] + kb * 32), acc[ct]);
+    }
+    f32x4* red = (f32x4*)smem;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+      if (ct < CT) red[(wave * 4 + ct) * 64 + lane] = acc[ct];
+    __syncthreads();
+    if (wave < CT) {
+      const int ct = wave;
+      f32x4 s = red[ct * 64 + lane];
+      for (int w = 1; w < kGroupWaves; ++w) s += red[(w * 4 + ct) * 64 + lane];
+      const int t = ct * 16 + col;
+      const int e0 = rb * kRouterRowsPerBlock + 4 * (lane >> 4);
+      if (t < T && e0 < E) {  // E % 4 == 0: the four experts are all real
+        uint64_t* dst = tagged + ((size_t)t * E + e0) / 2;
+        const uint64_t tag = (uint64_t)gen << 32;
+        __hip_atomic_store(dst, tag | pack_bf16x2(s[0], s[1]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(dst + 1, tag | pack_bf16x2(s[2], s[3]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    return;
+  }
+
+  // ---- workgroup 0: collect the logits, then route and group -------------
+  RouteHiddenLds& L = *(RouteHiddenLds*)smem;
+  unsigned res = 0;
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int e = VPL * lane + i;
+      res |= (unsigned)(!resident || (e < E && resident[e])) << i;
+    }
+  }
+  const int nwords = T * E / 2;
+  bool ok = true;
+  for (int i0 = 0; i0 < nwords; i0 += kGroupThreads) {
+    const int i = i0 + threadIdx.x;
+    if (i < nwords) {
+      uint64_t v = __hip_atomic_load(tagged + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      uint32_t spins = 0;
+      while ((uint32_t)(v >> 32) != gen && spins < kSyncSpinLimit) {
+        __builtin_amdgcn_s_sleep(2);
+        v = __hip_atomic_load(tagged + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ++spins;
+      }
+      ok = ok && (uint32_t)(v >> 32) == gen;
+      L.logits[i] = (uint32_t)v;
+      ((uint32_t*)logits)[i] = (uint32_t)v;
+      __hip_atomic_store(tagged + i, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  const bool all_ok = __syncthreads_and(ok);
+  if (threadIdx.x == 0) sync[31] = all_ok ? 0u : 1u;
+  for (int t = wave; t < T; t += kGroupWaves) {
+    int id;
+    float w;
+    route_token<VPL, true>(L.logits, t, E, k, flags, L.sv[wave], L.si[wave], &id, &w, L.selmask[t]);
+    if (lane < k) {
+      L.ids_s[t * k + lane] = id;
+      ids_out[(int64_t)t * k + lane] = id;
+      w_out[(int64_t)t * k + lane] = w;
+    }
+  }
+  __syncthreads();
+  if (wave == 0) group_scan<VPL>(L.selmask, T, E, bm, res, L.g);
+  __syncthreads();
+  group_write(L.g, L.ids_s, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, tile_src);
+}
+
 #define NKT_VPL_SWITCH(E, CASE) \
   switch ((E + 63) / 64) {      \
     CASE(1)                     \
@@ -623,6 +761,34 @@ hipError_t launch_route(const void* logits, int act_bf16, int T, int E, int k, u
 }
 
 bool route_group_fused(int T, int k) { return T <= kFusedRouteMaxTokens && T * k <= kFusedRouteMaxPairs; }
+
+bool route_hidden_fused(int T, int k, int E, int H) {
+  return route_group_fused(T, k) && E % 4 == 0 && E <= kMaxExperts && H % 128 == 0;
+}
+
+hipError_t launch_route_hidden(const void* x, const void* gate_packed, int H, int T, int E, int k, unsigned flags,
+                               int bm, int max_tiles, void* logits, void* tagged, uint32_t* sync, uint32_t gen,
+                               int32_t* ids,
+                               float* w, int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
+                               int32_t* tiles, int32_t* n_tiles, int32_t* tile_src, const uint8_t* resident,
+                               hipStream_t stream) {
+  if (T <= 0) return hipSuccess;
+  if (!route_hidden_fused(T, k, E, H) || gen == 0u) return hipErrorInvalidValue;
+  if (bm <= 0 || (bm & (bm - 1)) != 0) return hipErrorInvalidValue;
+  if (tile_src && bm != kTileSrcCols) return hipErrorInvalidValue;
+  const int NB = (E + kRouterRowsPerBlock - 1) / kRouterRowsPerBlock;
+  dim3 grid(1 + NB), block(64 * kGroupWaves);
+#define NKT_RH_CASE(V)                                                                                   \
+  case V:                                                                                                \
+    hipLaunchKernelGGL((route_hidden_kernel<V>), grid, block, 0, stream, (const uint16_t*)x,              \
+                       (const uint8_t*)gate_packed, H, T, E, k, flags, bm, max_tiles, (uint16_t*)logits,  \
+                       (uint64_t*)tagged, sync, gen, ids, w, counts, offsets, perm, inv, tiles, n_tiles, tile_src, \
+                       resident);                                                                        \
+    break;
+  NKT_VPL_SWITCH(E, NKT_RH_CASE)
+#undef NKT_RH_CASE
+  return hipGetLastError();
+}
 
 hipError_t launch_route_group(const void* logits, int act_bf16, int T, int E, int k,
                               unsigned flags, int bm, int max_tiles, int32_t* ids, float* w,

@@ -53,6 +53,7 @@ WS_SHARED_H = 9
 WS_SHARED_Y = 10
 WS_ROUTER_LOGITS = 11
 WS_NORMED = 12
+WS_SYNC = 13
 
 EXPORTED_SYMBOLS = (
     "nkt_moe_create",

@@ -217,7 +217,8 @@ class NativeMoE:
             if self._ws is not None:
                 for s in self._ws_streams:
                     self._ws.record_stream(s)
-            self._ws = torch.empty(max(need, 256), dtype=torch.uint8, device=self.device)
+            # zeroed: the workspace's leading sync area must start at zero (every call leaves it so)
+            self._ws = torch.zeros(max(need, 256), dtype=torch.uint8, device=self.device)
             self._ws_streams = set()
         self._ws_streams.add(stream)
         return self._ws

@@ -76,6 +76,13 @@ def test_weight_and_workspace_sizes():
             assert lib.nkt_moe_workspace_region(h, T, r, ctypes.byref(o), eb, 256) == 0
             offs.append(o.value)
         assert offs == sorted(offs) and all(o % 256 == 0 for o in offs)
+        # the sync area (NKT_WS_SYNC, then the router's tagged words) leads the
+        # workspace at a place and size independent of the token count
+        o = ctypes.c_size_t()
+        assert lib.nkt_moe_workspace_region(h, T, N.WS_SYNC, ctypes.byref(o), eb, 256) == 0
+        assert o.value == 0
+        sync_end = offs[0]
+        assert sync_end == 256 + 64 * E * 4  # 32 status words (padded), then 64 tokens x E/2 tagged words
     assert lib.nkt_moe_workspace_bytes(h, 4097, ctypes.byref(sz), eb, 256) != 0
     lib.nkt_moe_destroy(h)
 
@@ -108,7 +115,7 @@ def test_calls_validate_before_touching_the_gpu():
     assert lib.nkt_moe_workspace_bytes(h, 65, ctypes.byref(nbytes), eb, 256) == -1
     assert b"max_tokens=64" in eb.value
     assert lib.nkt_moe_workspace_bytes(h, 64, ctypes.byref(nbytes), eb, 256) == 0 and nbytes.value > 0
-    assert lib.nkt_moe_workspace_region(h, 1, N.WS_NORMED + 1, ctypes.byref(off), eb, 256) == -1
+    assert lib.nkt_moe_workspace_region(h, 1, N.WS_SYNC + 1, ctypes.byref(off), eb, 256) == -1
     assert b"region" in eb.value
     assert lib.nkt_moe_pack_weight(h, 1, 0, None, None, None, None, None, eb, 256) == -1
     assert lib.nkt_moe_pack_weight(h, 0, 9, None, None, None, None, None, eb, 256) == -1

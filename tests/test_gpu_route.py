@@ -120,13 +120,15 @@ def test_route_repeatable(gpu_device):
 
 
 @pytest.mark.parametrize("name,T", [
-    ("qwen3_int4", 1), ("qwen3_int4", 16), ("qwen3_int4", 100), ("qwen3_int8", 1024),
-    ("mixtral_int4", 16), ("qwen15_int8_shared", 1), ("qwen15_int8_shared", 300),
+    ("qwen3_int4", 1), ("qwen3_int4", 16), ("qwen3_int4", 64), ("qwen3_int4", 100), ("qwen3_int8", 1024),
+    ("mixtral_int4", 16), ("qwen15_int8_shared", 1), ("qwen15_int8_shared", 64), ("qwen15_int8_shared", 300),
 ])
 def test_route_hidden_matches_oracle(gpu_device, name, T):
-    """Router GEMV fused with K1 + K2: bf16 logits against the oracle's single
-    rounding of the exact dot products (check_router_logits), and routing /
-    grouping of those logits bit-exact."""
+    """Router GEMV fused with K1 + K2 (one launch up to 64 tokens, three past
+    it): bf16 logits against the oracle's single rounding of the exact dot
+    products (check_router_logits), and routing / grouping of those logits
+    bit-exact; the single launch's flags are reset and its status word is 0."""
+    from nano_ktrans_amd import _native as N
     cfg = CONFIGS[name]
     announce(f"route_hidden {name} T={T}")
     g = torch.Generator().manual_seed(cfg.seed + 50)
@@ -146,6 +148,49 @@ def test_route_hidden_matches_oracle(gpu_device, name, T):
     assert np.array_equal(offsets.cpu().numpy(), ooffsets)
     assert np.array_equal(perm.cpu().numpy(), operm)
     assert np.array_equal(inv.cpu().numpy(), oinv)
+    if T <= 64:  # the single launch: flags of its ceil(E / 16) logit workgroups consumed
+        sync = native.region(T, N.WS_SYNC, torch.int32, (32,)).cpu().numpy()
+        assert sync[31] == 0 and not sync[:(cfg.E + 15) // 16].any()
+
+
+def test_route_hidden_single_launch_replays(gpu_device):
+    """The single-launch router + route + group captured in a HIP graph: every
+    replay (the same generation number each time) waits for its own logits --
+    eager calls with other inputs on the same workspace run between replays --
+    and equals the eager result bit for bit."""
+    from nano_ktrans_amd import _native as N
+    announce("route_hidden graph replays")
+    cfg = CONFIGS["qwen3_int4"]
+    T = 16
+    g = torch.Generator().manual_seed(77)
+    gate = (torch.randn(cfg.E, cfg.H, generator=g) * 0.02).to(torch.bfloat16)
+    xa = torch.randn(T, cfg.H, generator=g).to(torch.bfloat16).to(gpu_device)
+    xb = torch.randn(T, cfg.H, generator=g).to(torch.bfloat16).to(gpu_device)
+    native = _router_only(cfg.E, cfg.k, cfg.softmax, cfg.renorm, torch.bfloat16, gpu_device, hidden=cfg.H)
+    native.load_router(gate)
+    ref_a = [t.clone() for t in native.route_hidden(xa)]
+    ref_b = [t.clone() for t in native.route_hidden(xb)]
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        native.route_hidden(xa)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        views = native.route_hidden(xa)
+    for r in range(4):
+        got_b = [t.clone() for t in native.route_hidden(xb)]
+        torch.cuda.synchronize()
+        for a, b in zip(got_b, ref_b):
+            assert torch.equal(a, b)
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(views, ref_a):
+            assert torch.equal(a, b), f"replay {r}"
+    sync = native.region(T, N.WS_SYNC, torch.int32, (32,)).cpu().numpy()
+    assert sync[31] == 0 and not sync[:(cfg.E + 15) // 16].any()
 
 
 def test_route_hidden_rejects_missing_router_and_fp32(gpu_device):
