@@ -116,10 +116,12 @@ int nkt_moe_pack_weight(void* handle, int slot, int expert, const void* src, con
 int nkt_moe_bind_weights(void* handle, const void* const* ptrs, char* err, size_t err_len);
 
 /* Workspace size for num_tokens tokens, and the byte offset of each region.
- * The sync area -- every byte before the offset of NKT_WS_TOPK_IDS: the
- * NKT_WS_SYNC words and the single-launch router's tagged logit words, placed
- * first and sized independently of num_tokens -- must be zero before a
- * workspace's first use; every call leaves it zero. */
+ * The sync area -- the first NKT_SYNC_AREA_BYTES bytes of every workspace,
+ * the same for every handle and token count (the NKT_WS_SYNC words and the
+ * single-launch router's tagged logit words) -- must be zero before a
+ * workspace's first use; every call of every handle leaves it zero, so one
+ * workspace may serve several handles in turn. */
+#define NKT_SYNC_AREA_BYTES 65792
 int nkt_moe_workspace_bytes(void* handle, int num_tokens, size_t* bytes, char* err, size_t err_len);
 int nkt_moe_workspace_region(void* handle, int num_tokens, int region, size_t* offset,
                              char* err, size_t err_len);

@@ -131,6 +131,12 @@ bool prefill_form_ok(const Handle* h, bool shared) {
 
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// Sync area sizes: 32 status words (padded), then kFusedRouteMaxTokens x
+// kMaxExperts / 2 tagged logit words of 8 bytes.
+constexpr size_t kSyncStatusBytes = 256;
+constexpr size_t kSyncTaggedBytes = (size_t)kFusedRouteMaxTokens * kMaxExperts * 4;
+static_assert(kSyncStatusBytes + kSyncTaggedBytes == NKT_SYNC_AREA_BYTES, "the sync area's published size");
+
 // int8 weights with bf16 activations: the prefill gate_up runs on the fp16
 // matrix cores from a power-of-two-scaled fp16 copy of x (H <= 4096)
 bool int8_f16_input(const Handle* h) { return h->wf == WF_I8 && h->act_bf16 && h->H <= 4096; }
@@ -173,18 +179,18 @@ WsLayout ws_layout(const Handle* h, int T) {
   const bool x16 = int8_f16_input(h);
   sz[kWsX16] = x16 ? (size_t)T * h->H * 2 : 0;
   sz[kWsXInv] = x16 ? (size_t)T * 4 : 0;
-  // the sync area first, at a size and place that do not depend on T: its
-  // words must be zero before a workspace's first use and every call leaves
-  // them zero, so no other region's old contents ever land there
-  sz[NKT_WS_SYNC] = 32 * 4;
-  sz[kWsTagged] = h->act_bf16 && h->E % 4 == 0
-                      ? (size_t)(h->max_tokens < kFusedRouteMaxTokens ? h->max_tokens : kFusedRouteMaxTokens) * h->E * 4
-                      : 0;
+  // The sync area first, the same size and place for every handle and
+  // token count (status words, the router's tagged logit words): it must be
+  // zero before a workspace's first use, every call of every handle leaves
+  // it zero, and so no region's old contents -- of this handle or of another
+  // sharing the workspace -- ever land there.
+  sz[NKT_WS_SYNC] = kSyncStatusBytes;
+  sz[kWsTagged] = kSyncTaggedBytes;
   size_t o = 0;
-  L.off[NKT_WS_SYNC] = o;
-  o += align_up(sz[NKT_WS_SYNC]);
-  L.off[kWsTagged] = o;
-  o += align_up(sz[kWsTagged]);
+  for (int i : {(int)NKT_WS_SYNC, kWsTagged}) {
+    L.off[i] = o;
+    o += align_up(sz[i]);
+  }
   for (int i = 0; i < kWsAll; ++i) {
     if (i == NKT_WS_SYNC || i == kWsTagged) continue;
     L.off[i] = o;

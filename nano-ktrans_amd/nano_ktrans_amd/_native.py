@@ -55,6 +55,9 @@ WS_ROUTER_LOGITS = 11
 WS_NORMED = 12
 WS_SYNC = 13
 
+# leading bytes of every workspace that must start at zero (every call leaves them zero)
+SYNC_AREA_BYTES = 65792
+
 EXPORTED_SYMBOLS = (
     "nkt_moe_create",
     "nkt_moe_destroy",

@@ -403,3 +403,27 @@ def test_decode_outlier_channels(gpu_device, name, E, T):
     err_abs, err_rel = compare(got, ref_h, layer.cfg)
     announce(f"  {name} T={T} outliers: max_abs={err_abs:.3e} rel_l2={err_rel:.3e} "
              f"max|ref|={np.abs(ref).max():.2f}")
+
+
+@pytest.mark.parametrize("name,E,T", [("qwen3_int4", 32, 16), ("mixtral_int4", None, 1), ("qwen3_int4", 32, 64)])
+def test_forward_matches_stages_and_leaves_sync_area_zero(gpu_device, name, E, T):
+    """The layer equals route -> experts -> combine through the separate entry
+    points bit for bit, and leaves the workspace's sync area (the
+    NKT_SYNC_AREA_BYTES before NKT_WS_TOPK_IDS) all zero."""
+    import ctypes
+
+    from nano_ktrans_amd import _native as N
+    announce(f"forward vs stages {name} E={E} T={T}")
+    layer, native = _layer(name, E=E)
+    x, logits = build_inputs(layer, T, seed=61, device="cuda")
+    a = native.forward(x, logits).clone()
+    torch.cuda.synchronize()
+    off = ctypes.c_size_t(0)
+    native.err.check(native.lib.nkt_moe_workspace_region(native.handle, T, N.WS_TOPK_IDS, ctypes.byref(off),
+                                                         native.err.buf, native.err.size), "region")
+    assert off.value == N.SYNC_AREA_BYTES and not native.workspace(T)[: off.value].any()
+    native.route(logits)
+    native.experts(x)
+    b = native.combine(T)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
