@@ -542,9 +542,12 @@ bool shared_side_ready(Handle* h, int T, const WsLayout& L, hipStream_t st) {
 // stream never runs ahead of the side stream's reads of x and the workspace,
 // and a graph being captured on st stays joined.
 // allow_side false: the shared expert stays on st (no side stream is made).
+// logits (nullable): the router logits when the caller gave them; a single
+// token then is routed inside its gate_up launch instead of by route().
 template <typename Route>
 int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayout& L, hipStream_t st, char* err,
-              size_t len, Route route, const void* residual = nullptr, bool allow_side = true) {
+              size_t len, Route route, const void* residual = nullptr, bool allow_side = true,
+              const void* logits = nullptr) {
   if (!x || !out) {
     set_err(err, len, "null hidden_states or output");
     return NKT_ERR;
@@ -568,6 +571,53 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
       (void)hipStreamWaitEvent(st, h->join_ev, 0);
       return NKT_ERR;
     }
+  }
+  // one token (decode form, every expert HBM-resident): the down GEMV and
+  // the combine run as one launch after the shared expert
+  const bool single = T == 1 && L.bm == kTileSrcCols && !h->resident && h->act_bf16 &&
+                      down_combine_supported(h->wf, h->H, h->I, h->I, h->k);
+  if (single) {
+    int rc = NKT_OK;
+    // routing inside gate_up pays when its workgroups run in about one round
+    // (Qwen3: 384, Qwen1.5-MoE: 352); with more (Mixtral-8x7B: 1792) every
+    // round would wait for the routing again, and the routing launch is cheaper
+    constexpr int64_t kInlineRouteMaxWorkgroups = 1024;
+    if (logits && gemv_workgroups(h->wf, PHASE_GATE_UP, 2 * h->I, h->H, h->I, L.max_tiles) <= kInlineRouteMaxWorkgroups) {
+      // K1 + K2 inside the gate_up launch (every workgroup routes the token)
+      GemmArgs a = expert_args(h, PHASE_GATE_UP, false, x, ws, L, T);
+      a.route_logits = logits;
+      a.route_E = h->E;
+      a.route_flags = h->flags;
+      a.ro_max_tiles = L.max_tiles;
+      a.ro_ids = ws_ptr<int32_t>(ws, L, NKT_WS_TOPK_IDS);
+      a.ro_w = ws_ptr<float>(ws, L, NKT_WS_TOPK_WEIGHTS);
+      a.ro_counts = ws_ptr<int32_t>(ws, L, NKT_WS_COUNTS);
+      a.ro_offsets = ws_ptr<int32_t>(ws, L, NKT_WS_OFFSETS);
+      a.ro_perm = ws_ptr<int32_t>(ws, L, NKT_WS_PERM);
+      a.ro_inv = ws_ptr<int32_t>(ws, L, NKT_WS_INV);
+      a.ro_tiles = ws_ptr<int32_t>(ws, L, kWsTiles);
+      a.ro_n_tiles = ws_ptr<int32_t>(ws, L, kWsNTiles);
+      a.ro_tile_src = ws_ptr<int32_t>(ws, L, kWsTileSrc);
+      if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, L.bm, L.max_tiles, st), "routing gate_up gemm", err,
+                     len))
+        return NKT_ERR;
+    } else {
+      rc = route();
+      if (rc == NKT_OK) rc = do_expert_phase(h, PHASE_GATE_UP, x, T, ws, L, st, err, len);
+    }
+    if (rc == NKT_OK && h->Is > 0) rc = do_shared(h, x, T, ws, L, st, err, len);
+    if (rc != NKT_OK) return rc;
+    if (!out) {
+      set_err(err, len, "null output");
+      return NKT_ERR;
+    }
+    GemmArgs b = expert_args(h, PHASE_DOWN, false, ws_ptr<void>(ws, L, NKT_WS_H), ws, L, T);
+    const bool sh = h->Is > 0;
+    const CombineTail c{ws_ptr<float>(ws, L, NKT_WS_TOPK_WEIGHTS), ws_ptr<int32_t>(ws, L, NKT_WS_PERM),
+                        sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_Y) : nullptr,
+                        sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE) : nullptr, residual, out};
+    if (!check_hip(launch_down_combine(b, c, h->wf, h->k, st), "down + combine kernel", err, len)) return NKT_ERR;
+    return NKT_OK;
   }
   int rc = route();
   if (rc == NKT_OK) rc = do_experts(h, x, T, ws, L, st, err, len);
@@ -903,7 +953,8 @@ int nkt_moe_forward(void* handle, const void* hidden_states, const void* router_
   const WsLayout L = ws_layout(h, num_tokens);
   hipStream_t st = (hipStream_t)stream;
   return run_layer(h, hidden_states, num_tokens, out, workspace, L, st, err, err_len,
-                   [&] { return do_route(h, router_logits, num_tokens, workspace, L, st, err, err_len); });
+                   [&] { return do_route(h, router_logits, num_tokens, workspace, L, st, err, err_len); }, nullptr,
+                   true, router_logits);
 }
 
 int nkt_moe_forward_noalloc(void* handle, const void* hidden_states, const void* router_logits, int num_tokens,
@@ -935,7 +986,7 @@ int nkt_moe_forward_noalloc(void* handle, const void* hidden_states, const void*
   hipStream_t st = (hipStream_t)stream;
   return run_layer(h, hidden_states, num_tokens, out, ws, L, st, err, err_len,
                    [&] { return do_route(h, router_logits, num_tokens, ws, L, st, err, err_len); }, nullptr,
-                   /*allow_side=*/false);
+                   /*allow_side=*/false, router_logits);
 }
 
 int nkt_moe_route_hidden(void* handle, const void* hidden_states, int num_tokens, void* workspace,

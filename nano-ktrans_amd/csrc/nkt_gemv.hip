@@ -33,6 +33,7 @@
 // scale multiplies each group's fp32 partial (int4) or the row total (int8).
 #include "nkt_common.h"
 #include "nkt_internal.h"
+#include "nkt_route_token.h"
 
 namespace nkt {
 
@@ -270,78 +271,20 @@ __device__ __forceinline__ void gemv_epilogue(const GemmArgs& a, const f32x4 (&a
 
 }  // namespace
 
-// Waves per workgroup: S K-parts of P row sets.
-__host__ __device__ constexpr int gemv_rowsets_per_wg(int S) { return S == 1 ? 4 : S == 2 ? 2 : 1; }
-
-// Grid: x = blocks of P row sets, y = tile slots (a slot past the routed tile
-// count exits at once).  NG > 0: each wave issues the loads of all its (at
-// most NG) groups at once and then consumes them; NG == 0: each wave streams
-// its groups through the D-deep ring.
+// One (tile, row set, K part) of the decode form: this wave's fp32 partial
+// sums of the row set's NT 16-row output tiles for the tile's positions,
+// columns = positions (16 at most, rows of them real).  expert: the tile's
+// expert; src / srcq: the input row of the lane's column in the full / quad
+// form; region: this wave's LDS staging area (NG KiB + the int4 scales).
 template <int WF, int PHASE, int RT, int S, int NG, int D, bool FULL>
-__global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(GemmArgs a, int n_rowsets) {
-  constexpr int P = gemv_rowsets_per_wg(S);
+__device__ __forceinline__ void gemv_accumulate(const GemmArgs& a, int expert, int rows, int src, int srcq, int kpart,
+                                                int rowset, uint8_t* region, uint32_t lane,
+                                                f32x4 (&acc)[PHASE == PHASE_GATE_UP ? 2 * RT : RT]) {
   constexpr int NT = (PHASE == PHASE_GATE_UP) ? 2 * RT : RT;
-  // Per-wave LDS region: the direct-to-LDS staging of the quad-form
-  // activations (NG KiB) and the int4 scales (32 B per tile and group), then
-  // reused for the wave's K-part partial sums (NT KiB).
   constexpr int kStageX = NG * 1024;
-  constexpr int kStageS = (WF == WF_I4) ? NT * NG * 32 : 0;
-  constexpr int kRed = S > 1 ? NT * 1024 : 0;
-  constexpr int kRegion = (kStageX + kStageS > kRed ? kStageX + kStageS : kRed) > 16
-                              ? (kStageX + kStageS > kRed ? kStageX + kStageS : kRed)
-                              : 16;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[S * P][kRegion];
-  __shared__ uint32_t arrived[P];  // K parts of each row set that have stored their sums
-
-  const int tile = blockIdx.y;
-  const uint32_t lane = threadIdx.x & 63;
   const int col = lane & 15;
-  // the input row of the lane's column comes straight from the tile index, so
-  // this load is issued first and waiting for it never waits for weights
-  int src = 0, srcq = 0;
-  if (a.tile_src) {
-    src = a.tile_src[tile * kTileSrcCols + col];
-    srcq = a.tile_src[tile * kTileSrcCols + (col & 3)];
-  }
-
-  const int wave = threadIdx.x >> 6;
-  const int kpart = wave % S;
-  const int rs_raw = blockIdx.x * P + wave / S;
-  const bool rs_ok = rs_raw < n_rowsets;
-  const int rowset = rs_ok ? rs_raw : 0;
   const int G = a.K / 128;
   const int NKB = a.K / block_k(WF);
-
-  // routed tiles: K2 writes every record up to the grid's max_tiles, those
-  // past the last tile with no rows (no wait for the tile count)
-  int expert, row0, rows;
-  if (a.n_tiles) {
-    const int4 rec = *(const int4*)(a.tiles + 4 * tile);
-    expert = rec.x;
-    row0 = rec.y;
-    rows = rec.z;
-  } else {
-    expert = 0;
-    row0 = tile * 16;
-    rows = min(16, a.num_rows - row0);
-  }
-  if (rows <= 0) return;
-  // split-K reduction by the last of a row set's waves to arrive (the others
-  // end at once): measured faster for six or more K parts of the down
-  // projection and of int4 gate_up (Mixtral), slower for fewer parts and
-  // for int8 gate_up, which keep the workgroup barrier
-  constexpr bool kLastReduces = S >= 6 && (PHASE == PHASE_DOWN || WF == WF_I4);
-  if (kLastReduces) {
-    if (threadIdx.x < P) arrived[threadIdx.x] = 0u;
-    __syncthreads();
-  }
-  // down: the output row of this lane's position, loaded before the K loop
-  int yrow = row0 + (lane & 15);
-  if (PHASE == PHASE_DOWN && a.out_rows && (int)(lane & 15) < rows) yrow = a.out_rows[yrow];
-  if (!a.tile_src) {  // rows read in place
-    src = row0 + (col < rows ? col : 0);
-    srcq = row0 + ((col & 3) < rows ? (col & 3) : 0);
-  }
   const uint8_t* xbase = (const uint8_t*)a.in + 16 * (lane >> 4);
 
   const uint8_t* wexp = a.w + (int64_t)expert * a.w_expert_bytes;
@@ -364,12 +307,10 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
   const int g_base = FULL ? kpart : kpart < G ? kpart : 0;
   constexpr bool IS_INT = WF == WF_I4 || WF == WF_I8;
 
-  f32x4 acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (NG > 0) {
-    uint8_t* region = lds[__builtin_amdgcn_readfirstlane(wave)];
     // weights first (registers), then the scales (LDS): the activation
     // addresses may still wait for src
     WSlot<WF, NT> sl[NG > 0 ? NG : 1];
@@ -481,6 +422,143 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
     }
   }
 
+}
+
+// Waves per workgroup: S K-parts of P row sets.
+__host__ __device__ constexpr int gemv_rowsets_per_wg(int S) { return S == 1 ? 4 : S == 2 ? 2 : 1; }
+
+// Grid: x = blocks of P row sets, y = tile slots (a slot past the routed tile
+// count exits at once).  NG > 0: each wave issues the loads of all its (at
+// most NG) groups at once and then consumes them; NG == 0: each wave streams
+// its groups through the D-deep ring.
+// ROUTE (gate_up, one token): the tile record comes from routing the
+// token inside the workgroup (GemmArgs::route_logits) instead of K2's list.
+template <int WF, int PHASE, int RT, int S, int NG, int D, bool FULL, bool ROUTE = false>
+__global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(GemmArgs a, int n_rowsets) {
+  constexpr int P = gemv_rowsets_per_wg(S);
+  constexpr int NT = (PHASE == PHASE_GATE_UP) ? 2 * RT : RT;
+  // Per-wave LDS region: the direct-to-LDS staging of the quad-form
+  // activations (NG KiB) and the int4 scales (32 B per tile and group), then
+  // reused for the wave's K-part partial sums (NT KiB).
+  constexpr int kStageX = NG * 1024;
+  constexpr int kStageS = (WF == WF_I4) ? NT * NG * 32 : 0;
+  constexpr int kRed = S > 1 ? NT * 1024 : 0;
+  constexpr int kRegion = (kStageX + kStageS > kRed ? kStageX + kStageS : kRed) > 16
+                              ? (kStageX + kStageS > kRed ? kStageX + kStageS : kRed)
+                              : 16;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[S * P][kRegion];
+  __shared__ uint32_t arrived[P];  // K parts of each row set that have stored their sums
+
+  const int tile = blockIdx.y;
+  const uint32_t lane = threadIdx.x & 63;
+  const int col = lane & 15;
+  // the input row of the lane's column comes straight from the tile index, so
+  // this load is issued first and waiting for it never waits for weights
+  int src = 0, srcq = 0;
+  if (!ROUTE && a.tile_src) {
+    src = a.tile_src[tile * kTileSrcCols + col];
+    srcq = a.tile_src[tile * kTileSrcCols + (col & 3)];
+  }
+
+  const int wave = threadIdx.x >> 6;
+  const int kpart = wave % S;
+  const int rs_raw = blockIdx.x * P + wave / S;
+  const bool rs_ok = rs_raw < n_rowsets;
+  const int rowset = rs_ok ? rs_raw : 0;
+
+  // routed tiles: K2 writes every record up to the grid's max_tiles, those
+  // past the last tile with no rows (no wait for the tile count)
+  int expert, row0, rows;
+  if (ROUTE) {
+    // K1 on the token's logits by wave 0 (the same code and bits as the
+    // routing kernels); tile = position = rank of the expert id among the k
+    __shared__ float rsv[kMaxTopK];
+    __shared__ int rsi[kMaxTopK];
+    __shared__ int rids[kMaxTopK];
+    __shared__ int rpos[kMaxTopK];
+    __shared__ int r_expert;
+    const int k = a.topk;
+    const bool first = blockIdx.x == 0 && tile == 0;
+    if (wave == 0) {
+      int id;
+      float w;
+      route_token<4, true>(a.route_logits, 0, a.route_E, k, a.route_flags, rsv, rsi, &id, &w);
+      int pos = 0;
+      for (int i = 0; i < k; ++i) pos += (__builtin_amdgcn_readlane(id, i) < id) ? 1 : 0;
+      if ((int)lane < k) {
+        rids[lane] = id;
+        rpos[lane] = pos;
+        if (pos == tile) r_expert = id;
+        if (first) {
+          a.ro_ids[lane] = id;
+          a.ro_w[lane] = w;
+          a.ro_perm[pos] = lane;
+          a.ro_inv[lane] = pos;
+        }
+      }
+    }
+    __syncthreads();
+    if (first) {
+      // K2 for one token: expert e holds position (#ids below e) if picked
+      const int nth = S * P * 64;
+      for (int e = threadIdx.x; e < a.route_E; e += nth) {
+        int c = 0, o = 0;
+        for (int i = 0; i < k; ++i) {
+          c += rids[i] == e ? 1 : 0;
+          o += rids[i] < e ? 1 : 0;
+        }
+        a.ro_counts[e] = c;
+        a.ro_offsets[e] = o;
+      }
+      if (threadIdx.x == 0) {
+        a.ro_offsets[a.route_E] = k;
+        a.ro_n_tiles[0] = k;
+      }
+      for (int ti = threadIdx.x; ti < a.ro_max_tiles; ti += nth) {
+        int e = 0;
+        for (int i = 0; i < k; ++i) e = rpos[i] == ti ? rids[i] : e;
+        *(int4*)(a.ro_tiles + 4 * ti) = ti < k ? int4{e, ti, 1, 0} : int4{0, 0, 0, 0};
+      }
+      for (int i = threadIdx.x; i < a.ro_max_tiles * kTileSrcCols; i += nth) a.ro_tile_src[i] = 0;
+    }
+    expert = r_expert;
+    row0 = tile;
+    rows = tile < k ? 1 : 0;
+    src = 0;
+    srcq = 0;
+  } else if (a.n_tiles) {
+    const int4 rec = *(const int4*)(a.tiles + 4 * tile);
+    expert = rec.x;
+    row0 = rec.y;
+    rows = rec.z;
+  } else {
+    expert = 0;
+    row0 = tile * 16;
+    rows = min(16, a.num_rows - row0);
+  }
+  if (rows <= 0) return;
+  // split-K reduction by the last of a row set's waves to arrive (the others
+  // end at once): measured faster for six or more K parts of the down
+  // projection and of int4 gate_up (Mixtral), slower for fewer parts and
+  // for int8 gate_up, which keep the workgroup barrier
+  constexpr bool kLastReduces = S >= 6 && (PHASE == PHASE_DOWN || WF == WF_I4);
+  if (kLastReduces) {
+    if (threadIdx.x < P) arrived[threadIdx.x] = 0u;
+    __syncthreads();
+  }
+  // down: the output row of this lane's position, loaded before the K loop
+  int yrow = row0 + (lane & 15);
+  if (PHASE == PHASE_DOWN && a.out_rows && (int)(lane & 15) < rows) yrow = a.out_rows[yrow];
+  if (!ROUTE && !a.tile_src) {  // rows read in place
+    src = row0 + (col < rows ? col : 0);
+    srcq = row0 + ((col & 3) < rows ? (col & 3) : 0);
+  }
+  const uint16_t* sexp = a.scales + (int64_t)expert * a.s_expert_elems;
+  const int orow0 = rowset * RT * 16;  // first output row of the row set
+  f32x4 acc[NT];
+  gemv_accumulate<WF, PHASE, RT, S, NG, D, FULL>(a, expert, rows, src, srcq, kpart, rowset,
+                                                 lds[__builtin_amdgcn_readfirstlane(wave)], lane, acc);
+
   if (S > 1 && !kLastReduces) {
     // each wave's partial sums go to its own region (its staged data is
     // consumed), the K part 0 wave adds the S parts in order
@@ -523,6 +601,62 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
 }
 
 // ---------------------------------------------------------------------------
+// Down projection + combine for one token (T = 1).  Every routed expert has
+// one position (tile p = position p = the p-th of the token's experts in
+// ascending id, its h row p), so the k expert rows of an output row set can
+// be added inside one workgroup: its waves take the (position, K part) pairs,
+// each through gemv_accumulate exactly as the down GEMV does for that tile,
+// and leave the column-0 partial sums in LDS; then y_p = the K parts added in
+// order (x the int8 row scale) and out = sum over p in order of w(p) y_p,
+// + gate x shared expert row, + residual, one rounding -- the arithmetic of
+// the down GEMV followed by combine_kernel, so the same bits, with no y
+// round trip through HBM and no combine launch.
+// ---------------------------------------------------------------------------
+constexpr int kDcWaves = 16;
+constexpr int kDcMaxItems = 64;  // positions x K parts
+
+template <int WF, int S, int NG, int D, bool FULL>
+__global__ void __launch_bounds__(64 * kDcWaves) gemv_down_combine_kernel(GemmArgs a, CombineTail c, int n_pos) {
+  constexpr int RT = 1;
+  constexpr int NT = RT;
+  constexpr int kStageX = NG * 1024;
+  constexpr int kStageS = (WF == WF_I4) ? NT * NG * 32 : 0;
+  constexpr int kRegion = kStageX + kStageS > 16 ? kStageX + kStageS : 16;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kDcWaves][kRegion];
+  __shared__ f32x4 part[kDcMaxItems][4];  // [position x S + K part][lane / 16]: rows 4 (l / 16) .. + 3, column 0
+  const uint32_t lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rowset = blockIdx.x;
+  const int n_items = n_pos * S;
+  for (int q = wave; q < n_items; q += kDcWaves) {
+    const int p = q / S, kpart = q % S;
+    const int expert = a.tiles[4 * p];
+    f32x4 acc[NT];
+    gemv_accumulate<WF, PHASE_DOWN, RT, S, NG, D, FULL>(a, expert, 1, p, p, kpart, rowset, lds[wave], lane, acc);
+    if ((lane & 15) == 0) part[q][lane >> 4] = acc[0];
+  }
+  __syncthreads();
+  if (threadIdx.x >= 16) return;
+  // thread r: output row orow0 + r (tile row r = 4 (r / 4) + r % 4 of lane group r / 4)
+  const int r = threadIdx.x;
+  const int orow = rowset * 16 + r;
+  float acc = 0.f;
+  for (int p = 0; p < n_pos; ++p) {
+    float y = part[p * S][r >> 2][r & 3];
+    for (int kp = 1; kp < S; ++kp) y += part[p * S + kp][r >> 2][r & 3];
+    if (WF == WF_I8) {
+      const int expert = a.tiles[4 * p];
+      y *= bf16_bits_to_f32(a.scales[(int64_t)expert * a.s_expert_elems + orow]);
+    }
+    const float term = c.w[c.perm[p]] * y;
+    acc = p == 0 ? term : acc + term;
+  }
+  if (c.y_shared) acc += c.shared_gate[0] * c.y_shared[orow];
+  if (c.residual) acc += bf16_bits_to_f32(((const uint16_t*)c.residual)[orow]);
+  ((uint16_t*)c.out)[orow] = (uint16_t)f32_to_bf16_bits(acc);
+}
+
+// ---------------------------------------------------------------------------
 // launch
 // ---------------------------------------------------------------------------
 namespace {
@@ -533,7 +667,19 @@ hipError_t launch_gemv_s(const GemmArgs& a, int max_tiles, int n_rowsets, hipStr
   constexpr int P = gemv_rowsets_per_wg(S);
   constexpr int D = (WF == WF_BF16) ? 2 : 3;
   dim3 grid((n_rowsets + P - 1) / P, max_tiles);
-  if (NG > 0 && a.K / 128 == S * NG)
+  const bool full = NG > 0 && a.K / 128 == S * NG;
+  if constexpr (PHASE == PHASE_GATE_UP) {
+    if (a.route_logits) {
+      if (full)
+        launch_timed(gemv_kernel<WF, PHASE, RT, S, NG, D, true, true>, grid, dim3(S * P * 64), 0, stream, tm, a,
+                     n_rowsets);
+      else
+        launch_timed(gemv_kernel<WF, PHASE, RT, S, NG, D, false, true>, grid, dim3(S * P * 64), 0, stream, tm, a,
+                     n_rowsets);
+      return hipGetLastError();
+    }
+  }
+  if (full)
     launch_timed(gemv_kernel<WF, PHASE, RT, S, NG, D, true>, grid, dim3(S * P * 64), 0, stream, tm, a, n_rowsets);
   else
     launch_timed(gemv_kernel<WF, PHASE, RT, S, NG, D, false>, grid, dim3(S * P * 64), 0, stream, tm, a, n_rowsets);
@@ -592,6 +738,60 @@ hipError_t launch_gemv_rt(const GemmArgs& a, int max_tiles, hipStream_t stream, 
   }
 }
 
+template <int WF, int S, int NG>
+hipError_t launch_down_combine_s(const GemmArgs& a, const CombineTail& c, int n_pos, hipStream_t stream) {
+  constexpr int D = (WF == WF_BF16) ? 2 : 3;
+  dim3 grid(a.N / 16), block(64 * kDcWaves);
+  if (NG > 0 && a.K / 128 == S * NG)
+    hipLaunchKernelGGL((gemv_down_combine_kernel<WF, S, NG, D, true>), grid, block, 0, stream, a, c, n_pos);
+  else
+    hipLaunchKernelGGL((gemv_down_combine_kernel<WF, S, NG, D, false>), grid, block, 0, stream, a, c, n_pos);
+  return hipGetLastError();
+}
+
+template <int WF, int NG>
+hipError_t launch_down_combine_ng(const GemmArgs& a, const CombineTail& c, int n_pos, int S, hipStream_t stream) {
+  switch (S) {
+    case 1:
+      return launch_down_combine_s<WF, 1, NG>(a, c, n_pos, stream);
+    case 2:
+      return launch_down_combine_s<WF, 2, NG>(a, c, n_pos, stream);
+    case 3:
+      return launch_down_combine_s<WF, 3, NG>(a, c, n_pos, stream);
+    case 4:
+      return launch_down_combine_s<WF, 4, NG>(a, c, n_pos, stream);
+    case 5:
+    case 6:
+      return launch_down_combine_s<WF, 6, NG>(a, c, n_pos, stream);
+    default:
+      return launch_down_combine_s<WF, 8, NG>(a, c, n_pos, stream);
+  }
+}
+
+// the K split of the down GEMV (launch_gemv_rt), so the partial sums match it
+template <int WF>
+hipError_t launch_down_combine_wf(const GemmArgs& a, const CombineTail& c, int n_pos, hipStream_t stream) {
+  const int G = a.K / 128;
+  constexpr int target = gemv_target_groups(WF);
+  int S = (G + target - 1) / target;
+  if (S > 8) S = 8;
+  if (S == 5 || S == 7) ++S;
+  const int NG = (G + S - 1) / S;
+  if (n_pos * S > kDcMaxItems) return hipErrorInvalidValue;
+  switch (NG) {
+    case 1:
+      return launch_down_combine_ng<WF, 1>(a, c, n_pos, S, stream);
+    case 2:
+      return launch_down_combine_ng<WF, 2>(a, c, n_pos, S, stream);
+    case 3:
+      return launch_down_combine_ng<WF, 3>(a, c, n_pos, S, stream);
+    case 4:
+      return launch_down_combine_ng<WF, 4>(a, c, n_pos, S, stream);
+    default:
+      return launch_down_combine_s<WF, 8, 0>(a, c, n_pos, stream);
+  }
+}
+
 template <int WF>
 hipError_t launch_gemv_wf(const GemmArgs& a, int phase, int max_tiles, hipStream_t stream,
                           const KernelTimer* tm) {
@@ -611,6 +811,44 @@ bool gemv_supported(int wf, int phase, int N, int K, int I) {
   const int out_dim = phase == PHASE_GATE_UP ? I : N;
   const int rows_per_set = (phase == PHASE_GATE_UP ? kGemvRtGateUp : kGemvRtDown) * 16;
   return out_dim % rows_per_set == 0;
+}
+
+int64_t gemv_workgroups(int wf, int phase, int N, int K, int I, int max_tiles) {
+  const int RT = phase == PHASE_GATE_UP ? kGemvRtGateUp : kGemvRtDown;
+  const int out_dim = phase == PHASE_GATE_UP ? I : N;
+  const int G = K / 128;
+  const int target = gemv_target_groups(wf);
+  int S = (G + target - 1) / target;
+  if (S > 8) S = 8;
+  if (S == 5 || S == 7) ++S;
+  const int P = gemv_rowsets_per_wg(S);
+  const int n_rowsets = out_dim / (RT * 16);
+  return (int64_t)((n_rowsets + P - 1) / P) * max_tiles;
+}
+
+bool down_combine_supported(int wf, int N, int K, int I, int n_pos) {
+  if (!gemv_supported(wf, PHASE_DOWN, N, K, I) || N % 16 != 0 || n_pos < 1) return false;
+  const int G = K / 128;
+  const int target = gemv_target_groups(wf);
+  int S = (G + target - 1) / target;
+  if (S > 8) S = 8;
+  if (S == 5 || S == 7) ++S;
+  return n_pos * S <= kDcMaxItems;
+}
+
+hipError_t launch_down_combine(const GemmArgs& a, const CombineTail& c, int wf, int n_pos, hipStream_t stream) {
+  if (!a.tiles || !c.perm || !c.w || !c.out) return hipErrorInvalidValue;
+  if (!down_combine_supported(wf, a.N, a.K, a.I, n_pos)) return hipErrorInvalidValue;
+  switch (wf) {
+    case WF_BF16:
+      return launch_down_combine_wf<WF_BF16>(a, c, n_pos, stream);
+    case WF_I8:
+      return launch_down_combine_wf<WF_I8>(a, c, n_pos, stream);
+    case WF_I4:
+      return launch_down_combine_wf<WF_I4>(a, c, n_pos, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream,

@@ -54,6 +54,24 @@ struct GemmArgs {
   // down of the routed experts: output row of each position (its pair
   // t k + slot), so y comes out in pair order; nullptr: the position
   const int32_t* out_rows;
+  // single-token decode gate_up that routes its token itself
+  // (route_logits != nullptr, [1, route_E] bf16): every workgroup runs K1
+  // on the one row of logits, workgroup (0, 0) also writes K1's and K2's
+  // outputs into the ro_* regions (ids, weights, counts, offsets, perm, inv,
+  // ro_max_tiles tile records and their source rows, the tile count)
+  const void* route_logits;
+  int route_E;
+  unsigned route_flags;
+  int ro_max_tiles;
+  int32_t* ro_ids;
+  float* ro_w;
+  int32_t* ro_counts;
+  int32_t* ro_offsets;
+  int32_t* ro_perm;
+  int32_t* ro_inv;
+  int32_t* ro_tiles;
+  int32_t* ro_n_tiles;
+  int32_t* ro_tile_src;
 };
 
 enum GemmPhase : int { PHASE_GATE_UP = 0, PHASE_DOWN = 1 };
@@ -129,6 +147,28 @@ hipError_t launch_gemm(const GemmArgs& a, int wf, int phase, int bm, int grid_ti
 bool gemv_supported(int wf, int phase, int N, int K, int I);
 hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream,
                        const KernelTimer* tm = nullptr);
+
+// Workgroups of a decode-form launch (gemv_supported shapes; the down
+// launch at its two-tile row sets).
+int64_t gemv_workgroups(int wf, int phase, int N, int K, int I, int max_tiles);
+
+// The combine's inputs beyond y for the single-token down + combine kernel:
+// routing weights w [k] by pair, perm [k] position -> pair, the gated shared
+// expert (y_shared [H] fp32 and its gate [1], nullable), residual [H] (act
+// dtype, nullable), out [H] bf16.
+struct CombineTail {
+  const float* w;
+  const int32_t* perm;
+  const float* y_shared;
+  const float* shared_gate;
+  const void* residual;
+  void* out;
+};
+
+// Down GEMV + combine in one launch for one token (n_pos = its k expert
+// positions, tiles 0 .. n_pos - 1 from K2, h rows by position, bf16).
+bool down_combine_supported(int wf, int N, int K, int I, int n_pos);
+hipError_t launch_down_combine(const GemmArgs& a, const CombineTail& c, int wf, int n_pos, hipStream_t stream);
 
 // Prefill form of K3 (tiles of 64 positions, bf16 / int8 / int4 weights).
 bool gemm2_supported(int wf, int phase, int N, int K, int I);

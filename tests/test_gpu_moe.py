@@ -405,10 +405,12 @@ def test_decode_outlier_channels(gpu_device, name, E, T):
              f"max|ref|={np.abs(ref).max():.2f}")
 
 
-@pytest.mark.parametrize("name,E,T", [("qwen3_int4", 32, 16), ("mixtral_int4", None, 1), ("qwen3_int4", 32, 64)])
+@pytest.mark.parametrize("name,E,T", [("qwen3_int4", 32, 16), ("mixtral_int4", None, 1), ("qwen3_int4", 32, 64),
+                                      ("qwen3_int4", None, 1), ("qwen15_int8_shared", None, 1)])
 def test_forward_matches_stages_and_leaves_sync_area_zero(gpu_device, name, E, T):
-    """The layer equals route -> experts -> combine through the separate entry
-    points bit for bit, and leaves the workspace's sync area (the
+    """The layer equals route -> experts -> shared -> combine through the
+    separate entry points bit for bit (at T = 1 the layer runs the down GEMV
+    and the combine as one launch), and leaves the workspace's sync area (the
     NKT_SYNC_AREA_BYTES before NKT_WS_TOPK_IDS) all zero."""
     import ctypes
 
@@ -422,8 +424,17 @@ def test_forward_matches_stages_and_leaves_sync_area_zero(gpu_device, name, E, T
     native.err.check(native.lib.nkt_moe_workspace_region(native.handle, T, N.WS_TOPK_IDS, ctypes.byref(off),
                                                          native.err.buf, native.err.size), "region")
     assert off.value == N.SYNC_AREA_BYTES and not native.workspace(T)[: off.value].any()
-    native.route(logits)
+    k, E = layer.cfg.k, layer.cfg.E
+    regions = [(N.WS_TOPK_IDS, torch.int32, (T, k)), (N.WS_TOPK_WEIGHTS, torch.float32, (T, k)),
+               (N.WS_COUNTS, torch.int32, (E,)), (N.WS_OFFSETS, torch.int32, (E + 1,)),
+               (N.WS_PERM, torch.int32, (T * k,)), (N.WS_INV, torch.int32, (T * k,))]
+    # the routing outputs the layer left (at T = 1 written by its gate_up launch)
+    routed = [native.region(T, r, dt, shp).clone() for r, dt, shp in regions]
+    for got, want in zip(routed, native.route(logits)):
+        assert torch.equal(got, want)
     native.experts(x)
+    if layer.cfg.Is:
+        native.shared(x)
     b = native.combine(T)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
