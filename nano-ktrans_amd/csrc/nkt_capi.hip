@@ -44,7 +44,8 @@ constexpr int kWsTileSrc = NKT_WS_NUM_REGIONS + 6; // int32 [max_tiles, 16] deco
 constexpr int kWsX16 = NKT_WS_NUM_REGIONS + 7;     // fp16 [T, H] scaled copy of x (int8 prefill gate_up)
 constexpr int kWsXInv = NKT_WS_NUM_REGIONS + 8;    // fp32 [T] 1 / scale of each row of that copy
 constexpr int kWsTagged = NKT_WS_NUM_REGIONS + 9; // u64 [T, E / 2] tagged logit pairs (single-launch router)
-constexpr int kWsAll = NKT_WS_NUM_REGIONS + 10;
+constexpr int kWsWpos = NKT_WS_NUM_REGIONS + 10;  // fp32 [T k] routing weights by position (fused route + group)
+constexpr int kWsAll = NKT_WS_NUM_REGIONS + 11;
 
 void set_err(char* err, size_t len, const char* fmt, ...) {
   if (!err || len == 0) return;
@@ -179,6 +180,7 @@ WsLayout ws_layout(const Handle* h, int T) {
   const bool x16 = int8_f16_input(h);
   sz[kWsX16] = x16 ? (size_t)T * h->H * 2 : 0;
   sz[kWsXInv] = x16 ? (size_t)T * 4 : 0;
+  sz[kWsWpos] = P * 4;
   // The sync area first, the same size and place for every handle and
   // token count (status words, the router's tagged logit words): it must be
   // zero before a workspace's first use, every call of every handle leaves
@@ -321,7 +323,7 @@ int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, 
   if (route_group_fused(T, h->k)) {
     if (!check_hip(launch_route_group(logits, h->act_bf16, T, h->E, h->k, h->flags, L.bm, L.max_tiles,
                                       ids, wts, counts, offsets, perm, inv, tiles, n_tiles, tile_src,
-                                      h->resident, st),
+                                      h->resident, ws_ptr<float>(ws, L, kWsWpos), st),
                    "route+group kernel", err, len))
       return NKT_ERR;
     return NKT_OK;
@@ -382,7 +384,7 @@ int do_route_hidden(Handle* h, const void* x, int T, void* ws, const WsLayout& L
                                        ws_ptr<int32_t>(ws, L, NKT_WS_INV), ws_ptr<int32_t>(ws, L, kWsTiles),
                                        ws_ptr<int32_t>(ws, L, kWsNTiles),
                                        L.bm == kTileSrcCols ? ws_ptr<int32_t>(ws, L, kWsTileSrc) : nullptr,
-                                       h->resident, st),
+                                       h->resident, ws_ptr<float>(ws, L, kWsWpos), st),
                    "router + route + group kernel", err, len))
       return NKT_ERR;
     return NKT_OK;
@@ -582,7 +584,8 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
     // (Qwen3: 384, Qwen1.5-MoE: 352); with more (Mixtral-8x7B: 1792) every
     // round would wait for the routing again, and the routing launch is cheaper
     constexpr int64_t kInlineRouteMaxWorkgroups = 1024;
-    if (logits && gemv_workgroups(h->wf, PHASE_GATE_UP, 2 * h->I, h->H, h->I, L.max_tiles) <= kInlineRouteMaxWorkgroups) {
+    if (logits && h->E <= 128 &&
+        gemv_workgroups(h->wf, PHASE_GATE_UP, 2 * h->I, h->H, h->I, L.max_tiles) <= kInlineRouteMaxWorkgroups) {
       // K1 + K2 inside the gate_up launch (every workgroup routes the token)
       GemmArgs a = expert_args(h, PHASE_GATE_UP, false, x, ws, L, T);
       a.route_logits = logits;
@@ -598,6 +601,7 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
       a.ro_tiles = ws_ptr<int32_t>(ws, L, kWsTiles);
       a.ro_n_tiles = ws_ptr<int32_t>(ws, L, kWsNTiles);
       a.ro_tile_src = ws_ptr<int32_t>(ws, L, kWsTileSrc);
+      a.ro_wpos = ws_ptr<float>(ws, L, kWsWpos);
       if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, L.bm, L.max_tiles, st), "routing gate_up gemm", err,
                      len))
         return NKT_ERR;
@@ -613,8 +617,7 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
     }
     GemmArgs b = expert_args(h, PHASE_DOWN, false, ws_ptr<void>(ws, L, NKT_WS_H), ws, L, T);
     const bool sh = h->Is > 0;
-    const CombineTail c{ws_ptr<float>(ws, L, NKT_WS_TOPK_WEIGHTS), ws_ptr<int32_t>(ws, L, NKT_WS_PERM),
-                        sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_Y) : nullptr,
+    const CombineTail c{ws_ptr<float>(ws, L, kWsWpos), sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_Y) : nullptr,
                         sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE) : nullptr, residual, out};
     if (!check_hip(launch_down_combine(b, c, h->wf, h->k, st), "down + combine kernel", err, len)) return NKT_ERR;
     return NKT_OK;

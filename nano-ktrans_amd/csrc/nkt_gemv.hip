@@ -482,7 +482,7 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
     if (wave == 0) {
       int id;
       float w;
-      route_token<4, true>(a.route_logits, 0, a.route_E, k, a.route_flags, rsv, rsi, &id, &w);
+      route_token<2, true>(a.route_logits, 0, a.route_E, k, a.route_flags, rsv, rsi, &id, &w);
       int pos = 0;
       for (int i = 0; i < k; ++i) pos += (__builtin_amdgcn_readlane(id, i) < id) ? 1 : 0;
       if ((int)lane < k) {
@@ -494,6 +494,7 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
           a.ro_w[lane] = w;
           a.ro_perm[pos] = lane;
           a.ro_inv[lane] = pos;
+          a.ro_wpos[pos] = w;
         }
       }
     }
@@ -624,16 +625,30 @@ __global__ void __launch_bounds__(64 * kDcWaves) gemv_down_combine_kernel(GemmAr
   constexpr int kRegion = kStageX + kStageS > 16 ? kStageX + kStageS : 16;
   __shared__ __attribute__((aligned(16))) uint8_t lds[kDcWaves][kRegion];
   __shared__ f32x4 part[kDcMaxItems][4];  // [position x S + K part][lane / 16]: rows 4 (l / 16) .. + 3, column 0
+  __shared__ float wpos[kMaxTopK];              // routing weight of each position
+  __shared__ float spos[kMaxTopK][16];          // int8: row scales of each position's expert
   const uint32_t lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rowset = blockIdx.x;
   const int n_items = n_pos * S;
   for (int q = wave; q < n_items; q += kDcWaves) {
     const int p = q / S, kpart = q % S;
+    // the combine's operands of position p ride with its K part 0: its
+    // routing weight (in position order, independent of the tile record) and
+    // the int8 row scales of its expert (issued with the weights)
+    float wv = 0.f;
+    if (kpart == 0 && lane == 0) wv = c.wpos[p];
     const int expert = a.tiles[4 * p];
+    float sc = 0.f;
+    if (WF == WF_I8 && kpart == 0 && lane < 16u)
+      sc = bf16_bits_to_f32(a.scales[(int64_t)expert * a.s_expert_elems + rowset * 16 + lane]);
     f32x4 acc[NT];
     gemv_accumulate<WF, PHASE_DOWN, RT, S, NG, D, FULL>(a, expert, 1, p, p, kpart, rowset, lds[wave], lane, acc);
     if ((lane & 15) == 0) part[q][lane >> 4] = acc[0];
+    if (kpart == 0) {
+      if (lane == 0) wpos[p] = wv;
+      if (WF == WF_I8 && lane < 16u) spos[p][lane] = sc;
+    }
   }
   __syncthreads();
   if (threadIdx.x >= 16) return;
@@ -644,11 +659,8 @@ __global__ void __launch_bounds__(64 * kDcWaves) gemv_down_combine_kernel(GemmAr
   for (int p = 0; p < n_pos; ++p) {
     float y = part[p * S][r >> 2][r & 3];
     for (int kp = 1; kp < S; ++kp) y += part[p * S + kp][r >> 2][r & 3];
-    if (WF == WF_I8) {
-      const int expert = a.tiles[4 * p];
-      y *= bf16_bits_to_f32(a.scales[(int64_t)expert * a.s_expert_elems + orow]);
-    }
-    const float term = c.w[c.perm[p]] * y;
+    if (WF == WF_I8) y *= spos[p][r];
+    const float term = wpos[p] * y;
     acc = p == 0 ? term : acc + term;
   }
   if (c.y_shared) acc += c.shared_gate[0] * c.y_shared[orow];
@@ -837,7 +849,7 @@ bool down_combine_supported(int wf, int N, int K, int I, int n_pos) {
 }
 
 hipError_t launch_down_combine(const GemmArgs& a, const CombineTail& c, int wf, int n_pos, hipStream_t stream) {
-  if (!a.tiles || !c.perm || !c.w || !c.out) return hipErrorInvalidValue;
+  if (!a.tiles || !c.wpos || !c.out) return hipErrorInvalidValue;
   if (!down_combine_supported(wf, a.N, a.K, a.I, n_pos)) return hipErrorInvalidValue;
   switch (wf) {
     case WF_BF16:

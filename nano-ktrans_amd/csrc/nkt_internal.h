@@ -72,6 +72,7 @@ struct GemmArgs {
   int32_t* ro_tiles;
   int32_t* ro_n_tiles;
   int32_t* ro_tile_src;
+  float* ro_wpos;
 };
 
 enum GemmPhase : int { PHASE_GATE_UP = 0, PHASE_DOWN = 1 };
@@ -102,12 +103,13 @@ hipError_t launch_route(const void* logits, int act_bf16, int T, int E, int k, u
 
 // K1 + K2 in one workgroup when route_group_fused(T, k).  resident (nullable,
 // [E] device bytes): experts with 0 are grouped but get no GEMM tiles.
+// wpos (nullable, [T k]): the routing weight of each position (pair perm[pos]).
 bool route_group_fused(int T, int k);
 hipError_t launch_route_group(const void* logits, int act_bf16, int T, int E, int k,
                               unsigned flags, int bm, int max_tiles, int32_t* ids, float* w,
                               int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
                               int32_t* tiles, int32_t* n_tiles, int32_t* tile_src,
-                              const uint8_t* resident, hipStream_t stream);
+                              const uint8_t* resident, float* wpos, hipStream_t stream);
 
 // Router GEMV + K1 + K2 in one launch (bf16 activations) when
 // route_hidden_fused(T, k, E, H): gate_packed is the router weight in the
@@ -122,7 +124,7 @@ hipError_t launch_route_hidden(const void* x, const void* gate_packed, int H, in
                                int32_t* ids,
                                float* w, int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
                                int32_t* tiles, int32_t* n_tiles, int32_t* tile_src, const uint8_t* resident,
-                               hipStream_t stream);
+                               float* wpos, hipStream_t stream);
 
 // K2 over many workgroups (large batches): hist holds group_hist_blocks(T*k) x E int32.
 int group_hist_blocks(int P);
@@ -153,12 +155,11 @@ hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipS
 int64_t gemv_workgroups(int wf, int phase, int N, int K, int I, int max_tiles);
 
 // The combine's inputs beyond y for the single-token down + combine kernel:
-// routing weights w [k] by pair, perm [k] position -> pair, the gated shared
+// routing weights by position wpos [k] (written by K2), the gated shared
 // expert (y_shared [H] fp32 and its gate [1], nullable), residual [H] (act
 // dtype, nullable), out [H] bf16.
 struct CombineTail {
-  const float* w;
-  const int32_t* perm;
+  const float* wpos;
   const float* y_shared;
   const float* shared_gate;
   const void* residual;

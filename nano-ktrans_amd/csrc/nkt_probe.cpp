@@ -1,7 +1,10 @@
 // nkt_probe: a torch-free driver of the C ABI (include/nkt_moe.h) for
 // hardware-counter runs (rocprofv3 --pmc) and kernel traces of the MoE layer.
 //
-//   nkt_probe <workload> <tokens> [copies] [passes]
+//   nkt_probe <workload> <tokens> [copies] [passes] [layer]
+//
+// With "layer" each step is one nkt_moe_forward call (the layer's own launch
+// sequence); otherwise the stage entry points run one by one.
 //
 // workload: qwen3_int4 | qwen3_int8 | mixtral_int4 | qwen15_int8 | tiny_f32.
 // It first runs a calibration kernel of known traffic (fp32 negate over
@@ -103,7 +106,7 @@ static uint16_t f32_to_bf16(float f) {
 
 int main(int argc, char** argv) {
   if (argc < 3) {
-    fprintf(stderr, "usage: %s <workload> <tokens> [copies=4] [passes=2]\n", argv[0]);
+    fprintf(stderr, "usage: %s <workload> <tokens> [copies=4] [passes=2] [layer]\n", argv[0]);
     return 2;
   }
   const Workload* w = nullptr;
@@ -116,6 +119,7 @@ int main(int argc, char** argv) {
   const int T = atoi(argv[2]);
   const int copies = argc > 3 ? atoi(argv[3]) : 4;
   const int passes = argc > 4 ? atoi(argv[4]) : 2;
+  const bool layer = argc > 5 && !strcmp(argv[5], "layer");
   if (T < 1 || copies < 1 || passes < 1) {
     fprintf(stderr, "tokens, copies and passes must be positive\n");
     return 2;
@@ -171,6 +175,7 @@ int main(int argc, char** argv) {
   NKT(nkt_moe_workspace_bytes(handles[0], T, &ws_bytes, err, sizeof(err)));
   void *ws, *x, *logits, *out;
   CHECK(hipMalloc(&ws, ws_bytes));
+  CHECK(hipMemset(ws, 0, ws_bytes));  // the workspace's sync area starts at zero
   CHECK(hipMalloc(&x, (size_t)T * w->H * es));
   CHECK(hipMalloc(&out, (size_t)T * w->H * es));
   CHECK(hipMalloc(&logits, (size_t)T * w->E * es));
@@ -197,6 +202,10 @@ int main(int argc, char** argv) {
   fflush(stdout);
   for (int p = 0; p < passes; ++p) {
     for (int c = 0; c < copies; ++c) {
+      if (layer) {
+        NKT(nkt_moe_forward(handles[c], x, logits, T, out, ws, ws_bytes, st, err, sizeof(err)));
+        continue;
+      }
       NKT(nkt_moe_route(handles[c], logits, T, ws, ws_bytes, st, err, sizeof(err)));
       NKT(nkt_moe_experts_phase(handles[c], 0, x, T, ws, ws_bytes, st, err, sizeof(err)));
       NKT(nkt_moe_experts_phase(handles[c], 1, x, T, ws, ws_bytes, st, err, sizeof(err)));

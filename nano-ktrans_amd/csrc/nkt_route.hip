@@ -149,11 +149,14 @@ __device__ __forceinline__ int nth_set_bit(uint64_t m, int r) {
 
 // ids: the P = T k expert ids (LDS).  Every thread of the workgroup, after a
 // barrier that follows group_scan.
+// ws (LDS) / wpos (nullable): the pairs' routing weights, and their copy in
+// position order.
 __device__ __forceinline__ void group_write(const GroupLds& g, const int32_t* ids, int T, int k, int E, int bm,
                                             int max_tiles, int32_t* __restrict__ counts,
                                             int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
                                             int32_t* __restrict__ inv, int32_t* __restrict__ tiles,
-                                            int32_t* __restrict__ n_tiles, int32_t* __restrict__ tile_src) {
+                                            int32_t* __restrict__ n_tiles, int32_t* __restrict__ tile_src,
+                                            const float* ws, float* __restrict__ wpos) {
   const int tid = threadIdx.x;
   const int P = T * k;
   const int n_tile_all = g.n_tile_all;
@@ -197,6 +200,7 @@ __device__ __forceinline__ void group_write(const GroupLds& g, const int32_t* id
     const int pos = g.off[e] + __popc(g.mlo[e] & below_lo) + __popc(g.mhi[e] & below_hi);
     perm[pos] = p;
     inv[p] = pos;
+    if (wpos) wpos[pos] = ws[p];
   }
 }
 
@@ -386,8 +390,9 @@ __global__ void __launch_bounds__(kGroupThreads) route_group_kernel(
     int32_t* __restrict__ ids_out, float* __restrict__ w_out, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ inv,
     int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles, int32_t* __restrict__ tile_src,
-    const uint8_t* __restrict__ resident) {
+    const uint8_t* __restrict__ resident, float* __restrict__ wpos) {
   __shared__ int32_t ids_s[kFusedRouteMaxPairs];
+  __shared__ float w_s[kFusedRouteMaxPairs];
   __shared__ uint32_t selmask[kFusedRouteMaxTokens][8];
   __shared__ GroupLds g;
   __shared__ float sv[kGroupWaves][kMaxTopK];
@@ -409,6 +414,7 @@ __global__ void __launch_bounds__(kGroupThreads) route_group_kernel(
     route_token<VPL, BF16>(logits, t, E, k, flags, sv[wave], si[wave], &id, &w, selmask[t]);
     if (lane < k) {
       ids_s[t * k + lane] = id;
+      w_s[t * k + lane] = w;
       ids_out[(int64_t)t * k + lane] = id;
       w_out[(int64_t)t * k + lane] = w;
     }
@@ -416,7 +422,7 @@ __global__ void __launch_bounds__(kGroupThreads) route_group_kernel(
   __syncthreads();
   if (wave == 0) group_scan<VPL>(selmask, T, E, bm, res, g);
   __syncthreads();
-  group_write(g, ids_s, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, tile_src);
+  group_write(g, ids_s, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, tile_src, w_s, wpos);
 }
 
 // ---------------------------------------------------------------------------
@@ -447,6 +453,7 @@ constexpr uint32_t kSyncSpinLimit = 1u << 20;
 
 struct RouteHiddenLds {
   int32_t ids_s[kFusedRouteMaxPairs];
+  float w_s[kFusedRouteMaxPairs];
   uint32_t selmask[kFusedRouteMaxTokens][8];
   GroupLds g;
   float sv[kGroupWaves][kMaxTopK];
@@ -461,7 +468,7 @@ __global__ void __launch_bounds__(kGroupThreads) route_hidden_kernel(
     uint32_t gen, int32_t* __restrict__ ids_out, float* __restrict__ w_out, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ inv,
     int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles, int32_t* __restrict__ tile_src,
-    const uint8_t* __restrict__ resident) {
+    const uint8_t* __restrict__ resident, float* __restrict__ wpos) {
   constexpr int kRedBytes = kGroupWaves * 4 * 1024;  // partial tiles: [wave][column tile][64 lanes x 16 B]
   constexpr int kLdsBytes = sizeof(RouteHiddenLds) > kRedBytes ? sizeof(RouteHiddenLds) : kRedBytes;
   __shared__ __attribute__((aligned(16))) uint8_t smem[kLdsBytes];
@@ -547,6 +554,7 @@ __global__ void __launch_bounds__(kGroupThreads) route_hidden_kernel(
     route_token<VPL, true>(L.logits, t, E, k, flags, L.sv[wave], L.si[wave], &id, &w, L.selmask[t]);
     if (lane < k) {
       L.ids_s[t * k + lane] = id;
+      L.w_s[t * k + lane] = w;
       ids_out[(int64_t)t * k + lane] = id;
       w_out[(int64_t)t * k + lane] = w;
     }
@@ -554,7 +562,8 @@ __global__ void __launch_bounds__(kGroupThreads) route_hidden_kernel(
   __syncthreads();
   if (wave == 0) group_scan<VPL>(L.selmask, T, E, bm, res, L.g);
   __syncthreads();
-  group_write(L.g, L.ids_s, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, tile_src);
+  group_write(L.g, L.ids_s, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, tile_src, L.w_s,
+              wpos);
 }
 
 #define NKT_VPL_SWITCH(E, CASE) \
@@ -596,7 +605,7 @@ hipError_t launch_route_hidden(const void* x, const void* gate_packed, int H, in
                                int32_t* ids,
                                float* w, int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
                                int32_t* tiles, int32_t* n_tiles, int32_t* tile_src, const uint8_t* resident,
-                               hipStream_t stream) {
+                               float* wpos, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
   if (!route_hidden_fused(T, k, E, H) || gen == 0u) return hipErrorInvalidValue;
   if (bm <= 0 || (bm & (bm - 1)) != 0) return hipErrorInvalidValue;
@@ -608,7 +617,7 @@ hipError_t launch_route_hidden(const void* x, const void* gate_packed, int H, in
     hipLaunchKernelGGL((route_hidden_kernel<V>), grid, block, 0, stream, (const uint16_t*)x,              \
                        (const uint8_t*)gate_packed, H, T, E, k, flags, bm, max_tiles, (uint16_t*)logits,  \
                        (uint64_t*)tagged, sync, gen, ids, w, counts, offsets, perm, inv, tiles, n_tiles, tile_src, \
-                       resident);                                                                        \
+                       resident, wpos);                                                                  \
     break;
   NKT_VPL_SWITCH(E, NKT_RH_CASE)
 #undef NKT_RH_CASE
@@ -619,7 +628,7 @@ hipError_t launch_route_group(const void* logits, int act_bf16, int T, int E, in
                               unsigned flags, int bm, int max_tiles, int32_t* ids, float* w,
                               int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
                               int32_t* tiles, int32_t* n_tiles, int32_t* tile_src,
-                              const uint8_t* resident, hipStream_t stream) {
+                              const uint8_t* resident, float* wpos, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
   if (!route_group_fused(T, k)) return hipErrorInvalidValue;
   if (bm <= 0 || (bm & (bm - 1)) != 0) return hipErrorInvalidValue;
@@ -630,11 +639,11 @@ hipError_t launch_route_group(const void* logits, int act_bf16, int T, int E, in
     if (act_bf16)                                                                               \
       hipLaunchKernelGGL((route_group_kernel<V, true>), grid, block, 0, stream, logits, T, E, k, \
                          flags, bm, max_tiles, ids, w, counts, offsets, perm, inv, tiles,       \
-                         n_tiles, tile_src, resident);                                          \
+                         n_tiles, tile_src, resident, wpos);                                    \
     else                                                                                        \
       hipLaunchKernelGGL((route_group_kernel<V, false>), grid, block, 0, stream, logits, T, E,  \
                          k, flags, bm, max_tiles, ids, w, counts, offsets, perm, inv, tiles,    \
-                         n_tiles, tile_src, resident);                                          \
+                         n_tiles, tile_src, resident, wpos);                                    \
     break;
   NKT_VPL_SWITCH(E, NKT_RG_CASE)
 #undef NKT_RG_CASE
