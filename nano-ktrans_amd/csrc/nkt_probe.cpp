@@ -9,8 +9,9 @@
 // workload: qwen3_int4 | qwen3_int8 | mixtral_int4 | qwen15_int8 | tiny_f32.
 // It first runs a calibration kernel of known traffic (fp32 negate over
 // 256 MiB in and out, three launches), then `copies` distinct weight copies of
-// the layer (random codes written straight into the device layout, bf16
-// scales of 2^-7, so every launch streams its weights from HBM) and `passes`
+// the layer (quantized projections packed by nkt_moe_pack_weight from random
+// codes with bf16 scales of 2^-7, dense ones random in the device layout, so
+// every launch streams its weights from HBM) and `passes`
 // passes of route -> gate_up -> down -> combine over them.  Activations are
 // uniform in [-2, 2); router logits are uniform in [-1, 1) plus, for the
 // prefill workload qwen3_int8, the Zipf(1.1) bias -1.1 ln(e + 1) over expert
@@ -143,6 +144,18 @@ int main(int argc, char** argv) {
   }
 
   const int es = w->act == NKT_DTYPE_F32 ? 4 : 2;
+  const bool quant = w->wf == NKT_WEIGHT_INT4_G128 || w->wf == NKT_WEIGHT_INT8_PC;
+  // one projection's source codes and scales, reused for every pack
+  const int max_i = w->I > w->Is ? w->I : w->Is;
+  const size_t src_bytes = (size_t)2 * max_i * w->H;
+  const size_t src_scale_elems = (size_t)2 * max_i * (w->H / 128 > 1 ? w->H / 128 : 1) + (size_t)w->H * (max_i / 128 + 1);
+  void *src = nullptr, *src_scales = nullptr;
+  if (quant) {
+    CHECK(hipMalloc(&src, src_bytes));
+    CHECK(hipMalloc(&src_scales, src_scale_elems * 2));
+    hipLaunchKernelGGL(fill_u16, dim3(1024), dim3(256), 0, st, (uint16_t*)src_scales, src_scale_elems,
+                       f32_to_bf16(0.0078125f));
+  }
   std::vector<void*> handles(copies);
   std::vector<std::vector<void*>> slots(copies, std::vector<void*>(NKT_NUM_SLOTS, nullptr));
   for (int c = 0; c < copies; ++c) {
@@ -157,17 +170,30 @@ int main(int argc, char** argv) {
       NKT(nkt_moe_weight_bytes(handles[c], s, &bytes, err, sizeof(err)));
       if (!bytes) continue;
       CHECK(hipMalloc(&slots[c][s], bytes));
-      const bool scale = s == NKT_SLOT_GATE_UP_SCALES || s == NKT_SLOT_DOWN_SCALES ||
-                         s == NKT_SLOT_SHARED_GATE_UP_SCALES || s == NKT_SLOT_SHARED_DOWN_SCALES;
-      if (scale)
-        hipLaunchKernelGGL(fill_u16, dim3(1024), dim3(256), 0, st, (uint16_t*)slots[c][s], bytes / 2, f32_to_bf16(0.0078125f));
-      else if (s == NKT_SLOT_SHARED_GATE || w->wf == NKT_WEIGHT_F32 || w->wf == NKT_WEIGHT_BF16)
+      if (s == NKT_SLOT_SHARED_GATE || w->wf == NKT_WEIGHT_F32 || w->wf == NKT_WEIGHT_BF16)
         // dense weights in the activation dtype, uniform in [-2, 2)
         hipLaunchKernelGGL(fill_act, dim3(1024), dim3(256), 0, st, slots[c][s], bytes / es, (uint64_t)(1000 * c + s),
                            es == 4 ? 1 : 0);
-      else
-        hipLaunchKernelGGL(fill_random, dim3(4096), dim3(256), 0, st, (uint32_t*)slots[c][s], bytes / 4,
-                           (uint64_t)(1000 * c + s));
+    }
+    if (quant) {
+      // projections: (slot, rows, columns, experts)
+      const int proj[4][4] = {{NKT_SLOT_GATE_UP, 2 * w->I, w->H, w->E},
+                              {NKT_SLOT_DOWN, w->H, w->I, w->E},
+                              {NKT_SLOT_SHARED_GATE_UP, 2 * w->Is, w->H, w->Is > 0 ? 1 : 0},
+                              {NKT_SLOT_SHARED_DOWN, w->H, w->Is, w->Is > 0 ? 1 : 0}};
+      for (const auto& pr : proj)
+        for (int e = 0; e < pr[3]; ++e) {
+          const size_t nq = (size_t)pr[1] * pr[2] / (w->wf == NKT_WEIGHT_INT4_G128 ? 2 : 1);
+          const size_t ns = (size_t)pr[1] * (w->wf == NKT_WEIGHT_INT4_G128 ? pr[2] / 128 : 1);
+          if (nq > src_bytes || ns > src_scale_elems) {
+            fprintf(stderr, "source buffer too small\n");
+            return 1;
+          }
+          hipLaunchKernelGGL(fill_random, dim3(4096), dim3(256), 0, st, (uint32_t*)src, nq / 4,
+                             (uint64_t)(1000000 * c + 10000 * pr[0] + e));
+          NKT(nkt_moe_pack_weight(handles[c], pr[0], e, src, src_scales, slots[c][pr[0]], slots[c][pr[0] + 1], st,
+                                  err, sizeof(err)));
+        }
     }
     NKT(nkt_moe_bind_weights(handles[c], (const void* const*)slots[c].data(), err, sizeof(err)));
   }
@@ -221,6 +247,8 @@ int main(int argc, char** argv) {
       if (s) CHECK(hipFree(s));
     nkt_moe_destroy(handles[c]);
   }
+  if (src) CHECK(hipFree(src));
+  if (src_scales) CHECK(hipFree(src_scales));
   CHECK(hipFree(ws));
   CHECK(hipFree(x));
   CHECK(hipFree(out));
