@@ -15,7 +15,8 @@
 // passes of route -> gate_up -> down -> combine over them.  Activations are
 // uniform in [-2, 2); router logits are uniform in [-1, 1) plus, for the
 // prefill workload qwen3_int8, the Zipf(1.1) bias -1.1 ln(e + 1) over expert
-// ids.  Prints one line per step so a long run shows progress.
+// ids.  Prints one line per pass (with the pass's time per layer, eager
+// launches) so a long run shows progress.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -226,7 +227,11 @@ int main(int argc, char** argv) {
   }
   printf("%s T=%d: %d copies, %zu workspace bytes\n", w->name, T, copies, ws_bytes);
   fflush(stdout);
+  hipEvent_t ev0, ev1;
+  CHECK(hipEventCreate(&ev0));
+  CHECK(hipEventCreate(&ev1));
   for (int p = 0; p < passes; ++p) {
+    CHECK(hipEventRecord(ev0, st));
     for (int c = 0; c < copies; ++c) {
       if (layer) {
         NKT(nkt_moe_forward(handles[c], x, logits, T, out, ws, ws_bytes, st, err, sizeof(err)));
@@ -238,10 +243,15 @@ int main(int argc, char** argv) {
       if (w->Is > 0) NKT(nkt_moe_shared(handles[c], x, T, ws, ws_bytes, st, err, sizeof(err)));
       NKT(nkt_moe_combine(handles[c], T, out, ws, ws_bytes, st, err, sizeof(err)));
     }
+    CHECK(hipEventRecord(ev1, st));
     CHECK(hipStreamSynchronize(st));
-    printf("pass %d done\n", p);
+    float ms = 0.f;
+    CHECK(hipEventElapsedTime(&ms, ev0, ev1));
+    printf("pass %d done: %.2f us per layer (eager launches)\n", p, 1000.0f * ms / copies);
     fflush(stdout);
   }
+  CHECK(hipEventDestroy(ev0));
+  CHECK(hipEventDestroy(ev1));
   for (int c = 0; c < copies; ++c) {
     for (void* s : slots[c])
       if (s) CHECK(hipFree(s));

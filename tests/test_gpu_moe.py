@@ -406,7 +406,9 @@ def test_decode_outlier_channels(gpu_device, name, E, T):
 
 
 @pytest.mark.parametrize("name,E,T", [("qwen3_int4", 32, 16), ("mixtral_int4", None, 1), ("qwen3_int4", 32, 64),
-                                      ("qwen3_int4", None, 1), ("qwen15_int8_shared", None, 1)])
+                                      ("qwen3_int4", None, 1), ("qwen15_int8_shared", None, 1),
+                                      ("qwen3_int4", None, 16), ("qwen3_int4", None, 4), ("mixtral_int4", None, 16),
+                                      ("qwen3_int8", 32, 16)])
 def test_forward_matches_stages_and_leaves_sync_area_zero(gpu_device, name, E, T):
     """The layer equals route -> experts -> shared -> combine through the
     separate entry points bit for bit (at T = 1 the layer runs the down GEMV
