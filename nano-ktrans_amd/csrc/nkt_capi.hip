@@ -431,8 +431,21 @@ hipError_t launch_expert_gemm(const Handle* h, const GemmArgs& a, int phase, int
   return launch_gemm(a, h->wf, phase, bm, tiles, st, tm);
 }
 
+// The layer call's prefill form keeps y compact: fp16 by position with a
+// power-of-two scale per 256-column slab, in the NKT_WS_Y region (the fp16
+// rows first, then the fp32 inverse scales [T k, H / 256]) -- half the bytes
+// down writes and the combine reads again; the combine still sums in fp32.
+// The stage entry points keep NKT_WS_Y in fp32.
+bool compact_y(const Handle* h, const WsLayout& L) {
+  return L.bm == kPrefillTileM && prefill_form_ok(h, false) && h->H % 256 == 0;
+}
+uint16_t* y16_ptr(void* ws, const WsLayout& L) { return ws_ptr<uint16_t>(ws, L, NKT_WS_Y); }
+float* yscale_ptr(const Handle* h, void* ws, const WsLayout& L, int T) {
+  return (float*)(ws_ptr<uint8_t>(ws, L, NKT_WS_Y) + (size_t)T * h->k * h->H * 2);
+}
+
 int do_expert_phase(Handle* h, int phase, const void* x, int T, void* ws, const WsLayout& L,
-                    hipStream_t st, char* err, size_t len, const KernelTimer* tm = nullptr) {
+                    hipStream_t st, char* err, size_t len, const KernelTimer* tm = nullptr, bool compact = false) {
   if (phase == PHASE_GATE_UP && !x) {
     set_err(err, len, "null hidden_states");
     return NKT_ERR;
@@ -444,6 +457,10 @@ int do_expert_phase(Handle* h, int phase, const void* x, int T, void* ws, const 
       return NKT_ERR;
   } else {
     GemmArgs b = expert_args(h, PHASE_DOWN, false, ws_ptr<void>(ws, L, NKT_WS_H), ws, L, T);
+    if (compact && compact_y(h, L)) {
+      b.y16 = y16_ptr(ws, L);
+      b.yscale = yscale_ptr(h, ws, L, T);
+    }
     if (!check_hip(launch_expert_gemm(h, b, PHASE_DOWN, L.bm, L.max_tiles, st, tm), "down gemm", err, len))
       return NKT_ERR;
   }
@@ -451,9 +468,9 @@ int do_expert_phase(Handle* h, int phase, const void* x, int T, void* ws, const 
 }
 
 int do_experts(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipStream_t st,
-               char* err, size_t len) {
+               char* err, size_t len, bool compact = false) {
   if (do_expert_phase(h, PHASE_GATE_UP, x, T, ws, L, st, err, len) != NKT_OK) return NKT_ERR;
-  return do_expert_phase(h, PHASE_DOWN, x, T, ws, L, st, err, len);
+  return do_expert_phase(h, PHASE_DOWN, x, T, ws, L, st, err, len, nullptr, compact);
 }
 
 int do_shared(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipStream_t st,
@@ -483,18 +500,20 @@ int do_shared(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipS
 }
 
 int do_combine(Handle* h, int T, void* out, void* ws, const WsLayout& L, hipStream_t st, char* err,
-               size_t len, const void* extra = nullptr, const void* residual = nullptr) {
+               size_t len, const void* extra = nullptr, const void* residual = nullptr, bool compact = false) {
   if (!out) {
     set_err(err, len, "null output");
     return NKT_ERR;
   }
   const bool sh = h->Is > 0;
+  const bool y16 = compact && compact_y(h, L);
   if (!check_hip(launch_combine(ws_ptr<float>(ws, L, NKT_WS_Y), ws_ptr<int32_t>(ws, L, NKT_WS_TOPK_IDS),
                                 ws_ptr<float>(ws, L, NKT_WS_TOPK_WEIGHTS),
                                 y_pair_order(L) ? nullptr : ws_ptr<int32_t>(ws, L, NKT_WS_INV),
                                 sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_Y) : nullptr,
                                 sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE) : nullptr, h->resident,
-                                extra, residual, T, h->k, h->H, out, h->act_bf16, st),
+                                extra, residual, T, h->k, h->H, out, h->act_bf16, st,
+                                y16 ? y16_ptr(ws, L) : nullptr, y16 ? yscale_ptr(h, ws, L, T) : nullptr),
                  "combine kernel", err, len))
     return NKT_ERR;
   return NKT_OK;
@@ -623,14 +642,14 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
     return NKT_OK;
   }
   int rc = route();
-  if (rc == NKT_OK) rc = do_experts(h, x, T, ws, L, st, err, len);
+  if (rc == NKT_OK) rc = do_experts(h, x, T, ws, L, st, err, len, true);
   if (rc == NKT_OK && !side && h->Is > 0) rc = do_shared(h, x, T, ws, L, st, err, len);
   if (side) {
     const hipError_t we = hipStreamWaitEvent(st, h->join_ev, 0);
     if (rc == NKT_OK && !check_hip(we, "join wait", err, len)) rc = NKT_ERR;
   }
   if (rc != NKT_OK) return rc;
-  return do_combine(h, T, out, ws, L, st, err, len, nullptr, residual);
+  return do_combine(h, T, out, ws, L, st, err, len, nullptr, residual, true);
 }
 
 // ---------------------------------------------------------------------------

@@ -61,9 +61,12 @@ __global__ void __launch_bounds__(256) shared_gate_kernel(const void* __restrict
 // order; inv == nullptr) or at rows inv[t k + j] (position order); in pair
 // order every load is issued at once.  The terms are added in ascending
 // expert id through the thread's own LDS slots.
-template <int K>
+// Y16: y is the prefill down's compact form (fp16 [rows, H] + fp32 inverse
+// scale per row and 256-column slab, yscale), expanded to fp32 on load.
+template <int K, bool Y16>
 __global__ void __launch_bounds__(256) combine_kernel(
-    const float* __restrict__ y, const int32_t* __restrict__ ids, const float* __restrict__ w,
+    const float* __restrict__ y, const uint16_t* __restrict__ y16, const float* __restrict__ yscale,
+    const int32_t* __restrict__ ids, const float* __restrict__ w,
     const int32_t* __restrict__ inv, const float* __restrict__ y_shared, const float* __restrict__ shared_gate, const uint8_t* __restrict__ resident,
     const void* __restrict__ extra, const void* __restrict__ residual, int num_tokens, int H,
     void* __restrict__ out, int out_bf16) {
@@ -73,12 +76,26 @@ __global__ void __launch_bounds__(256) combine_kernel(
   if (4 * c >= H) return;
   // every load first: the k rows, the gated shared row, ids and weights
   f32x4 v[K];
+  float vs16[K];
 #pragma unroll
   for (int j = 0; j < K; ++j) {
     // a corrupt position never reads outside y
     const int64_t row = inv ? min(max(inv[(int64_t)t * K + j], 0), num_tokens * K - 1) : (int64_t)t * K + j;
-    v[j] = *(const f32x4*)(y + row * H + 4 * c);
+    if (Y16) {
+      const u32x2 hv = *(const u32x2*)(y16 + row * H + 4 * c);
+      vs16[j] = yscale[row * (H / 256) + (4 * c) / 256];
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        v[j][2 * q] = (float)__builtin_bit_cast(_Float16, (uint16_t)(hv[q] & 0xffffu));
+        v[j][2 * q + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(hv[q] >> 16));
+      }
+    } else {
+      v[j] = *(const f32x4*)(y + row * H + 4 * c);
+    }
   }
+  if (Y16)
+#pragma unroll
+    for (int j = 0; j < K; ++j) v[j] *= vs16[j];
   f32x4 vs = f32x4{0.f, 0.f, 0.f, 0.f};
   float sg = 0.f;
   if (y_shared) {
@@ -229,13 +246,18 @@ hipError_t launch_shared_gate(const void* x, const void* gate_w, int act_bf16, i
 
 hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, const int32_t* inv, const float* y_shared, const float* shared_gate, const uint8_t* resident,
                           const void* extra, const void* residual, int T, int k, int H, void* out,
-                          int out_bf16, hipStream_t stream) {
+                          int out_bf16, hipStream_t stream, const uint16_t* y16, const float* yscale) {
   if (T <= 0) return hipSuccess;
+  if (y16 && (!yscale || H % 256 != 0)) return hipErrorInvalidValue;
   dim3 grid(T, (H / 4 + 255) / 256), block(256);
-#define NKT_COMBINE_CASE(KK)                                                                   \
-  case KK:                                                                                     \
-    hipLaunchKernelGGL(combine_kernel<KK>, grid, block, 0, stream, y, ids, w, inv, y_shared,   \
-                       shared_gate, resident, extra, residual, T, H, out, out_bf16);           \
+#define NKT_COMBINE_CASE(KK)                                                                          \
+  case KK:                                                                                            \
+    if (y16)                                                                                          \
+      hipLaunchKernelGGL((combine_kernel<KK, true>), grid, block, 0, stream, y, y16, yscale, ids, w, inv, \
+                         y_shared, shared_gate, resident, extra, residual, T, H, out, out_bf16);      \
+    else                                                                                              \
+      hipLaunchKernelGGL((combine_kernel<KK, false>), grid, block, 0, stream, y, y16, yscale, ids, w, inv, \
+                         y_shared, shared_gate, resident, extra, residual, T, H, out, out_bf16);      \
     break;
   switch (k) {
     NKT_COMBINE_CASE(1)

@@ -209,6 +209,62 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[1
         a.hsum[(int64_t)(row0 + tid) * (a.I / 128) + slab] = s;
       }
     }
+  } else if (a.y16) {
+    // compact y: per position, the slab's 256 rows as fp16 times 2^sh, sh
+    // from the largest |y| of the position in the slab (lanes l, l ^ 16,
+    // l ^ 32, l ^ 48 hold one position's rows of this wave; the waves meet
+    // in LDS), so that largest value lands in [2^14, 2^15); 2^-sh goes to
+    // yscale [position][slab]
+    float m[kCT];
+#pragma unroll
+    for (int c = 0; c < kCT; ++c) m[c] = 0.f;
+#pragma unroll
+    for (int r = 0; r < kRT; ++r) {
+      f32x4 sr = f32x4{1.f, 1.f, 1.f, 1.f};
+      if (WF == WF_I8) sr = bf16x4_to_f32(*(const u32x2*)(sexp + wrow[r] + rq));
+#pragma unroll
+      for (int c = 0; c < kCT; ++c) {
+        if (WF == WF_I8) acc[r][c] *= sr;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) m[c] = fmaxf(m[c], fabsf(acc[r][c][v]));
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < kCT; ++c) {
+      m[c] = fmaxf(m[c], __shfl_xor(m[c], 16));
+      m[c] = fmaxf(m[c], __shfl_xor(m[c], 32));
+      if (lane < 16) hpart[wave][c * 16 + lane] = m[c];
+    }
+    __syncthreads();
+    const int n_slabs = a.N / 256;
+#pragma unroll
+    for (int c = 0; c < kCT; ++c) {
+      const int pl = c * 16 + (lane & 15);
+      float mx = hpart[0][pl];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) mx = fmaxf(mx, hpart[w][pl]);
+      int sh = 0;
+      if (mx > 0.f && mx <= 3.402823466e38f) {
+        int e;
+        frexpf(mx, &e);
+        sh = min(max(15 - e, -126), 126);
+      }
+      const float sc = __builtin_ldexpf(1.0f, sh);
+      if (pl < rows) {
+        const int64_t orow = orow_l[pl];
+        if (wave == 0 && lane < 16) a.yscale[orow * n_slabs + slab] = __builtin_ldexpf(1.0f, -sh);
+#pragma unroll
+        for (int r = 0; r < kRT; ++r) {
+          u32x2 pk;
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const _Float16 lo = (_Float16)(acc[r][c][2 * q] * sc), hi = (_Float16)(acc[r][c][2 * q + 1] * sc);
+            pk[q] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+          }
+          *(u32x2*)(a.y16 + orow * a.N + wrow[r] + rq) = pk;
+        }
+      }
+    }
   } else {
 #pragma unroll
     for (int r = 0; r < kRT; ++r) {

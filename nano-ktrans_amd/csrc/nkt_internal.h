@@ -54,6 +54,11 @@ struct GemmArgs {
   // down of the routed experts: output row of each position (its pair
   // t k + slot), so y comes out in pair order; nullptr: the position
   const int32_t* out_rows;
+  // prefill down, compact y (y16 != nullptr, out unused): y16 [rows, N] fp16
+  // by position, each 256-row slab of a position times a power of two whose
+  // inverse goes to yscale [rows, N / 256]
+  uint16_t* y16;
+  float* yscale;
   // single-token decode gate_up that routes its token itself
   // (route_logits != nullptr, [1, route_E] bf16): every workgroup runs K1
   // on the one row of logits, workgroup (0, 0) also writes K1's and K2's
@@ -196,10 +201,12 @@ hipError_t launch_shared_gate(const void* x, const void* gate_w, int act_bf16, i
                               float* gate_out, hipStream_t stream);
 
 // y: the k expert rows of token t at rows t k .. t k + k - 1 (pair order,
-// inv == nullptr) or at rows inv[t k + j] (position order)
+// inv == nullptr) or at rows inv[t k + j] (position order); y16 != nullptr:
+// the rows are the prefill down's compact y (fp16 + yscale), y unused
 hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, const int32_t* inv, const float* y_shared,
                           const float* shared_gate, const uint8_t* resident, const void* extra, const void* residual,
-                          int T, int k, int H, void* out, int out_bf16, hipStream_t stream);
+                          int T, int k, int H, void* out, int out_bf16, hipStream_t stream,
+                          const uint16_t* y16 = nullptr, const float* yscale = nullptr);
 
 // bf16 RMSNorm rows of x [T, H] with weight w [H] (decoder-block form)
 hipError_t launch_rmsnorm(const void* x, const void* w, float eps, int T, int H, void* out, hipStream_t stream);

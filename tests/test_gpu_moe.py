@@ -408,12 +408,16 @@ def test_decode_outlier_channels(gpu_device, name, E, T):
 @pytest.mark.parametrize("name,E,T", [("qwen3_int4", 32, 16), ("mixtral_int4", None, 1), ("qwen3_int4", 32, 64),
                                       ("qwen3_int4", None, 1), ("qwen15_int8_shared", None, 1),
                                       ("qwen3_int4", None, 16), ("qwen3_int4", None, 4), ("mixtral_int4", None, 16),
-                                      ("qwen3_int8", 32, 16)])
+                                      ("qwen3_int8", 32, 16), ("qwen3_int8", 32, 512), ("qwen15_int8_shared", None, 1024)])
 def test_forward_matches_stages_and_leaves_sync_area_zero(gpu_device, name, E, T):
     """The layer equals route -> experts -> shared -> combine through the
     separate entry points bit for bit (at T = 1 the layer runs the down GEMV
-    and the combine as one launch), and leaves the workspace's sync area (the
-    NKT_SYNC_AREA_BYTES before NKT_WS_TOPK_IDS) all zero."""
+    and the combine as one launch) in the decode form; in the prefill form
+    the layer keeps y as fp16 with a power-of-two scale per position and
+    256-column slab (the stages keep fp32 y), so every output element is
+    within 2^-12 of the largest |y| plus one bf16 step of the stages'.
+    The layer leaves the workspace's sync area (the NKT_SYNC_AREA_BYTES
+    before NKT_WS_TOPK_IDS) all zero."""
     import ctypes
 
     from nano_ktrans_amd import _native as N
@@ -434,9 +438,18 @@ def test_forward_matches_stages_and_leaves_sync_area_zero(gpu_device, name, E, T
     routed = [native.region(T, r, dt, shp).clone() for r, dt, shp in regions]
     for got, want in zip(routed, native.route(logits)):
         assert torch.equal(got, want)
-    native.experts(x)
+    _, y = native.experts(x)
     if layer.cfg.Is:
         native.shared(x)
     b = native.combine(T)
     torch.cuda.synchronize()
-    assert torch.equal(a, b)
+    if T * k <= 12 * E:  # decode form
+        assert torch.equal(a, b)
+    else:
+        ymax = y.abs().max().item()
+        # the sums differ by at most 2^-12 ymax; each is then rounded to bf16
+        # (one step is at most 2^-7 of the value)
+        bound = 2.0 ** -12 * ymax + 2.0 ** -7 * torch.maximum(a.float().abs(), b.float().abs())
+        diff = (a.float() - b.float()).abs()
+        announce(f"  compact y: max diff {diff.max().item():.3e}, largest |y| {ymax:.3e}")
+        assert bool((diff <= bound).all())
