@@ -491,11 +491,29 @@ __global__ void __launch_bounds__(kGroupThreads) route_hidden_kernel(
     f32x4 acc[4];
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int kb = wave; kb < NKB; kb += kGroupWaves) {
-      const u32x4 a = *(const u32x4*)(ablk + (size_t)kb * 1024);
+    // four K blocks per wave at a time, every load issued before the first
+    // MFMA (one memory round trip per four blocks, not one per block); all
+    // four column tiles always (rows past T read row 0; their sums are never
+    // stored), K blocks past the end re-read the last one and add nothing
+    constexpr int kKbBatch = 4;
+    for (int kb0 = wave; kb0 < NKB; kb0 += kKbBatch * kGroupWaves) {
+      u32x4 a[kKbBatch], xv[kKbBatch][4];
 #pragma unroll
-      for (int ct = 0; ct < 4; ++ct)
-        if (ct < CT) acc[ct] = mfma_bf16(a, *(const u32x4*)(xcol[ct] + kb * 32), acc[ct]);
+      for (int i = 0; i < kKbBatch; ++i) {
+        const int kb = min(kb0 + i * kGroupWaves, NKB - 1);
+        a[i] = *(const u32x4*)(ablk + (size_t)kb * 1024);
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) xv[i][ct] = *(const u32x4*)(xcol[ct] + kb * 32);
+      }
+      // keep the loads ahead of the MFMAs (the scheduler would sink each to
+      // its use, a round trip per block)
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < kKbBatch; ++i) {
+        if (kb0 + i * kGroupWaves >= NKB) a[i] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) acc[ct] = mfma_bf16(a[i], xv[i][ct], acc[ct]);
+      }
     }
     f32x4* red = (f32x4*)smem;
 #pragma unroll
