@@ -492,9 +492,9 @@ __global__ void __launch_bounds__(kGroupThreads) route_hidden_kernel(
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
     // four K blocks per wave at a time, every load issued before the first
-    // MFMA (one memory round trip per four blocks, not one per block); all
-    // four column tiles always (rows past T read row 0; their sums are never
-    // stored), K blocks past the end re-read the last one and add nothing
+    // MFMA (one memory round trip per four blocks, not one per block); K
+    // blocks past the end re-read the last one and add nothing, column tiles
+    // past CT load nothing (their sums are never stored)
     constexpr int kKbBatch = 4;
     for (int kb0 = wave; kb0 < NKB; kb0 += kKbBatch * kGroupWaves) {
       u32x4 a[kKbBatch], xv[kKbBatch][4];
@@ -503,7 +503,8 @@ __global__ void __launch_bounds__(kGroupThreads) route_hidden_kernel(
         const int kb = min(kb0 + i * kGroupWaves, NKB - 1);
         a[i] = *(const u32x4*)(ablk + (size_t)kb * 1024);
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct) xv[i][ct] = *(const u32x4*)(xcol[ct] + kb * 32);
+        for (int ct = 0; ct < 4; ++ct)
+          xv[i][ct] = ct < CT ? *(const u32x4*)(xcol[ct] + kb * 32) : u32x4{0u, 0u, 0u, 0u};
       }
       // keep the loads ahead of the MFMAs (the scheduler would sink each to
       // its use, a round trip per block)
