@@ -61,12 +61,37 @@ __global__ void __launch_bounds__(256) shared_gate_kernel(const void* __restrict
 // order; inv == nullptr) or at rows inv[t k + j] (position order); in pair
 // order every load is issued at once.  The terms are added in ascending
 // expert id through the thread's own LDS slots.
-// Y16: y is the prefill down's compact form (fp16 [rows, H] + fp32 inverse
-// scale per row and 256-column slab, yscale), expanded to fp32 on load.
-template <int K, bool Y16>
+// The end of one token's four output columns: + the offload backend's sum,
+// + gate x shared expert row, + the residual, one rounding, store.
+__device__ __forceinline__ void combine_tail(f32x4 acc, int t, int col, int H, const void* extra, const f32x4* vs,
+                                             float sg, const void* residual, void* out, int out_bf16) {
+  const int64_t o = (int64_t)t * H + col;
+  if (extra) {
+    if (out_bf16)
+      acc += bf16x4_to_f32(*(const u32x2*)((const uint16_t*)extra + o));
+    else
+      acc += *(const f32x4*)((const float*)extra + o);
+  }
+  if (vs) acc += sg * *vs;
+  if (residual) {
+    if (out_bf16)
+      acc += bf16x4_to_f32(*(const u32x2*)((const uint16_t*)residual + o));
+    else
+      acc += *(const f32x4*)((const float*)residual + o);
+  }
+  if (out_bf16) {
+    u32x2 pk;
+    pk[0] = pack_bf16x2(acc[0], acc[1]);
+    pk[1] = pack_bf16x2(acc[2], acc[3]);
+    *(u32x2*)((uint16_t*)out + o) = pk;
+  } else {
+    *(f32x4*)((float*)out + o) = acc;
+  }
+}
+
+template <int K>
 __global__ void __launch_bounds__(256) combine_kernel(
-    const float* __restrict__ y, const uint16_t* __restrict__ y16, const float* __restrict__ yscale,
-    const int32_t* __restrict__ ids, const float* __restrict__ w,
+    const float* __restrict__ y, const int32_t* __restrict__ ids, const float* __restrict__ w,
     const int32_t* __restrict__ inv, const float* __restrict__ y_shared, const float* __restrict__ shared_gate, const uint8_t* __restrict__ resident,
     const void* __restrict__ extra, const void* __restrict__ residual, int num_tokens, int H,
     void* __restrict__ out, int out_bf16) {
@@ -76,26 +101,12 @@ __global__ void __launch_bounds__(256) combine_kernel(
   if (4 * c >= H) return;
   // every load first: the k rows, the gated shared row, ids and weights
   f32x4 v[K];
-  float vs16[K];
 #pragma unroll
   for (int j = 0; j < K; ++j) {
     // a corrupt position never reads outside y
     const int64_t row = inv ? min(max(inv[(int64_t)t * K + j], 0), num_tokens * K - 1) : (int64_t)t * K + j;
-    if (Y16) {
-      const u32x2 hv = *(const u32x2*)(y16 + row * H + 4 * c);
-      vs16[j] = yscale[row * (H / 256) + (4 * c) / 256];
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        v[j][2 * q] = (float)__builtin_bit_cast(_Float16, (uint16_t)(hv[q] & 0xffffu));
-        v[j][2 * q + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(hv[q] >> 16));
-      }
-    } else {
-      v[j] = *(const f32x4*)(y + row * H + 4 * c);
-    }
+    v[j] = *(const f32x4*)(y + row * H + 4 * c);
   }
-  if (Y16)
-#pragma unroll
-    for (int j = 0; j < K; ++j) v[j] *= vs16[j];
   f32x4 vs = f32x4{0.f, 0.f, 0.f, 0.f};
   float sg = 0.f;
   if (y_shared) {
@@ -125,28 +136,72 @@ __global__ void __launch_bounds__(256) combine_kernel(
   f32x4 acc = terms[0][threadIdx.x];
 #pragma unroll
   for (int r = 1; r < K; ++r) acc += terms[r][threadIdx.x];
-  if (extra) {
-    if (out_bf16) {
-      const u32x2 e = *(const u32x2*)((const uint16_t*)extra + (int64_t)t * H + 4 * c);
-      acc += bf16x4_to_f32(e);
-    } else {
-      acc += *(const f32x4*)((const float*)extra + (int64_t)t * H + 4 * c);
+  combine_tail(acc, t, 4 * c, H, extra, y_shared ? &vs : nullptr, sg, residual, out, out_bf16);
+}
+
+// The same sum over the prefill layer's compact y (fp16 rows, one fp32
+// inverse scale per row and 256-column slab in yscale), eight columns per
+// thread so every row load is 16 bytes: each half of four columns goes
+// through the thread's LDS slots in turn, with combine_kernel's order and
+// arithmetic on the expanded values.
+template <int K>
+__global__ void __launch_bounds__(256) combine16_kernel(
+    const uint16_t* __restrict__ y16, const float* __restrict__ yscale, const int32_t* __restrict__ ids,
+    const float* __restrict__ w, const int32_t* __restrict__ inv, const float* __restrict__ y_shared,
+    const float* __restrict__ shared_gate, const uint8_t* __restrict__ resident, const void* __restrict__ extra,
+    const void* __restrict__ residual, int num_tokens, int H, void* __restrict__ out, int out_bf16) {
+  __shared__ f32x4 terms[K][256];
+  const int t = blockIdx.x;
+  const int c = blockIdx.y * blockDim.x + threadIdx.x;  // 8-column group
+  if (8 * c >= H) return;
+  u32x4 hv[K];
+  float sc[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const int64_t row = inv ? min(max(inv[(int64_t)t * K + j], 0), num_tokens * K - 1) : (int64_t)t * K + j;
+    hv[j] = *(const u32x4*)(y16 + row * H + 8 * c);
+    sc[j] = yscale[row * (H / 256) + (8 * c) / 256];
+  }
+  int sid[K];
+  float sw[K];
+  bool sres[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    sid[j] = ids[(int64_t)t * K + j];
+    sw[j] = w[(int64_t)t * K + j];
+    sres[j] = resident ? resident[sid[j]] != 0 : true;
+  }
+  int rk[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    int r = 0;
+#pragma unroll
+    for (int i = 0; i < K; ++i) r += (sid[i] < sid[j]) ? 1 : 0;
+    rk[j] = r;
+  }
+  const float sg = y_shared ? shared_gate[t] : 0.f;
+  const f32x4 zero = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      f32x4 v;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t word = hv[j][2 * half + q];
+        v[2 * q] = (float)__builtin_bit_cast(_Float16, (uint16_t)(word & 0xffffu));
+        v[2 * q + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(word >> 16));
+      }
+      v *= sc[j];
+      terms[rk[j]][threadIdx.x] = sres[j] ? sw[j] * v : zero;
     }
-  }
-  if (y_shared) acc += sg * vs;
-  if (residual) {
-    if (out_bf16)
-      acc += bf16x4_to_f32(*(const u32x2*)((const uint16_t*)residual + (int64_t)t * H + 4 * c));
-    else
-      acc += *(const f32x4*)((const float*)residual + (int64_t)t * H + 4 * c);
-  }
-  if (out_bf16) {
-    u32x2 pk;
-    pk[0] = pack_bf16x2(acc[0], acc[1]);
-    pk[1] = pack_bf16x2(acc[2], acc[3]);
-    *(u32x2*)((uint16_t*)out + (int64_t)t * H + 4 * c) = pk;
-  } else {
-    *(f32x4*)((float*)out + (int64_t)t * H + 4 * c) = acc;
+    f32x4 acc = terms[0][threadIdx.x];
+#pragma unroll
+    for (int r = 1; r < K; ++r) acc += terms[r][threadIdx.x];
+    const int col = 8 * c + 4 * half;
+    f32x4 vs = zero;
+    if (y_shared) vs = *(const f32x4*)(y_shared + (int64_t)t * H + col);
+    combine_tail(acc, t, col, H, extra, y_shared ? &vs : nullptr, sg, residual, out, out_bf16);
   }
 }
 
@@ -249,15 +304,15 @@ hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, co
                           int out_bf16, hipStream_t stream, const uint16_t* y16, const float* yscale) {
   if (T <= 0) return hipSuccess;
   if (y16 && (!yscale || H % 256 != 0)) return hipErrorInvalidValue;
-  dim3 grid(T, (H / 4 + 255) / 256), block(256);
-#define NKT_COMBINE_CASE(KK)                                                                          \
-  case KK:                                                                                            \
-    if (y16)                                                                                          \
-      hipLaunchKernelGGL((combine_kernel<KK, true>), grid, block, 0, stream, y, y16, yscale, ids, w, inv, \
-                         y_shared, shared_gate, resident, extra, residual, T, H, out, out_bf16);      \
-    else                                                                                              \
-      hipLaunchKernelGGL((combine_kernel<KK, false>), grid, block, 0, stream, y, y16, yscale, ids, w, inv, \
-                         y_shared, shared_gate, resident, extra, residual, T, H, out, out_bf16);      \
+  dim3 grid(T, (H / 4 + 255) / 256), grid16(T, (H / 8 + 255) / 256), block(256);
+#define NKT_COMBINE_CASE(KK)                                                                              \
+  case KK:                                                                                                \
+    if (y16)                                                                                              \
+      hipLaunchKernelGGL(combine16_kernel<KK>, grid16, block, 0, stream, y16, yscale, ids, w, inv, y_shared, \
+                         shared_gate, resident, extra, residual, T, H, out, out_bf16);                    \
+    else                                                                                                  \
+      hipLaunchKernelGGL(combine_kernel<KK>, grid, block, 0, stream, y, ids, w, inv, y_shared, shared_gate,  \
+                         resident, extra, residual, T, H, out, out_bf16);                                 \
     break;
   switch (k) {
     NKT_COMBINE_CASE(1)
