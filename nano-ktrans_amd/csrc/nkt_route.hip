@@ -247,16 +247,33 @@ __global__ void __launch_bounds__(1024) scatter_kernel(const int32_t* __restrict
   const int nb = gridDim.x;
   const int b = blockIdx.x;
   // totals per expert and the pairs of earlier blocks, blocks in order
-  if (tid < E) {
-    int t = 0, q = 0;
+  if (hist) {
+    if (tid < E) {
+      int t = 0, q = 0;
 #pragma unroll 8
-    for (int bb = 0; bb < nb; ++bb) {
-      const int c = hist[(int64_t)bb * E + tid];
-      q += bb < b ? c : 0;
-      t += c;
+      for (int bb = 0; bb < nb; ++bb) {
+        const int c = hist[(int64_t)bb * E + tid];
+        q += bb < b ? c : 0;
+        t += c;
+      }
+      tot[tid] = t;
+      pre[tid] = q;
     }
-    tot[tid] = t;
-    pre[tid] = q;
+  } else {
+    // no count launch (few pairs): every block counts all pairs itself
+    if (tid < E) {
+      tot[tid] = 0;
+      pre[tid] = 0;
+    }
+    __syncthreads();
+    const int pstart = b * kPairsPerBlock;
+    for (int p = tid; p < P; p += 1024) {
+      const int e = ids[p];
+      if (e >= 0 && e < E) {
+        atomicAdd(&tot[e], 1);
+        if (p < pstart) atomicAdd(&pre[e], 1);
+      }
+    }
   }
   for (int i = tid; i < kScatterWaves * kMaxExperts; i += 1024) (&whist[0][0])[i] = 0;
   __syncthreads();
@@ -366,6 +383,8 @@ __global__ void __launch_bounds__(1024) scatter_kernel(const int32_t* __restrict
 
 int group_hist_blocks(int P) { return (P + kPairsPerBlock - 1) / kPairsPerBlock; }
 
+constexpr int kSelfCountMaxPairs = 8192;
+
 hipError_t launch_group_multi(const int32_t* ids, int T, int k, int E, int bm, int max_tiles, int32_t* hist,
                               int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv, int32_t* tiles,
                               int32_t* n_tiles, int32_t* tile_src, const uint8_t* resident,
@@ -374,11 +393,16 @@ hipError_t launch_group_multi(const int32_t* ids, int T, int k, int E, int bm, i
   const int P = T * k;
   const int nb = group_hist_blocks(P);
   if (nb <= 0) return hipSuccess;
-  hipLaunchKernelGGL(count_kernel, dim3(nb), dim3(1024), 0, stream, ids, P, E, hist);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(scatter_kernel, dim3(nb), dim3(1024), 0, stream, ids, P, k, E, bm, max_tiles, hist, counts,
-                     offsets, perm, inv, tiles, n_tiles, tile_src, resident);
+  // up to kSelfCountMaxPairs pairs every scatter block reads all ids itself
+  // (at most 64 KiB each), which costs less than a count launch
+  const bool self_count = P <= kSelfCountMaxPairs;
+  if (!self_count) {
+    hipLaunchKernelGGL(count_kernel, dim3(nb), dim3(1024), 0, stream, ids, P, E, hist);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(scatter_kernel, dim3(nb), dim3(1024), 0, stream, ids, P, k, E, bm, max_tiles,
+                     self_count ? nullptr : hist, counts, offsets, perm, inv, tiles, n_tiles, tile_src, resident);
   return hipGetLastError();
 }
 
