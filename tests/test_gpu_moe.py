@@ -116,7 +116,8 @@ def test_qwen3_int8_prefill_row_scales(gpu_device):
     """The int8 prefill gate_up multiplies power-of-two-scaled fp16 copies of
     the token rows: rows scaled by 2^-40 .. 2^40, a zero row and rows whose
     entries span 2^20 must each match the oracle to the bf16 tolerance of
-    their own magnitude (routing from the unscaled rows)."""
+    their own magnitude (routing from the unscaled rows); so must rows whose
+    entries span 2^40 and 2^64."""
     announce("forward qwen3_int8 E=32 T=320 scaled rows")
     layer, native = _layer("qwen3_int8", E=32)
     T = 320
@@ -127,6 +128,13 @@ def test_qwen3_int8_prefill_row_scales(gpu_device):
     xf = xf * scale[:, None]
     xf[7] = 0.0
     xf[9, ::97] *= 2.0 ** 20  # one row spanning 2^20 (plus the N(0,1) spread)
+    # rows spanning 2^40 and 2^64: entries below 2^-32 of the row's largest
+    # fall out of the fp16 copy; their share of the output is below the
+    # bf16 tolerance of the row's own magnitude
+    xf[11, ::97] *= 2.0 ** 20
+    xf[11, 1::97] *= 2.0 ** -20
+    xf[13, ::53] *= 2.0 ** 32
+    xf[13, 5::53] *= 2.0 ** -32
     xs = xf.to(torch.bfloat16)
     out = native.forward(xs, logits)
     torch.cuda.synchronize()
