@@ -17,7 +17,11 @@ Printed JSON fields beyond the standard ones:
   roofline       dominant kernel: algorithmic bytes (active experts' codes + scales,
                  activations in/out) / its average event-timed duration vs 8 TB/s;
                  traffic (and, for the prefill form, MFMA busy %) from rocprofv3
-                 counters on nano-ktrans_amd/nkt_probe (profiles/pmc_moe_layer_counters.md)
+                 counters on nano-ktrans_amd/nkt_probe (profiles/pmc_moe_layer_counters.md);
+                 beside the rated peak, the practical one measured in the same run:
+                 vendor_copy (a 256 MB torch device copy, read + write bytes/s) for
+                 the HBM bound, vendor_gemm (torch.matmul in fp16 of the same
+                 multiply-adds as one dense [T k, N, K] GEMM) for the MFMA bound
   cpu_baseline   the reference CPU expert loop (oracle/cpu_loop.py, a torch
                  restatement of nano_ktrans/kernels/cpu_moe.py:491-539) on this
                  host's cores for the headline; cpu_baselines: every config
@@ -341,7 +345,7 @@ def bench_workload(w, T, layers, router, steps, warmup, device):
                 breakdown_us=stages, layer_bytes=layer_bytes, layer_hbm_frac=layer_bytes / (ms * 1e-3) / HBM_PEAK,
                 gate_up=dict(kernel=form, bytes=gate_up_bytes, flops=gate_up_flops, us=gate_up_us),
                 down=dict(kernel=form, bytes=down_bytes, flops=down_flops, us=down_us),
-                inputs=(xs[0], ls[0]))
+                shape=dict(k=w.k, H=w.H, I=w.I), inputs=(xs[0], ls[0]))
 
 
 COUNTERS_MD = os.path.join(ROOT, "profiles", "pmc_moe_layer_counters.md")
@@ -372,6 +376,57 @@ def counter_table():
     return out
 
 
+_CEILINGS = {}
+
+
+def _event_ms(fn, reps):
+    import torch
+
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def vendor_gemm_tflops(M, N, K):
+    """Rate (TFLOP/s) of one dense fp16 [M, K] x [K, N] product through
+    torch.matmul (the vendor GEMM library) on this GPU: the practical
+    matrix-core ceiling for the same multiply-add count, measured because
+    MI355X's clock drops well below its rated one under sustained MFMA load."""
+    key = ("gemm", M, N, K)
+    if key not in _CEILINGS:
+        import torch
+
+        a = torch.randn(M, K, device="cuda", dtype=torch.float16)
+        b = torch.randn(K, N, device="cuda", dtype=torch.float16)
+        flop = 2.0 * M * N * K
+        ms = _event_ms(lambda: a @ b, max(3, min(20, int(4e12 / flop))))
+        _CEILINGS[key] = flop / (ms * 1e-3) / 1e12
+        del a, b
+    return _CEILINGS[key]
+
+
+def vendor_copy_gbps(nbytes=256 << 20):
+    """Rate (GB/s, bytes read + written) of a device-to-device copy of nbytes
+    through torch on this GPU: the practical HBM streaming rate."""
+    key = ("copy", nbytes)
+    if key not in _CEILINGS:
+        import torch
+
+        src = torch.empty(nbytes // 2, device="cuda", dtype=torch.float16).normal_()
+        dst = torch.empty_like(src)
+        ms = _event_ms(lambda: dst.copy_(src), 20)
+        _CEILINGS[key] = 2.0 * nbytes / (ms * 1e-3) / 1e9
+        del src, dst
+    return _CEILINGS[key]
+
+
 def roofline_for(res, bound=None):
     """Roofline of the dominant kernel (the longer of the two expert-GEMM kernels),
     its duration from the dispatch-stamped events of time_kernel.  bound None:
@@ -386,10 +441,13 @@ def roofline_for(res, bound=None):
     traffic = row.get("traffic")
     if bound == "hbm":
         achieved = d["bytes"] / sec / 1e9
+        copy = vendor_copy_gbps()
         return dict(kernel=name, bound="hbm", achieved=round(achieved, 1),
                     peak=HBM_PEAK / 1e9, unit="GB/s", frac=round(achieved * 1e9 / HBM_PEAK, 4),
                     traffic=traffic, algorithmic_bytes_per_launch=round(d["bytes"]),
-                    us_per_launch=round(d["us"], 2))
+                    us_per_launch=round(d["us"], 2),
+                    vendor_copy=dict(GBps=round(copy, 1), frac_of_peak=round(copy * 1e9 / HBM_PEAK, 4),
+                                     kernel_frac_of_copy=round(achieved / copy, 4)))
     peak = MFMA_F32_PEAK if res["wfmt"] == "f32" else MFMA_BF16_PEAK
     achieved = d["flops"] / sec / 1e12
     out = dict(kernel=name, bound="mfma", achieved=round(achieved, 1),
@@ -397,6 +455,15 @@ def roofline_for(res, bound=None):
                traffic=traffic, algorithmic_flops_per_launch=d["flops"], us_per_launch=round(d["us"], 2))
     if row.get("mfma_util") is not None:
         out["mfma_busy_pct_counters"] = row["mfma_util"]
+    sh = res.get("shape")
+    if sh and res["wfmt"] != "f32":
+        # the same multiply-adds as one dense fp16 GEMM: M = T k (token, expert) pairs
+        M = res["tokens"] * sh["k"]
+        N, K = (2 * sh["I"], sh["H"]) if k == "gate_up" else (sh["H"], sh["I"])
+        lib = vendor_gemm_tflops(M, N, K)
+        out["vendor_gemm"] = dict(shape_mnk=[M, N, K], TFLOPs=round(lib, 1),
+                                  frac_of_peak=round(lib * 1e12 / peak, 4),
+                                  kernel_frac_of_vendor=round(achieved / lib, 4))
     return out
 
 
