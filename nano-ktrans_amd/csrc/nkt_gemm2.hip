@@ -129,27 +129,94 @@ __device__ __forceinline__ void gemm2_sources(const GemmArgs& a, const TileItem&
 // XS (int8 gate_up on the fp16 matrix cores): acc holds sum (1024 + u) x / s
 // for the input rows scaled by s; it is rescaled per position and the code
 // offset is 1152 (1024 + 128).
+template <int kRT>
+struct EpiPre {
+  bool valid;
+  u32x2 s[kRT];
+};
+
+template <bool XS>
+__device__ __forceinline__ bool i8_row_terms(const GemmArgs& a, const int* srcl, float (&v)[16], float& xi) {
+  const int G = a.K / 128;
+  if (G > 16) return false;
+  const int tid = threadIdx.x;
+  if (tid < kBM) {
+    const float* xr = a.xsum + (int64_t)srcl[tid] * G;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) v[g] = g < G ? xr[g] : 0.f;
+    if (XS) xi = a.xinv[srcl[tid]];
+  }
+  return true;
+}
+
+__device__ __forceinline__ void i8_row_terms_store(int G, float* xtot_l, float* xinv_l, const float (&v)[16], float xi,
+                                                   bool xs) {
+  const int tid = threadIdx.x;
+  if (tid < kBM) {
+    float t = 0.f;
+#pragma unroll
+    for (int g = 0; g < 16; ++g)
+      if (g < G) t += v[g];
+    xtot_l[tid] = t;
+    if (xs) xinv_l[tid] = xi;
+  }
+}
+
+// LDS writes of this wave visible to its other lanes (no workgroup barrier)
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Stores one column tile's rows of 16-bit output through this wave's LDS
+// staging rows: lane l holds, for position l % 16, the four columns
+// 16 r + 4 (l / 16) .. + 3 of each of its NR row tiles (pk[r]); the 16
+// positions' NR x 16 contiguous columns then leave as 16-byte pieces, so a
+// store instruction writes whole row segments instead of 16 scattered
+// 8-byte pieces.  dst(p): the output row of position p (0..15) at the
+// wave's first column; positions >= n_rows are not stored.
+template <int NR, typename Dst>
+__device__ __forceinline__ void staged_rows_store(uint8_t* stage, const u32x2 (&pk)[NR], int lane, int n_rows, Dst dst) {
+  constexpr int RB = NR * 32, SB = RB + 16, LPP = RB / 16, PPI = 64 / LPP;
+  const int rq = 4 * (lane >> 4);
+#pragma unroll
+  for (int r = 0; r < NR; ++r) *(u32x2*)(stage + (lane & 15) * SB + (r * 16 + rq) * 2) = pk[r];
+  wave_lds_fence();
+#pragma unroll
+  for (int i = 0; i < 16 / PPI; ++i) {
+    const int pp = i * PPI + lane / LPP;
+    const u32x4 v = *(const u32x4*)(stage + pp * SB + (lane % LPP) * 16);
+    if (pp < n_rows) *(u32x4*)(dst(pp) + (lane % LPP) * 8) = v;
+  }
+  wave_lds_fence();  // read before the next column tile rewrites the rows
+}
+
 template <int WF, int PHASE, int kWaves, bool XS = false>
 __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[16 / kWaves][kCT], const int* srcl,
                                                const int* orow_l,
                                                float (*hpart)[kBM], float* xtot_l, float* xinv_l, const int* wrow,
-                                               const uint16_t* sexp, int row0, int rows, int slab) {
+                                               const uint16_t* sexp, int row0, int rows, int slab,
+                                               const EpiPre<16 / kWaves>* pre = nullptr, uint8_t* stage = nullptr) {
   constexpr int kRT = 16 / kWaves;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int G = a.K / 128;
   const int rq = 4 * (lane >> 4);
+  const bool have = pre && pre->valid;
+  auto scale_of = [&](int r) -> u32x2 { return have ? pre->s[r] : *(const u32x2*)(sexp + wrow[r] + rq); };
   if (WF == WF_I8) {
-    // the code offset: -128 x the row's K sum (group sums added in order)
-    if (tid < kBM) {
-      const float* xr = a.xsum + (int64_t)srcl[tid] * G;
-      float t = 0.f;
-      for (int g = 0; g < G; ++g) t += xr[g];
-      xtot_l[tid] = t;
-      if (XS) xinv_l[tid] = a.xinv[srcl[tid]];
+    if (!have) {
+      if (tid < kBM) {
+        const float* xr = a.xsum + (int64_t)srcl[tid] * G;
+        float t = 0.f;
+        for (int g = 0; g < G; ++g) t += xr[g];
+        xtot_l[tid] = t;
+        if (XS) xinv_l[tid] = a.xinv[srcl[tid]];
+      }
+      lds_barrier();
     }
-    __syncthreads();
 #pragma unroll
     for (int c = 0; c < kCT; ++c) {
       const float cv = (XS ? -1152.0f : -128.0f) * xtot_l[c * 16 + (lane & 15)];
@@ -170,14 +237,15 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[1
     if (WF == WF_I8) {
 #pragma unroll
       for (int r = 0; r < HR; ++r) {
-        sg[r] = bf16x4_to_f32(*(const u32x2*)(sexp + wrow[r] + rq));
-        su[r] = bf16x4_to_f32(*(const u32x2*)(sexp + wrow[r + HR] + rq));
+        sg[r] = bf16x4_to_f32(scale_of(r));
+        su[r] = bf16x4_to_f32(scale_of(r + HR));
       }
     }
 #pragma unroll
     for (int c = 0; c < kCT; ++c) {
       const int pl = c * 16 + (lane & 15);
       float part = 0.f;
+      u32x2 pk[HR];
 #pragma unroll
       for (int r = 0; r < HR; ++r) {
         f32x4 gv = acc[r][c], uv = acc[r + HR][c];
@@ -185,15 +253,21 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[1
           gv *= sg[r];
           uv *= su[r];
         }
-        u32x2 pk;
-        pk[0] = pack_bf16x2(silu_f32(gv[0]) * uv[0], silu_f32(gv[1]) * uv[1]);
-        pk[1] = pack_bf16x2(silu_f32(gv[2]) * uv[2], silu_f32(gv[3]) * uv[3]);
-        const f32x4 hb = bf16x4_to_f32(pk);
+        pk[r][0] = pack_bf16x2(silu_f32(gv[0]) * uv[0], silu_f32(gv[1]) * uv[1]);
+        pk[r][1] = pack_bf16x2(silu_f32(gv[2]) * uv[2], silu_f32(gv[3]) * uv[3]);
+        const f32x4 hb = bf16x4_to_f32(pk[r]);
         part += hb[0];
         part += hb[1];
         part += hb[2];
         part += hb[3];
-        if (pl < rows) *(u32x2*)((uint16_t*)a.out + (int64_t)(row0 + pl) * a.I + hcol0 + r * 16 + rq) = pk;
+      }
+      if (stage) {
+        staged_rows_store(stage, pk, lane, rows - c * 16,
+                          [&](int p) { return (uint16_t*)a.out + (int64_t)(row0 + c * 16 + p) * a.I + hcol0; });
+      } else if (pl < rows) {
+#pragma unroll
+        for (int r = 0; r < HR; ++r)
+          *(u32x2*)((uint16_t*)a.out + (int64_t)(row0 + pl) * a.I + hcol0 + r * 16 + rq) = pk[r];
       }
       // the 4 lanes holding one position's columns: fixed-order butterfly
       part += __shfl_xor(part, 16);
@@ -201,7 +275,7 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[1
       if (lane < 16) hpart[wave][pl] = part;
     }
     if (a.hsum) {
-      __syncthreads();
+      lds_barrier();
       if (tid < kBM && tid < rows) {
         float s = hpart[0][tid];
 #pragma unroll
@@ -221,7 +295,7 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[1
 #pragma unroll
     for (int r = 0; r < kRT; ++r) {
       f32x4 sr = f32x4{1.f, 1.f, 1.f, 1.f};
-      if (WF == WF_I8) sr = bf16x4_to_f32(*(const u32x2*)(sexp + wrow[r] + rq));
+      if (WF == WF_I8) sr = bf16x4_to_f32(scale_of(r));
 #pragma unroll
       for (int c = 0; c < kCT; ++c) {
         if (WF == WF_I8) acc[r][c] *= sr;
@@ -235,7 +309,7 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[1
       m[c] = fmaxf(m[c], __shfl_xor(m[c], 32));
       if (lane < 16) hpart[wave][c * 16 + lane] = m[c];
     }
-    __syncthreads();
+    lds_barrier();
     const int n_slabs = a.N / 256;
 #pragma unroll
     for (int c = 0; c < kCT; ++c) {
@@ -250,26 +324,29 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[1
         sh = min(max(15 - e, -126), 126);
       }
       const float sc = __builtin_ldexpf(1.0f, sh);
-      if (pl < rows) {
-        const int64_t orow = orow_l[pl];
-        if (wave == 0 && lane < 16) a.yscale[orow * n_slabs + slab] = __builtin_ldexpf(1.0f, -sh);
+      u32x2 pk[kRT];
 #pragma unroll
-        for (int r = 0; r < kRT; ++r) {
-          u32x2 pk;
+      for (int r = 0; r < kRT; ++r)
 #pragma unroll
-          for (int q = 0; q < 2; ++q) {
-            const _Float16 lo = (_Float16)(acc[r][c][2 * q] * sc), hi = (_Float16)(acc[r][c][2 * q + 1] * sc);
-            pk[q] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
-          }
-          *(u32x2*)(a.y16 + orow * a.N + wrow[r] + rq) = pk;
+        for (int q = 0; q < 2; ++q) {
+          const _Float16 lo = (_Float16)(acc[r][c][2 * q] * sc), hi = (_Float16)(acc[r][c][2 * q + 1] * sc);
+          pk[r][q] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
         }
+      if (pl < rows && wave == 0 && lane < 16) a.yscale[(int64_t)orow_l[pl] * n_slabs + slab] = __builtin_ldexpf(1.0f, -sh);
+      if (stage) {
+        staged_rows_store(stage, pk, lane, rows - c * 16,
+                          [&](int p) { return a.y16 + (int64_t)orow_l[c * 16 + p] * a.N + wrow[0]; });
+      } else if (pl < rows) {
+        const int64_t orow = orow_l[pl];
+#pragma unroll
+        for (int r = 0; r < kRT; ++r) *(u32x2*)(a.y16 + orow * a.N + wrow[r] + rq) = pk[r];
       }
     }
   } else {
 #pragma unroll
     for (int r = 0; r < kRT; ++r) {
       f32x4 sr = f32x4{1.f, 1.f, 1.f, 1.f};
-      if (WF == WF_I8) sr = bf16x4_to_f32(*(const u32x2*)(sexp + wrow[r] + rq));
+      if (WF == WF_I8) sr = bf16x4_to_f32(scale_of(r));
 #pragma unroll
       for (int c = 0; c < kCT; ++c) {
         const int pl = c * 16 + (lane & 15);
@@ -594,11 +671,19 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
     __builtin_amdgcn_sched_barrier(0);
   };
 
+  EpiPre<kRT> pre;
+  float rv[16], rxi = 0.f;
+  pre.valid = i8_row_terms<F16>(a, srcl, rv, rxi);
+  if (pre.valid) {
+#pragma unroll
+    for (int r = 0; r < kRT; ++r) pre.s[r] = *(const u32x2*)(sexp + wrow[r] + 4 * (lane >> 4));
+  }
   issue_tok(0, tb0);
   issue_tok(1, tb1);
   issue_w(0, w0);
   issue_tok(2, tb2);
   issue_w(1, w1);
+  if (pre.valid) i8_row_terms_store(a.K / 128, xtot_l, xinv_l, rv, rxi, F16);
   __asm__ volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0x0F7C);  // vmcnt(12): T0 landed
   lds_barrier();
@@ -622,7 +707,11 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
   if (rest >= 5) step(f0, f1, w1, w0, tb1, tb2, x + 4);
   wait_vmem();  // out-of-range loads past the last stage land before the LDS is reused
   __syncthreads();
-  gemm2_epilogue<WF_I8, PHASE, kWaves, F16>(a, acc, srcl, orow_l, hpart, xtot_l, xinv_l, wrow, sexp, it.row0, it.rows, it.slab);
+  // the epilogue's store staging: 16 rows of 144 B per wave in the token
+  // buffers, free once every wave has passed the barrier above
+  uint8_t* stage = wave < 3 ? tb0 + wave * 2304 : tb1;
+  gemm2_epilogue<WF_I8, PHASE, kWaves, F16>(a, acc, srcl, orow_l, hpart, xtot_l, xinv_l, wrow, sexp, it.row0, it.rows,
+                                            it.slab, &pre, stage);
 }
 
 // Per-row sums of each 128-wide K group of a bf16 matrix [rows, K] -> fp32

@@ -246,7 +246,8 @@ def test_stages_match_forward(gpu_device):
 
 
 @pytest.mark.parametrize("name,E,T", [("qwen15_int8_shared", None, 16), ("qwen3_int4", 32, 16),
-                                      ("qwen3_int8", 32, 512), ("mixtral_int4", None, 300)])
+                                      ("qwen3_int8", 32, 512), ("mixtral_int4", None, 300),
+                                      ("qwen3_int4", None, 8), ("mixtral_int4", None, 16)])
 def test_graph_replay_matches_eager(gpu_device, name, E, T):
     """The layer captured in a HIP graph (the shared expert, or in the prefill
     form gate_up's pre-pass over x, as a branch forked beside the routing)
@@ -418,7 +419,11 @@ def test_decode_outlier_channels(gpu_device, name, E, T):
 @pytest.mark.parametrize("name,E,T", [("qwen3_int4", 32, 16), ("mixtral_int4", None, 1), ("qwen3_int4", 32, 64),
                                       ("qwen3_int4", None, 1), ("qwen15_int8_shared", None, 1),
                                       ("qwen3_int4", None, 16), ("qwen3_int4", None, 4), ("mixtral_int4", None, 16),
-                                      ("qwen3_int8", 32, 16), ("qwen3_int8", 32, 512), ("qwen15_int8_shared", None, 1024)])
+                                      ("qwen3_int8", 32, 16), ("qwen3_int8", 32, 512), ("qwen15_int8_shared", None, 1024),
+                                      # 2 .. 16 tokens: routed inside the gate_up launch
+                                      ("qwen3_int4", None, 2), ("qwen3_int4", None, 8), ("qwen3_int4", 32, 13),
+                                      ("qwen15_int8_shared", None, 5), ("mixtral_int4", None, 3),
+                                      ("qwen3_int8", 32, 7)])
 def test_forward_matches_stages_and_leaves_sync_area_zero(gpu_device, name, E, T):
     """The layer equals route -> experts -> shared -> combine through the
     separate entry points bit for bit (at T = 1 the layer runs the down GEMV
