@@ -245,7 +245,6 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[1
     for (int c = 0; c < kCT; ++c) {
       const int pl = c * 16 + (lane & 15);
       float part = 0.f;
-      u32x2 pk[HR];
 #pragma unroll
       for (int r = 0; r < HR; ++r) {
         f32x4 gv = acc[r][c], uv = acc[r + HR][c];
@@ -253,21 +252,16 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[1
           gv *= sg[r];
           uv *= su[r];
         }
-        pk[r][0] = pack_bf16x2(silu_f32(gv[0]) * uv[0], silu_f32(gv[1]) * uv[1]);
-        pk[r][1] = pack_bf16x2(silu_f32(gv[2]) * uv[2], silu_f32(gv[3]) * uv[3]);
-        const f32x4 hb = bf16x4_to_f32(pk[r]);
+        u32x2 pk;
+        pk[0] = pack_bf16x2(silu_f32(gv[0]) * uv[0], silu_f32(gv[1]) * uv[1]);
+        pk[1] = pack_bf16x2(silu_f32(gv[2]) * uv[2], silu_f32(gv[3]) * uv[3]);
+        const f32x4 hb = bf16x4_to_f32(pk);
         part += hb[0];
         part += hb[1];
         part += hb[2];
         part += hb[3];
-      }
-      if (stage) {
-        staged_rows_store(stage, pk, lane, rows - c * 16,
-                          [&](int p) { return (uint16_t*)a.out + (int64_t)(row0 + c * 16 + p) * a.I + hcol0; });
-      } else if (pl < rows) {
-#pragma unroll
-        for (int r = 0; r < HR; ++r)
-          *(u32x2*)((uint16_t*)a.out + (int64_t)(row0 + pl) * a.I + hcol0 + r * 16 + rq) = pk[r];
+        // h goes out directly: staged like y below it measured ~2 % slower
+        if (pl < rows) *(u32x2*)((uint16_t*)a.out + (int64_t)(row0 + pl) * a.I + hcol0 + r * 16 + rq) = pk;
       }
       // the 4 lanes holding one position's columns: fixed-order butterfly
       part += __shfl_xor(part, 16);
@@ -707,11 +701,11 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
   if (rest >= 5) step(f0, f1, w1, w0, tb1, tb2, x + 4);
   wait_vmem();  // out-of-range loads past the last stage land before the LDS is reused
   __syncthreads();
-  // the epilogue's store staging: 16 rows of 144 B per wave in the token
+  // down's compact y staging: 16 rows of 144 B per wave in the token
   // buffers, free once every wave has passed the barrier above
   uint8_t* stage = wave < 3 ? tb0 + wave * 2304 : tb1;
   gemm2_epilogue<WF_I8, PHASE, kWaves, F16>(a, acc, srcl, orow_l, hpart, xtot_l, xinv_l, wrow, sexp, it.row0, it.rows,
-                                            it.slab, &pre, stage);
+                                            it.slab, &pre, PHASE == PHASE_DOWN ? stage : nullptr);
 }
 
 // Per-row sums of each 128-wide K group of a bf16 matrix [rows, K] -> fp32
