@@ -63,8 +63,10 @@ __global__ void __launch_bounds__(256) shared_gate_kernel(const void* __restrict
 // expert id through the thread's own LDS slots.
 // The end of one token's four output columns: + the offload backend's sum,
 // + gate x shared expert row, + the residual, one rounding, store.
-__device__ __forceinline__ void combine_tail(f32x4 acc, int t, int col, int H, const void* extra, const f32x4* vs,
-                                             float sg, const void* residual, void* out, int out_bf16) {
+// (shared: whether the gated shared expert row vs is added; by value, so
+// the row stays in registers)
+__device__ __forceinline__ void combine_tail(f32x4 acc, int t, int col, int H, const void* extra, bool shared,
+                                             f32x4 vs, float sg, const void* residual, void* out, int out_bf16) {
   const int64_t o = (int64_t)t * H + col;
   if (extra) {
     if (out_bf16)
@@ -72,7 +74,7 @@ __device__ __forceinline__ void combine_tail(f32x4 acc, int t, int col, int H, c
     else
       acc += *(const f32x4*)((const float*)extra + o);
   }
-  if (vs) acc += sg * *vs;
+  if (shared) acc += sg * vs;
   if (residual) {
     if (out_bf16)
       acc += bf16x4_to_f32(*(const u32x2*)((const uint16_t*)residual + o));
@@ -136,7 +138,7 @@ __global__ void __launch_bounds__(256) combine_kernel(
   f32x4 acc = terms[0][threadIdx.x];
 #pragma unroll
   for (int r = 1; r < K; ++r) acc += terms[r][threadIdx.x];
-  combine_tail(acc, t, 4 * c, H, extra, y_shared ? &vs : nullptr, sg, residual, out, out_bf16);
+  combine_tail(acc, t, 4 * c, H, extra, y_shared != nullptr, vs, sg, residual, out, out_bf16);
 }
 
 // The same sum over the prefill layer's compact y (fp16 rows, one fp32
@@ -201,7 +203,7 @@ __global__ void __launch_bounds__(256) combine16_kernel(
     const int col = 8 * c + 4 * half;
     f32x4 vs = zero;
     if (y_shared) vs = *(const f32x4*)(y_shared + (int64_t)t * H + col);
-    combine_tail(acc, t, col, H, extra, y_shared ? &vs : nullptr, sg, residual, out, out_bf16);
+    combine_tail(acc, t, col, H, extra, y_shared != nullptr, vs, sg, residual, out, out_bf16);
   }
 }
 
