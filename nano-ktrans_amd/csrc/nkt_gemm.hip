@@ -343,9 +343,15 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(GemmArgs a) {
 // ---------------------------------------------------------------------------
 // configuration table
 // ---------------------------------------------------------------------------
+// Tokens per expert (T k / E) up to which the decode form runs, from the
+// measured crossover of the two forms' layer times: int8 weights ~4 (the
+// prefill form's fp16 matrix cores win early), int4 ~16 (its decode form
+// streams half the bytes of int8 per MFMA operand), others 12.
+double decode_form_max_avg(int wf) { return wf == WF_I8 ? 4.0 : wf == WF_I4 ? 16.0 : 12.0; }
+
 int gemm_tile_m(int num_tokens, int topk, int num_experts, int wf, bool prefill_form) {
   const double avg = (double)num_tokens * topk / (double)num_experts;
-  if (avg <= 12.0) return 16;
+  if (avg <= decode_form_max_avg(wf)) return 16;
   if (wf != WF_F32 && prefill_form) return kPrefillTileM;
   if (avg <= 40.0) return 32;
   return 64;

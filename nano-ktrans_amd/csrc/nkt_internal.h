@@ -138,6 +138,9 @@ hipError_t launch_group_multi(const int32_t* ids, int T, int k, int E, int bm, i
                               int32_t* n_tiles, int32_t* tile_src, const uint8_t* resident,
                               hipStream_t stream);
 
+// Tokens per expert up to which the decode form runs (by weight format).
+double decode_form_max_avg(int wf);
+
 // Tile shapes: returns the token-tile height (BM) used for num_tokens:
 // 16 for decode-sized expert groups (gemv form), else kPrefillTileM when
 // the prefill form takes the shape (prefill_form), else 32 / 64 (the tiled

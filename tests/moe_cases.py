@@ -46,6 +46,12 @@ class MoEConfig:
     def act_dtype(self) -> torch.dtype:
         return torch.float32 if self.act == "f32" else torch.bfloat16
 
+    def decode_form(self, T: int) -> bool:
+        """Whether the library runs a batch of T tokens in its decode form:
+        up to 4 tokens per expert (T k / E) for int8 weights, 16 for int4 and
+        12 for the others."""
+        return T * self.k <= {"int8_per_channel": 4, "int4_g128": 16}.get(self.wfmt, 12) * self.E
+
 
 CONFIGS = {
     "tiny_mixtral_fp32": MoEConfig("tiny_mixtral_fp32", 256, 8, 2, 512, 0, True, True, "f32", "f32", 0),

@@ -69,12 +69,13 @@ def test_qwen3_int4_cut_experts(gpu_device, T):
     _check(layer, native, T)
 
 
-@pytest.mark.parametrize("T", [40, 48, 64])
+@pytest.mark.parametrize("T", [40, 48, 64, 72])
 def test_qwen3_int4_decode_form_multi_tile_experts(gpu_device, T):
-    """Four experts picked by every token.  T = 40, 48: the decode form
-    (T k <= 12 E): each hot expert holds T positions in ceil(T / 16) tiles, so
-    the tile records past an expert's first tile and its tiles' source columns
-    of rank >= 16 are used; T = 64 is past that form (prefill tiles)."""
+    """Four experts picked by every token.  T = 40 .. 64: the decode form
+    (T k <= 16 E for int4 weights): each hot expert holds T positions in
+    ceil(T / 16) tiles, so the tile records past an expert's first tile and
+    its tiles' source columns of rank >= 16 are used; T = 72 is past that form
+    (prefill tiles)."""
     announce(f"forward qwen3_int4 E=32 T={T} skewed")
     layer, native = _layer("qwen3_int4", E=32)
     bias = torch.zeros(32)
@@ -458,7 +459,7 @@ def test_forward_matches_stages_and_leaves_sync_area_zero(gpu_device, name, E, T
         native.shared(x)
     b = native.combine(T)
     torch.cuda.synchronize()
-    if T * k <= 12 * E:  # decode form
+    if layer.cfg.decode_form(T):
         assert torch.equal(a, b)
     else:
         ymax = y.abs().max().item()
