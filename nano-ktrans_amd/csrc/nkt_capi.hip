@@ -521,6 +521,18 @@ int do_combine(Handle* h, int T, void* out, void* ws, const WsLayout& L, hipStre
 
 constexpr int kSharedSideMinTokens = 8;
 
+// Chunks of the shared expert in the single-token layer's two launches
+// (Is / I of the routed shape; Qwen1.5-MoE: 5632 / 1408 = 4), or 0 when it
+// keeps launches of its own: no shared expert, Is not a multiple of I, more
+// than kMaxSharedChunks chunks, or too many positions for the down + combine
+// launch.
+int shared_chunks(const Handle* h) {
+  if (h->Is <= 0 || h->Is % h->I != 0) return 0;
+  const int c = h->Is / h->I;
+  if (c > kMaxSharedChunks || !down_combine_supported(h->wf, h->H, h->I, h->I, h->k + c)) return 0;
+  return c;
+}
+
 // Whether the shared expert can run on the side stream beside the routed
 // experts: its decode form (T up to kSharedDecodeMaxTokens) touches no
 // workspace region the routed experts use; the stream and events are made on
@@ -600,11 +612,20 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
   if (single) {
     int rc = NKT_OK;
     // routing inside gate_up pays when its workgroups run in about one round
-    // (Qwen3: 384, Qwen1.5-MoE: 352); with more (Mixtral-8x7B: 1792) every
-    // round would wait for the routing again, and the routing launch is cheaper
+    // (Qwen3: 384, Qwen1.5-MoE: 352 + 352 for the shared expert's chunks);
+    // with more (Mixtral-8x7B: 1792) every round would wait for the routing
+    // again, and the routing launch is cheaper
     constexpr int64_t kInlineRouteMaxWorkgroups = 1024;
-    if (logits && h->E <= 128 &&
-        gemv_workgroups(h->wf, PHASE_GATE_UP, 2 * h->I, h->H, h->I, L.max_tiles) <= kInlineRouteMaxWorkgroups) {
+    // a shared expert whose intermediate size is a multiple of the routed
+    // one's rides in both launches as Is / I chunks of the routed shape (no
+    // launches of its own); its gate comes from the gate_up launch
+    const int chunks = shared_chunks(h);
+    const int route_tiles = L.max_tiles > h->k + chunks ? L.max_tiles : h->k + chunks;
+    const bool inline_route =
+        logits && h->E <= 128 &&
+        gemv_workgroups(h->wf, PHASE_GATE_UP, 2 * h->I, h->H, h->I, route_tiles) <= kInlineRouteMaxWorkgroups;
+    const bool merged = inline_route && chunks > 0;
+    if (inline_route) {
       // K1 + K2 inside the gate_up launch (every workgroup routes the token)
       GemmArgs a = expert_args(h, PHASE_GATE_UP, false, x, ws, L, T);
       a.route_logits = logits;
@@ -621,14 +642,23 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
       a.ro_n_tiles = ws_ptr<int32_t>(ws, L, kWsNTiles);
       a.ro_tile_src = ws_ptr<int32_t>(ws, L, kWsTileSrc);
       a.ro_wpos = ws_ptr<float>(ws, L, kWsWpos);
-      if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, L.bm, L.max_tiles, st), "routing gate_up gemm", err,
+      if (merged) {
+        a.sh_chunks = chunks;
+        a.sh_I = h->Is;
+        a.sh_w = (const uint8_t*)h->w[NKT_SLOT_SHARED_GATE_UP];
+        a.sh_scales = (const uint16_t*)h->w[NKT_SLOT_SHARED_GATE_UP + 1];
+        a.sh_h = ws_ptr<void>(ws, L, NKT_WS_SHARED_H);
+        a.sh_gate_w = h->w[NKT_SLOT_SHARED_GATE];
+        a.sh_gate = ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE);
+      }
+      if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, L.bm, route_tiles, st), "routing gate_up gemm", err,
                      len))
         return NKT_ERR;
     } else {
       rc = route();
       if (rc == NKT_OK) rc = do_expert_phase(h, PHASE_GATE_UP, x, T, ws, L, st, err, len);
     }
-    if (rc == NKT_OK && h->Is > 0) rc = do_shared(h, x, T, ws, L, st, err, len);
+    if (rc == NKT_OK && h->Is > 0 && !merged) rc = do_shared(h, x, T, ws, L, st, err, len);
     if (rc != NKT_OK) return rc;
     if (!out) {
       set_err(err, len, "null output");
@@ -636,7 +666,14 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
     }
     GemmArgs b = expert_args(h, PHASE_DOWN, false, ws_ptr<void>(ws, L, NKT_WS_H), ws, L, T);
     const bool sh = h->Is > 0;
-    const CombineTail c{ws_ptr<float>(ws, L, kWsWpos), sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_Y) : nullptr,
+    if (merged) {
+      b.sh_chunks = chunks;
+      b.sh_I = h->Is;
+      b.sh_w = (const uint8_t*)h->w[NKT_SLOT_SHARED_DOWN];
+      b.sh_scales = (const uint16_t*)h->w[NKT_SLOT_SHARED_DOWN + 1];
+      b.sh_h = ws_ptr<void>(ws, L, NKT_WS_SHARED_H);
+    }
+    const CombineTail c{ws_ptr<float>(ws, L, kWsWpos), sh && !merged ? ws_ptr<float>(ws, L, NKT_WS_SHARED_Y) : nullptr,
                         sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE) : nullptr, residual, out};
     if (!check_hip(launch_down_combine(b, c, h->wf, h->k, st), "down + combine kernel", err, len)) return NKT_ERR;
     return NKT_OK;

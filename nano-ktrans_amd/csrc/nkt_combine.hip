@@ -22,38 +22,8 @@ __global__ void __launch_bounds__(256) shared_gate_kernel(const void* __restrict
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
-  float s = 0.f;
-  if (act_bf16 && H % 8 == 0) {
-    // 8 bf16 per lane per 16-byte load, four loads of x and of g in flight
-    const uint16_t* xr = (const uint16_t*)x + (int64_t)t * H;
-    const uint16_t* g = (const uint16_t*)gw;
-    for (int c0 = lane * 8; c0 < H; c0 += 4 * 512) {
-      u32x4 xv[4], gv[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int c = c0 + u * 512;
-        xv[u] = c < H ? *(const u32x4*)(xr + c) : u32x4{0u, 0u, 0u, 0u};
-        gv[u] = c < H ? *(const u32x4*)(g + c) : u32x4{0u, 0u, 0u, 0u};
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-          s += __uint_as_float(xv[u][h] << 16) * __uint_as_float(gv[u][h] << 16);
-          s += __uint_as_float(xv[u][h] & 0xffff0000u) * __uint_as_float(gv[u][h] & 0xffff0000u);
-        }
-    }
-  } else if (act_bf16) {
-    const uint16_t* xr = (const uint16_t*)x + (int64_t)t * H;
-    const uint16_t* g = (const uint16_t*)gw;
-    for (int i = lane; i < H; i += 64) s += bf16_bits_to_f32(xr[i]) * bf16_bits_to_f32(g[i]);
-  } else {
-    const float* xr = (const float*)x + (int64_t)t * H;
-    const float* g = (const float*)gw;
-    for (int i = lane; i < H; i += 64) s += xr[i] * g[i];
-  }
-  s = wave_sum_butterfly(s);
-  if (lane == 0) out[t] = 1.0f / (1.0f + __expf(-s));
+  const float v = shared_gate_value(x, gw, act_bf16, t, H, lane);
+  if (lane == 0) out[t] = v;
 }
 
 // One workgroup per (token, 1024-column slice); one thread per 4 columns.

@@ -306,4 +306,44 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// K4 for token t by one whole wave: sigmoid(x[t] . g) (fp32 products and
+// sums in a fixed order: each lane's strided share, then the butterfly), the
+// value in every lane.  The shared-gate kernel and the single-token layer's
+// gate_up launch both call it, so they give the same bits.
+__device__ __forceinline__ float shared_gate_value(const void* __restrict__ x, const void* __restrict__ gw,
+                                                   int act_bf16, int t, int H, int lane) {
+  float s = 0.f;
+  if (act_bf16 && H % 8 == 0) {
+    // 8 bf16 per lane per 16-byte load, four loads of x and of g in flight
+    const uint16_t* xr = (const uint16_t*)x + (int64_t)t * H;
+    const uint16_t* g = (const uint16_t*)gw;
+    for (int c0 = lane * 8; c0 < H; c0 += 4 * 512) {
+      u32x4 xv[4], gv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int c = c0 + u * 512;
+        xv[u] = c < H ? *(const u32x4*)(xr + c) : u32x4{0u, 0u, 0u, 0u};
+        gv[u] = c < H ? *(const u32x4*)(g + c) : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          s += __uint_as_float(xv[u][h] << 16) * __uint_as_float(gv[u][h] << 16);
+          s += __uint_as_float(xv[u][h] & 0xffff0000u) * __uint_as_float(gv[u][h] & 0xffff0000u);
+        }
+    }
+  } else if (act_bf16) {
+    const uint16_t* xr = (const uint16_t*)x + (int64_t)t * H;
+    const uint16_t* g = (const uint16_t*)gw;
+    for (int i = lane; i < H; i += 64) s += bf16_bits_to_f32(xr[i]) * bf16_bits_to_f32(g[i]);
+  } else {
+    const float* xr = (const float*)x + (int64_t)t * H;
+    const float* g = (const float*)gw;
+    for (int i = lane; i < H; i += 64) s += xr[i] * g[i];
+  }
+  s = wave_sum_butterfly(s);
+  return 1.0f / (1.0f + __expf(-s));
+}
+
 }  // namespace nkt

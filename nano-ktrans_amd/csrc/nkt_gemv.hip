@@ -230,10 +230,11 @@ __device__ __forceinline__ void mma_group(const WSlot<WF, NT>& r, const u32x4 (&
 // Output rows orow0 .. orow0 + 16 RT of the tile's positions: SwiGLU into h
 // (gate_up) or y / bf16 logits (down); int8 row scales applied here.
 // yrow: the output row of this lane's position (down).
+// up: gate_up's first up row (int8 scales); out: h or y.
 template <int WF, int PHASE, int RT>
 __device__ __forceinline__ void gemv_epilogue(const GemmArgs& a, const f32x4 (&acc)[PHASE == PHASE_GATE_UP ? 2 * RT : RT],
-                                              int rows, int row0, int orow0, const uint16_t* sexp, uint32_t lane,
-                                              int yrow) {
+                                              int rows, int row0, int orow0, const uint16_t* sexp, int up, void* out,
+                                              uint32_t lane, int yrow) {
   const int t_out = lane & 15;
   if (t_out >= rows) return;
   const int64_t pos = row0 + t_out;
@@ -245,7 +246,7 @@ __device__ __forceinline__ void gemv_epilogue(const GemmArgs& a, const f32x4 (&a
       f32x4 s1 = acc[RT + r];
       if (WF == WF_I8) {
         s0 *= bf16x4_to_f32(*(const u32x2*)(sexp + orow));
-        s1 *= bf16x4_to_f32(*(const u32x2*)(sexp + a.I + orow));
+        s1 *= bf16x4_to_f32(*(const u32x2*)(sexp + up + orow));
       }
       float h[4];
 #pragma unroll
@@ -253,7 +254,7 @@ __device__ __forceinline__ void gemv_epilogue(const GemmArgs& a, const f32x4 (&a
       u32x2 pk;
       pk[0] = pack_bf16x2(h[0], h[1]);
       pk[1] = pack_bf16x2(h[2], h[3]);
-      *(u32x2*)((uint16_t*)a.out + pos * a.I + orow) = pk;
+      *(u32x2*)((uint16_t*)out + pos * a.I + orow) = pk;
     } else {
       if (WF == WF_I8) s0 *= bf16x4_to_f32(*(const u32x2*)(sexp + orow));
       if (a.out_cols > 0) {
@@ -261,43 +262,76 @@ __device__ __forceinline__ void gemv_epilogue(const GemmArgs& a, const f32x4 (&a
 #pragma unroll
         for (int v = 0; v < 4; ++v)
           if (orow + v < a.out_cols)
-            ((uint16_t*)a.out)[pos * a.out_cols + orow + v] = (uint16_t)f32_to_bf16_bits(s0[v]);
+            ((uint16_t*)out)[pos * a.out_cols + orow + v] = (uint16_t)f32_to_bf16_bits(s0[v]);
       } else {
-        *(f32x4*)((float*)a.out + (int64_t)yrow * a.N + orow) = s0;
+        *(f32x4*)((float*)out + (int64_t)yrow * a.N + orow) = s0;
       }
     }
   }
+}
+
+// Where one tile's operands live: its weight blocks and scales (expert base),
+// gate_up's first up row, the K extent of a stored weight row (the stride of
+// its 16-row blocks) and the activation rows (row length K).
+struct TileSrc {
+  const uint8_t* w;
+  const uint16_t* s;
+  const uint8_t* x;
+  int up;
+  int kstride;
+};
+
+__device__ __forceinline__ TileSrc routed_src(const GemmArgs& a, int expert) {
+  return TileSrc{a.w + (int64_t)expert * a.w_expert_bytes, a.scales + (int64_t)expert * a.s_expert_elems,
+                 (const uint8_t*)a.in, a.I, a.K};
+}
+
+// Chunk c of the shared expert (GemmArgs::sh_chunks): gate_up rows [cI, cI + I)
+// of the gate and the up projection (sh_I rows apart); down the K range
+// [cI, cI + I) of every row, its input the same columns of the shared h.
+template <int WF, int PHASE>
+__device__ __forceinline__ TileSrc shared_chunk_src(const GemmArgs& a, int c) {
+  if (PHASE == PHASE_GATE_UP) {
+    const int r0 = c * a.I;
+    return TileSrc{a.sh_w + (int64_t)(r0 >> 4) * (a.K / block_k(WF)) * 1024,
+                   WF == WF_BF16 ? a.sh_scales : a.sh_scales + (int64_t)r0 * (WF == WF_I4 ? a.K / 128 : 1),
+                   (const uint8_t*)a.in, a.sh_I, a.K};
+  }
+  return TileSrc{a.sh_w + (int64_t)c * (a.K / block_k(WF)) * 1024,
+                 WF == WF_I4 ? a.sh_scales + (int64_t)c * (a.K / 128) * 16 : a.sh_scales,
+                 (const uint8_t*)a.sh_h + (int64_t)c * a.K * 2, 0, a.sh_I};
 }
 
 }  // namespace
 
 // One (tile, row set, K part) of the decode form: this wave's fp32 partial
 // sums of the row set's NT 16-row output tiles for the tile's positions,
-// columns = positions (16 at most, rows of them real).  expert: the tile's
-// expert; src / srcq: the input row of the lane's column in the full / quad
-// form; region: this wave's LDS staging area (NG KiB + the int4 scales).
+// columns = positions (16 at most, rows of them real).  ts: where the tile's
+// operands live; src / srcq: the input row of the lane's column in the full /
+// quad form; region: this wave's LDS staging area (NG KiB + the int4 scales).
 template <int WF, int PHASE, int RT, int S, int NG, int D, bool FULL>
-__device__ __forceinline__ void gemv_accumulate(const GemmArgs& a, int expert, int rows, int src, int srcq, int kpart,
-                                                int rowset, uint8_t* region, uint32_t lane,
+__device__ __forceinline__ void gemv_accumulate(const GemmArgs& a, const TileSrc& ts, int rows, int src, int srcq,
+                                                int kpart, int rowset, uint8_t* region, uint32_t lane,
                                                 f32x4 (&acc)[PHASE == PHASE_GATE_UP ? 2 * RT : RT]) {
   constexpr int NT = (PHASE == PHASE_GATE_UP) ? 2 * RT : RT;
   constexpr int kStageX = NG * 1024;
   const int col = lane & 15;
   const int G = a.K / 128;
-  const int NKB = a.K / block_k(WF);
-  const uint8_t* xbase = (const uint8_t*)a.in + 16 * (lane >> 4);
+  const int NKB = ts.kstride / block_k(WF);  // blocks per stored 16-row block
+  const int GS = ts.kstride / 128;           // scale groups per stored row
+  const uint8_t* xbase = ts.x + 16 * (lane >> 4);
 
-  const uint8_t* wexp = a.w + (int64_t)expert * a.w_expert_bytes;
-  const uint16_t* sexp = a.scales + (int64_t)expert * a.s_expert_elems;
+  const uint8_t* wexp = ts.w;
+  const uint16_t* sexp = ts.s;
   const int orow0 = rowset * RT * 16;  // first output row of the row set
   uint32_t rbo[NT], sbo[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    const int wrow = (PHASE == PHASE_GATE_UP) ? (t < RT ? orow0 + 16 * t : a.I + orow0 + 16 * (t - RT))
+    const int wrow = (PHASE == PHASE_GATE_UP) ? (t < RT ? orow0 + 16 * t : ts.up + orow0 + 16 * (t - RT))
                                               : orow0 + 16 * t;
     const uint32_t rb = (uint32_t)(wrow >> 4);
     rbo[t] = rb * (uint32_t)NKB * 1024u;
-    sbo[t] = rb * (uint32_t)G * 16u;
+    sbo[t] = rb * (uint32_t)GS * 16u;
   }
 
   // this wave's groups: kpart + S*i, i < n
@@ -330,7 +364,7 @@ __device__ __forceinline__ void gemv_accumulate(const GemmArgs& a, int expert, i
     __builtin_amdgcn_sched_barrier(0);
     if (rows <= 4) {
       // quad form: one load per group into LDS, the B operands built per step
-      const uint8_t* xq_row = (const uint8_t*)a.in + (int64_t)srcq * a.K * 2 + 64 * (col >> 2) + 16 * (lane >> 4);
+      const uint8_t* xq_row = ts.x + (int64_t)srcq * a.K * 2 + 64 * (col >> 2) + 16 * (lane >> 4);
 #pragma unroll
       for (int i = 0; i < NG; ++i) load16_to_lds(xq_row + (g_base + S * min(i, n_last)) * 256, region + i * 1024);
       if (WF == WF_I4 && lane < (uint32_t)(NT * NG * 8)) load4_to_lds(s_src, region + kStageX);
@@ -369,7 +403,7 @@ __device__ __forceinline__ void gemv_accumulate(const GemmArgs& a, int expert, i
     }
   } else if (rows <= 4) {
     // the ring with quad-form activations (one register load per group)
-    const uint8_t* xq_row = (const uint8_t*)a.in + (int64_t)srcq * a.K * 2 + 64 * (col >> 2) + 16 * (lane >> 4);
+    const uint8_t* xq_row = ts.x + (int64_t)srcq * a.K * 2 + 64 * (col >> 2) + 16 * (lane >> 4);
     WSlot<WF, NT> rw[D];
     u32x4 rx[D];
 #pragma unroll
@@ -469,9 +503,12 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
   // routed tiles: K2 writes every record up to the grid's max_tiles, those
   // past the last tile with no rows (no wait for the tile count)
   int expert, row0, rows;
+  int shc = -1;  // the shared-expert chunk this tile computes (ROUTE), else -1
   if (ROUTE) {
     // K1 on the token's logits by wave 0 (the same code and bits as the
-    // routing kernels); tile = position = rank of the expert id among the k
+    // routing kernels); tile = position = rank of the expert id among the k.
+    // Tiles k .. k + sh_chunks - 1 are the shared expert's chunks: no
+    // routing, and wave 0 of workgroup (0, k) first computes its gate.
     __shared__ float rsv[kMaxTopK];
     __shared__ int rsi[kMaxTopK];
     __shared__ int rids[kMaxTopK];
@@ -479,7 +516,12 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
     __shared__ int r_expert;
     const int k = a.topk;
     const bool first = blockIdx.x == 0 && tile == 0;
-    if (wave == 0) {
+    if (tile >= k && tile < k + a.sh_chunks) shc = tile - k;
+    if (wave == 0 && shc == 0 && blockIdx.x == 0) {
+      const float g = shared_gate_value(a.in, a.sh_gate_w, a.act_bf16, 0, a.K, (int)lane);
+      if (lane == 0) a.sh_gate[0] = g;
+    }
+    if (wave == 0 && shc < 0) {
       int id;
       float w;
       route_token<2, true>(a.route_logits, 0, a.route_E, k, a.route_flags, rsv, rsi, &id, &w);
@@ -522,9 +564,9 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
       }
       for (int i = threadIdx.x; i < a.ro_max_tiles * kTileSrcCols; i += nth) a.ro_tile_src[i] = 0;
     }
-    expert = r_expert;
-    row0 = tile;
-    rows = tile < k ? 1 : 0;
+    expert = shc < 0 ? r_expert : 0;
+    row0 = shc < 0 ? tile : 0;
+    rows = tile < k || shc >= 0 ? 1 : 0;
     src = 0;
     srcq = 0;
   } else if (a.n_tiles) {
@@ -554,10 +596,11 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
     src = row0 + (col < rows ? col : 0);
     srcq = row0 + ((col & 3) < rows ? (col & 3) : 0);
   }
-  const uint16_t* sexp = a.scales + (int64_t)expert * a.s_expert_elems;
+  const bool sh = ROUTE && shc >= 0;
+  const TileSrc ts = sh ? shared_chunk_src<WF, PHASE>(a, shc) : routed_src(a, expert);
   const int orow0 = rowset * RT * 16;  // first output row of the row set
   f32x4 acc[NT];
-  gemv_accumulate<WF, PHASE, RT, S, NG, D, FULL>(a, expert, rows, src, srcq, kpart, rowset,
+  gemv_accumulate<WF, PHASE, RT, S, NG, D, FULL>(a, ts, rows, src, srcq, kpart, rowset,
                                                  lds[__builtin_amdgcn_readfirstlane(wave)], lane, acc);
 
   if (S > 1 && !kLastReduces) {
@@ -598,7 +641,8 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
     }
   }
   if (!rs_ok) return;
-  gemv_epilogue<WF, PHASE, RT>(a, acc, rows, row0, orow0, sexp, lane, yrow);
+  gemv_epilogue<WF, PHASE, RT>(a, acc, rows, row0, orow0, ts.s, ts.up,
+                               sh ? (void*)((uint16_t*)a.sh_h + (int64_t)shc * a.I) : a.out, lane, yrow);
 }
 
 // ---------------------------------------------------------------------------
@@ -612,6 +656,11 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
 // + gate x shared expert row, + residual, one rounding -- the arithmetic of
 // the down GEMV followed by combine_kernel, so the same bits, with no y
 // round trip through HBM and no combine launch.
+// With a.sh_chunks = C > 0 the shared expert's down projection rides along
+// as C more positions n_pos .. n_pos + C - 1, chunk c the K range
+// [cI, cI + I) of the shared down rows (its input the same columns of the
+// shared h the gate_up launch wrote); its row is the C chunk rows added in
+// chunk order (each x the int8 row scale), times the gate that launch wrote.
 // ---------------------------------------------------------------------------
 constexpr int kDcWaves = 16;
 constexpr int kDcMaxItems = 64;  // positions x K parts
@@ -625,28 +674,33 @@ __global__ void __launch_bounds__(64 * kDcWaves) gemv_down_combine_kernel(GemmAr
   constexpr int kRegion = kStageX + kStageS > 16 ? kStageX + kStageS : 16;
   __shared__ __attribute__((aligned(16))) uint8_t lds[kDcWaves][kRegion];
   __shared__ f32x4 part[kDcMaxItems][4];  // [position x S + K part][lane / 16]: rows 4 (l / 16) .. + 3, column 0
-  __shared__ float wpos[kMaxTopK];              // routing weight of each position
-  __shared__ float spos[kMaxTopK][16];          // int8: row scales of each position's expert
+  __shared__ float wpos[kMaxTopK];                         // routing weight of each position
+  __shared__ float spos[kMaxTopK + kMaxSharedChunks][16];  // int8: row scales of each position's expert
   const uint32_t lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rowset = blockIdx.x;
-  const int n_items = n_pos * S;
+  const int n_sh = a.sh_chunks;
+  const int n_items = (n_pos + n_sh) * S;
   for (int q = wave; q < n_items; q += kDcWaves) {
     const int p = q / S, kpart = q % S;
+    const bool sh = p >= n_pos;
     // the combine's operands of position p ride with its K part 0: its
     // routing weight (in position order, independent of the tile record) and
     // the int8 row scales of its expert (issued with the weights)
     float wv = 0.f;
-    if (kpart == 0 && lane == 0) wv = c.wpos[p];
-    const int expert = a.tiles[4 * p];
+    if (!sh && kpart == 0 && lane == 0) wv = c.wpos[p];
+    const int expert = sh ? 0 : a.tiles[4 * p];
     float sc = 0.f;
     if (WF == WF_I8 && kpart == 0 && lane < 16u)
-      sc = bf16_bits_to_f32(a.scales[(int64_t)expert * a.s_expert_elems + rowset * 16 + lane]);
+      sc = bf16_bits_to_f32(sh ? a.sh_scales[rowset * 16 + lane]
+                               : a.scales[(int64_t)expert * a.s_expert_elems + rowset * 16 + lane]);
+    const TileSrc ts = sh ? shared_chunk_src<WF, PHASE_DOWN>(a, p - n_pos) : routed_src(a, expert);
+    const int src = sh ? 0 : p;
     f32x4 acc[NT];
-    gemv_accumulate<WF, PHASE_DOWN, RT, S, NG, D, FULL>(a, expert, 1, p, p, kpart, rowset, lds[wave], lane, acc);
+    gemv_accumulate<WF, PHASE_DOWN, RT, S, NG, D, FULL>(a, ts, 1, src, src, kpart, rowset, lds[wave], lane, acc);
     if ((lane & 15) == 0) part[q][lane >> 4] = acc[0];
     if (kpart == 0) {
-      if (lane == 0) wpos[p] = wv;
+      if (!sh && lane == 0) wpos[p] = wv;
       if (WF == WF_I8 && lane < 16u) spos[p][lane] = sc;
     }
   }
@@ -663,7 +717,19 @@ __global__ void __launch_bounds__(64 * kDcWaves) gemv_down_combine_kernel(GemmAr
     const float term = wpos[p] * y;
     acc = p == 0 ? term : acc + term;
   }
-  if (c.y_shared) acc += c.shared_gate[0] * c.y_shared[orow];
+  if (n_sh > 0) {
+    float ys = 0.f;
+    for (int j = 0; j < n_sh; ++j) {
+      const int p = n_pos + j;
+      float y = part[p * S][r >> 2][r & 3];
+      for (int kp = 1; kp < S; ++kp) y += part[p * S + kp][r >> 2][r & 3];
+      if (WF == WF_I8) y *= spos[p][r];
+      ys = j == 0 ? y : ys + y;
+    }
+    acc += c.shared_gate[0] * ys;
+  } else if (c.y_shared) {
+    acc += c.shared_gate[0] * c.y_shared[orow];
+  }
   if (c.residual) acc += bf16_bits_to_f32(((const uint16_t*)c.residual)[orow]);
   ((uint16_t*)c.out)[orow] = (uint16_t)f32_to_bf16_bits(acc);
 }
@@ -789,7 +855,7 @@ hipError_t launch_down_combine_wf(const GemmArgs& a, const CombineTail& c, int n
   if (S > 8) S = 8;
   if (S == 5 || S == 7) ++S;
   const int NG = (G + S - 1) / S;
-  if (n_pos * S > kDcMaxItems) return hipErrorInvalidValue;
+  if ((n_pos + a.sh_chunks) * S > kDcMaxItems) return hipErrorInvalidValue;
   switch (NG) {
     case 1:
       return launch_down_combine_ng<WF, 1>(a, c, n_pos, S, stream);
@@ -839,7 +905,8 @@ int64_t gemv_workgroups(int wf, int phase, int N, int K, int I, int max_tiles) {
 }
 
 bool down_combine_supported(int wf, int N, int K, int I, int n_pos) {
-  if (!gemv_supported(wf, PHASE_DOWN, N, K, I) || N % 16 != 0 || n_pos < 1) return false;
+  if (!gemv_supported(wf, PHASE_DOWN, N, K, I) || N % 16 != 0 || n_pos < 1 || n_pos > kMaxTopK + kMaxSharedChunks)
+    return false;
   const int G = K / 128;
   const int target = gemv_target_groups(wf);
   int S = (G + target - 1) / target;
@@ -849,8 +916,12 @@ bool down_combine_supported(int wf, int N, int K, int I, int n_pos) {
 }
 
 hipError_t launch_down_combine(const GemmArgs& a, const CombineTail& c, int wf, int n_pos, hipStream_t stream) {
-  if (!a.tiles || !c.wpos || !c.out) return hipErrorInvalidValue;
-  if (!down_combine_supported(wf, a.N, a.K, a.I, n_pos)) return hipErrorInvalidValue;
+  if (!a.tiles || !c.wpos || !c.out || n_pos > kMaxTopK) return hipErrorInvalidValue;
+  if (a.sh_chunks < 0 || a.sh_chunks > kMaxSharedChunks ||
+      (a.sh_chunks > 0 && (!a.sh_w || !a.sh_h || !c.shared_gate || (wf != WF_BF16 && !a.sh_scales) ||
+                           (int64_t)a.sh_chunks * a.K != a.sh_I)))
+    return hipErrorInvalidValue;
+  if (!down_combine_supported(wf, a.N, a.K, a.I, n_pos + a.sh_chunks)) return hipErrorInvalidValue;
   switch (wf) {
     case WF_BF16:
       return launch_down_combine_wf<WF_BF16>(a, c, n_pos, stream);
@@ -867,6 +938,13 @@ hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipS
                        const KernelTimer* tm) {
   if (max_tiles <= 0) return hipSuccess;
   if (a.perm && !a.tile_src) return hipErrorInvalidValue;  // gathered rows come from tile_src
+  // shared-expert chunks: only in the single-token gate_up that routes its
+  // token, with a tile slot for each of them
+  if (a.sh_chunks != 0 &&
+      (phase != PHASE_GATE_UP || !a.route_logits || a.sh_chunks < 0 || a.sh_chunks > kMaxSharedChunks ||
+       max_tiles < a.topk + a.sh_chunks || !a.sh_w || !a.sh_h || !a.sh_gate_w || !a.sh_gate ||
+       (wf != WF_BF16 && !a.sh_scales) || (int64_t)a.sh_chunks * a.I != a.sh_I))
+    return hipErrorInvalidValue;
   switch (wf) {
     case WF_BF16:
       return launch_gemv_wf<WF_BF16>(a, phase, max_tiles, stream, tm);

@@ -78,7 +78,25 @@ struct GemmArgs {
   int32_t* ro_n_tiles;
   int32_t* ro_tile_src;
   float* ro_wpos;
+  // single-token layer with a shared expert of intermediate size sh_I =
+  // sh_chunks x I (sh_chunks > 0): the shared expert rides in the routed
+  // launches as sh_chunks more tiles after the k routed ones.  Chunk c is
+  // an expert of the routed shape cut from the shared one: gate_up rows
+  // [cI, cI + I) of its gate and of its up projection (output h[0][cI ..]),
+  // down the K range [cI, cI + I) of its down projection (input the same h
+  // columns).  sh_w / sh_scales: the shared slot of this phase.  gate_up's
+  // workgroup (0, k) also writes sigmoid(x . sh_gate_w) to sh_gate[0].
+  int sh_chunks;
+  int sh_I;
+  const uint8_t* sh_w;
+  const uint16_t* sh_scales;
+  void* sh_h;  // bf16 [1, sh_I]
+  const void* sh_gate_w;
+  float* sh_gate;
 };
+
+// most chunks of a shared expert in the single-token layer's launches
+constexpr int kMaxSharedChunks = 8;
 
 enum GemmPhase : int { PHASE_GATE_UP = 0, PHASE_DOWN = 1 };
 

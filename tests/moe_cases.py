@@ -52,6 +52,12 @@ class MoEConfig:
         12 for the others."""
         return T * self.k <= {"int8_per_channel": 4, "int4_g128": 16}.get(self.wfmt, 12) * self.E
 
+    def shared_in_single_token_launches(self, T: int) -> bool:
+        """Whether the layer runs the shared expert inside the single-token
+        launches (as Is / I chunks of the routed shape) instead of its own."""
+        return (T == 1 and self.Is > 0 and self.Is % self.I == 0 and self.Is // self.I <= 8
+                and self.act == "bf16" and self.E <= 128)
+
 
 CONFIGS = {
     "tiny_mixtral_fp32": MoEConfig("tiny_mixtral_fp32", 256, 8, 2, 512, 0, True, True, "f32", "f32", 0),

@@ -219,6 +219,34 @@ def test_qwen15_shared_full(gpu_device, T):
     _check(layer, native, T)
 
 
+@pytest.mark.parametrize("name", ["qwen15_int8_shared", "small_int8_shared"])
+def test_single_token_shared_expert_in_routed_launches(gpu_device, name):
+    """One token, a shared expert whose intermediate size is a multiple of the
+    routed one's (Qwen1.5-MoE: 4 chunks of 1408, the small case: 1 chunk):
+    the shared expert runs as Is / I chunks inside the routing gate_up launch
+    and the down + combine launch.  The gate and h that launch leaves equal
+    the shared stage's (K4, then the shared expert's gate_up) bit for bit,
+    and the output matches the oracle."""
+    from nano_ktrans_amd import _native as N
+
+    layer, native = _layer(name)
+    assert layer.cfg.shared_in_single_token_launches(1)
+    Is = layer.cfg.Is
+    for seed in (71, 72, 73):
+        announce(f"single-token shared chunks {name} seed={seed}")
+        x, logits = build_inputs(layer, 1, seed=seed, device="cuda")
+        out = native.forward(x, logits).clone()
+        torch.cuda.synchronize()
+        gate_layer = native.region(1, N.WS_SHARED_GATE, torch.float32, (1,)).clone()
+        h_layer = native.region(1, N.WS_SHARED_H, torch.bfloat16, (1, Is)).clone()
+        gate_stage, _ = native.shared(x)
+        h_stage = native.region(1, N.WS_SHARED_H, torch.bfloat16, (1, Is))
+        torch.cuda.synchronize()
+        assert torch.equal(gate_layer, gate_stage)
+        assert torch.equal(h_layer, h_stage)
+        compare(out.float().cpu().numpy(), oracle_forward(layer, x, logits), layer.cfg)
+
+
 def test_forward_deterministic(gpu_device):
     announce("forward determinism qwen3_int4 E=32 T=64")
     layer, native = _layer("qwen3_int4", E=32)
@@ -246,8 +274,8 @@ def test_stages_match_forward(gpu_device):
     assert torch.allclose(gate.cpu(), ref_gate, rtol=1e-5, atol=1e-6)
 
 
-@pytest.mark.parametrize("name,E,T", [("qwen15_int8_shared", None, 16), ("qwen3_int4", 32, 16),
-                                      ("qwen3_int8", 32, 512), ("mixtral_int4", None, 300),
+@pytest.mark.parametrize("name,E,T", [("qwen15_int8_shared", None, 16), ("qwen15_int8_shared", None, 1),
+                                      ("qwen3_int4", 32, 16), ("qwen3_int8", 32, 512), ("mixtral_int4", None, 300),
                                       ("qwen3_int4", None, 8), ("mixtral_int4", None, 16)])
 def test_graph_replay_matches_eager(gpu_device, name, E, T):
     """The layer captured in a HIP graph (the shared expert, or in the prefill
@@ -424,13 +452,15 @@ def test_decode_outlier_channels(gpu_device, name, E, T):
                                       # 2 .. 16 tokens: routed inside the gate_up launch
                                       ("qwen3_int4", None, 2), ("qwen3_int4", None, 8), ("qwen3_int4", 32, 13),
                                       ("qwen15_int8_shared", None, 5), ("mixtral_int4", None, 3),
-                                      ("qwen3_int8", 32, 7)])
+                                      ("qwen3_int8", 32, 7), ("small_int8_shared", None, 1)])
 def test_forward_matches_stages_and_leaves_sync_area_zero(gpu_device, name, E, T):
     """The layer equals route -> experts -> shared -> combine through the
     separate entry points bit for bit (at T = 1 the layer runs the down GEMV
     and the combine as one launch) in the decode form; in the prefill form
     the layer keeps y as fp16 with a power-of-two scale per position and
-    256-column slab (the stages keep fp32 y), so every output element is
+    256-column slab (the stages keep fp32 y), and a single token's shared
+    expert runs as Is / I chunks whose down sums are added chunk by chunk
+    (the stage sums all of K at once), so there every output element is
     within 2^-12 of the largest |y| plus one bf16 step of the stages'.
     The layer leaves the workspace's sync area (the NKT_SYNC_AREA_BYTES
     before NKT_WS_TOPK_IDS) all zero."""
@@ -455,14 +485,15 @@ def test_forward_matches_stages_and_leaves_sync_area_zero(gpu_device, name, E, T
     for got, want in zip(routed, native.route(logits)):
         assert torch.equal(got, want)
     _, y = native.experts(x)
+    ymax = y.abs().max().item()
     if layer.cfg.Is:
-        native.shared(x)
+        _, ysh = native.shared(x)
+        ymax = max(ymax, ysh.abs().max().item())
     b = native.combine(T)
     torch.cuda.synchronize()
-    if layer.cfg.decode_form(T):
+    if layer.cfg.decode_form(T) and not layer.cfg.shared_in_single_token_launches(T):
         assert torch.equal(a, b)
     else:
-        ymax = y.abs().max().item()
         # the sums differ by at most 2^-12 ymax; each is then rounded to bf16
         # (one step is at most 2^-7 of the value)
         bound = 2.0 ** -12 * ymax + 2.0 ** -7 * torch.maximum(a.float().abs(), b.float().abs())
