@@ -76,12 +76,14 @@ extern "C" {
 #define NKT_WS_INV 5          /* int32 [T * k]  p -> pos */
 #define NKT_WS_H 6            /* act dtype [T*k, I]  SwiGLU activations by position */
 #define NKT_WS_Y 7            /* fp32 [T*k, H] expert outputs of nkt_moe_experts*: row = pair t*k + slot in the decode
-                                 form (T*k / E up to 4 for int8 weights, 16 for int4, 12 for the others), else position.  nkt_moe_forward* in the prefill form leaves it compact:
-                                 fp16 [T*k, H] by position, each 256-column slab of a row times a power of two, then
-                                 fp32 [T*k, H/256] with the inverse of each slab's factor */
+                                 form (T*k / E up to 4 for int8 weights, 16 for int4, 12 for the others), else
+                                 position.  nkt_moe_forward* in the prefill form leaves it compact: fp16 [T*k, H] by
+                                 position, each 256-column slab of a row times a power of two, then fp32 [T*k, H/256]
+                                 with the inverse of each slab's factor */
 #define NKT_WS_SHARED_GATE 8  /* fp32 [T] sigmoid(x . g)                              */
 #define NKT_WS_SHARED_H 9     /* act dtype [T, I_s]                                    */
-#define NKT_WS_SHARED_Y 10    /* fp32 [T, H]                                           */
+#define NKT_WS_SHARED_Y 10    /* fp32 [T, H]; not written by a single-token nkt_moe_forward* whose shared expert
+                                 runs inside the routed launches (I_s a multiple of I, bf16 activations) */
 #define NKT_WS_ROUTER_LOGITS 11 /* bf16 [T, E] router logits of the *_hidden entry points */
 #define NKT_WS_NORMED 12        /* bf16 [T, H] RMSNorm output of nkt_moe_forward_block    */
 #define NKT_WS_SYNC 13          /* uint32 [32]: word 31 is the status of the last single-launch router
