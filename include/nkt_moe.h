@@ -82,8 +82,9 @@ extern "C" {
                                  with the inverse of each slab's factor */
 #define NKT_WS_SHARED_GATE 8  /* fp32 [T] sigmoid(x . g)                              */
 #define NKT_WS_SHARED_H 9     /* act dtype [T, I_s]                                    */
-#define NKT_WS_SHARED_Y 10    /* fp32 [T, H]; not written by a single-token nkt_moe_forward* whose shared expert
-                                 runs inside the routed launches (I_s a multiple of I, bf16 activations) */
+#define NKT_WS_SHARED_Y 10    /* fp32 [T, H]; not written by a decode-form nkt_moe_forward* whose shared expert
+                                 runs inside the routed launches (I_s a multiple of I, I_s / I <= 8, bf16
+                                 activations, up to 256 tokens) */
 #define NKT_WS_ROUTER_LOGITS 11 /* bf16 [T, E] router logits of the *_hidden entry points */
 #define NKT_WS_NORMED 12        /* bf16 [T, H] RMSNorm output of nkt_moe_forward_block    */
 #define NKT_WS_SYNC 13          /* uint32 [32]: word 31 is the status of the last single-launch router

@@ -45,7 +45,8 @@ constexpr int kWsX16 = NKT_WS_NUM_REGIONS + 7;     // fp16 [T, H] scaled copy of
 constexpr int kWsXInv = NKT_WS_NUM_REGIONS + 8;    // fp32 [T] 1 / scale of each row of that copy
 constexpr int kWsTagged = NKT_WS_NUM_REGIONS + 9; // u64 [T, E / 2] tagged logit pairs (single-launch router)
 constexpr int kWsWpos = NKT_WS_NUM_REGIONS + 10;  // fp32 [T k] routing weights by position (fused route + group)
-constexpr int kWsAll = NKT_WS_NUM_REGIONS + 11;
+constexpr int kWsShChunkY = NKT_WS_NUM_REGIONS + 11;  // fp32 [Is / I, T, H] the shared expert's chunk rows
+constexpr int kWsAll = NKT_WS_NUM_REGIONS + 12;
 
 void set_err(char* err, size_t len, const char* fmt, ...) {
   if (!err || len == 0) return;
@@ -138,6 +139,20 @@ constexpr size_t kSyncStatusBytes = 256;
 constexpr size_t kSyncTaggedBytes = (size_t)kFusedRouteMaxTokens * kMaxExperts * 4;
 static_assert(kSyncStatusBytes + kSyncTaggedBytes == NKT_SYNC_AREA_BYTES, "the sync area's published size");
 
+// Chunks of the shared expert that ride in the routed experts' launches
+// when both run in the decode form: Is / I of the routed shape (Qwen1.5-MoE:
+// 5632 / 1408 = 4), each one more expert of every tile of 16 tokens, the
+// shared gate from gate_up and the chunk rows added by the combine; 0 (the
+// shared expert keeps launches of its own) without a shared expert, with Is
+// not a multiple of I, more than kMaxSharedChunks chunks or fp32
+// activations.
+int shared_chunk_count(const Handle* h, const WsLayout& L) {
+  if (h->Is <= 0 || h->Is % h->I != 0 || !h->act_bf16) return 0;
+  if (L.bm != kTileSrcCols || L.bm_shared != kTileSrcCols) return 0;
+  const int c = h->Is / h->I;
+  return c <= kMaxSharedChunks ? c : 0;
+}
+
 // int8 weights with bf16 activations: the prefill gate_up runs on the fp16
 // matrix cores from a power-of-two-scaled fp16 copy of x (H <= 4096)
 bool int8_f16_input(const Handle* h) { return h->wf == WF_I8 && h->act_bf16 && h->H <= 4096; }
@@ -181,6 +196,7 @@ WsLayout ws_layout(const Handle* h, int T) {
   sz[kWsX16] = x16 ? (size_t)T * h->H * 2 : 0;
   sz[kWsXInv] = x16 ? (size_t)T * 4 : 0;
   sz[kWsWpos] = P * 4;
+  sz[kWsShChunkY] = (size_t)shared_chunk_count(h, L) * T * h->H * 4;
   // The sync area first, the same size and place for every handle and
   // token count (status words, the router's tagged logit words): it must be
   // zero before a workspace's first use, every call of every handle leaves
@@ -444,16 +460,40 @@ float* yscale_ptr(const Handle* h, void* ws, const WsLayout& L, int T) {
   return (float*)(ws_ptr<uint8_t>(ws, L, NKT_WS_Y) + (size_t)T * h->k * h->H * 2);
 }
 
+// The shared expert's chunks in a routed launch of this phase
+// (GemmArgs::sh_chunks): tiles from tile0 on; gate_up also writes the gate.
+void set_shared_chunks(const Handle* h, GemmArgs& a, int phase, void* ws, const WsLayout& L, int T, int tile0,
+                       int chunks) {
+  const bool gu = phase == PHASE_GATE_UP;
+  a.sh_chunks = chunks;
+  a.sh_I = h->Is;
+  a.sh_tile0 = tile0;
+  a.sh_tokens = T;
+  a.sh_w = (const uint8_t*)h->w[gu ? NKT_SLOT_SHARED_GATE_UP : NKT_SLOT_SHARED_DOWN];
+  a.sh_scales = (const uint16_t*)h->w[(gu ? NKT_SLOT_SHARED_GATE_UP : NKT_SLOT_SHARED_DOWN) + 1];
+  a.sh_h = ws_ptr<void>(ws, L, NKT_WS_SHARED_H);
+  if (gu) {
+    a.sh_gate_w = h->w[NKT_SLOT_SHARED_GATE];
+    a.sh_gate = ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE);
+  } else {
+    a.sh_y = ws_ptr<float>(ws, L, kWsShChunkY);
+  }
+}
+
+// chunks > 0: the shared expert's chunks ride along (after the routed tiles)
 int do_expert_phase(Handle* h, int phase, const void* x, int T, void* ws, const WsLayout& L,
-                    hipStream_t st, char* err, size_t len, const KernelTimer* tm = nullptr, bool compact = false) {
+                    hipStream_t st, char* err, size_t len, const KernelTimer* tm = nullptr, bool compact = false,
+                    int chunks = 0) {
   if (phase == PHASE_GATE_UP && !x) {
     set_err(err, len, "null hidden_states");
     return NKT_ERR;
   }
-  if (!check_weights(h, false, err, len)) return NKT_ERR;
+  if (!check_weights(h, chunks > 0, err, len)) return NKT_ERR;
+  const int tiles = L.max_tiles + chunks * ((T + 15) / 16);
   if (phase == PHASE_GATE_UP) {
     GemmArgs a = expert_args(h, PHASE_GATE_UP, false, x, ws, L, T);
-    if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, L.bm, L.max_tiles, st, tm), "gate_up gemm", err, len))
+    if (chunks > 0) set_shared_chunks(h, a, PHASE_GATE_UP, ws, L, T, L.max_tiles, chunks);
+    if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, L.bm, tiles, st, tm), "gate_up gemm", err, len))
       return NKT_ERR;
   } else {
     GemmArgs b = expert_args(h, PHASE_DOWN, false, ws_ptr<void>(ws, L, NKT_WS_H), ws, L, T);
@@ -461,16 +501,17 @@ int do_expert_phase(Handle* h, int phase, const void* x, int T, void* ws, const 
       b.y16 = y16_ptr(ws, L);
       b.yscale = yscale_ptr(h, ws, L, T);
     }
-    if (!check_hip(launch_expert_gemm(h, b, PHASE_DOWN, L.bm, L.max_tiles, st, tm), "down gemm", err, len))
+    if (chunks > 0) set_shared_chunks(h, b, PHASE_DOWN, ws, L, T, L.max_tiles, chunks);
+    if (!check_hip(launch_expert_gemm(h, b, PHASE_DOWN, L.bm, tiles, st, tm), "down gemm", err, len))
       return NKT_ERR;
   }
   return NKT_OK;
 }
 
 int do_experts(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipStream_t st,
-               char* err, size_t len, bool compact = false) {
-  if (do_expert_phase(h, PHASE_GATE_UP, x, T, ws, L, st, err, len) != NKT_OK) return NKT_ERR;
-  return do_expert_phase(h, PHASE_DOWN, x, T, ws, L, st, err, len, nullptr, compact);
+               char* err, size_t len, bool compact = false, int chunks = 0) {
+  if (do_expert_phase(h, PHASE_GATE_UP, x, T, ws, L, st, err, len, nullptr, false, chunks) != NKT_OK) return NKT_ERR;
+  return do_expert_phase(h, PHASE_DOWN, x, T, ws, L, st, err, len, nullptr, compact, chunks);
 }
 
 int do_shared(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipStream_t st,
@@ -499,21 +540,24 @@ int do_shared(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipS
   return NKT_OK;
 }
 
+// chunks > 0: the shared expert's row is the sum of its chunk rows
 int do_combine(Handle* h, int T, void* out, void* ws, const WsLayout& L, hipStream_t st, char* err,
-               size_t len, const void* extra = nullptr, const void* residual = nullptr, bool compact = false) {
+               size_t len, const void* extra = nullptr, const void* residual = nullptr, bool compact = false,
+               int chunks = 0) {
   if (!out) {
     set_err(err, len, "null output");
     return NKT_ERR;
   }
   const bool sh = h->Is > 0;
   const bool y16 = compact && compact_y(h, L);
+  const float* ysh = !sh ? nullptr : chunks > 0 ? ws_ptr<float>(ws, L, kWsShChunkY) : ws_ptr<float>(ws, L, NKT_WS_SHARED_Y);
   if (!check_hip(launch_combine(ws_ptr<float>(ws, L, NKT_WS_Y), ws_ptr<int32_t>(ws, L, NKT_WS_TOPK_IDS),
                                 ws_ptr<float>(ws, L, NKT_WS_TOPK_WEIGHTS),
-                                y_pair_order(L) ? nullptr : ws_ptr<int32_t>(ws, L, NKT_WS_INV),
-                                sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_Y) : nullptr,
+                                y_pair_order(L) ? nullptr : ws_ptr<int32_t>(ws, L, NKT_WS_INV), ysh,
                                 sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE) : nullptr, h->resident,
                                 extra, residual, T, h->k, h->H, out, h->act_bf16, st,
-                                y16 ? y16_ptr(ws, L) : nullptr, y16 ? yscale_ptr(h, ws, L, T) : nullptr),
+                                y16 ? y16_ptr(ws, L) : nullptr, y16 ? yscale_ptr(h, ws, L, T) : nullptr,
+                                chunks > 0 ? chunks : 1),
                  "combine kernel", err, len))
     return NKT_ERR;
   return NKT_OK;
@@ -521,17 +565,6 @@ int do_combine(Handle* h, int T, void* out, void* ws, const WsLayout& L, hipStre
 
 constexpr int kSharedSideMinTokens = 8;
 
-// Chunks of the shared expert in the single-token layer's two launches
-// (Is / I of the routed shape; Qwen1.5-MoE: 5632 / 1408 = 4), or 0 when it
-// keeps launches of its own: no shared expert, Is not a multiple of I, more
-// than kMaxSharedChunks chunks, or too many positions for the down + combine
-// launch.
-int shared_chunks(const Handle* h) {
-  if (h->Is <= 0 || h->Is % h->I != 0) return 0;
-  const int c = h->Is / h->I;
-  if (c > kMaxSharedChunks || !down_combine_supported(h->wf, h->H, h->I, h->I, h->k + c)) return 0;
-  return c;
-}
 
 // Whether the shared expert can run on the side stream beside the routed
 // experts: its decode form (T up to kSharedDecodeMaxTokens) touches no
@@ -586,8 +619,16 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
     return NKT_ERR;
   }
   if (!check_weights(h, h->Is > 0, err, len)) return NKT_ERR;
+  // one token (decode form, every expert HBM-resident): the down GEMV and
+  // the combine run as one launch
+  const bool single = T == 1 && L.bm == kTileSrcCols && !h->resident && h->act_bf16 &&
+                      down_combine_supported(h->wf, h->H, h->I, h->I, h->k);
+  // the shared expert as chunks of the routed launches (no launches of its
+  // own); the single-token down + combine takes them as more positions
+  int chunks = shared_chunk_count(h, L);
+  if (single && chunks > 0 && !down_combine_supported(h->wf, h->H, h->I, h->I, h->k + chunks)) chunks = 0;
   std::unique_lock<std::mutex> lk(h->side_mu, std::defer_lock);
-  const bool side = allow_side && shared_side_ready(h, T, L, st);
+  const bool side = allow_side && chunks == 0 && shared_side_ready(h, T, L, st);
   if (side) {
     lk.lock();
     if (!check_hip(hipEventRecord(h->fork_ev, st), "fork event", err, len) ||
@@ -605,26 +646,18 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
       return NKT_ERR;
     }
   }
-  // one token (decode form, every expert HBM-resident): the down GEMV and
-  // the combine run as one launch after the shared expert
-  const bool single = T == 1 && L.bm == kTileSrcCols && !h->resident && h->act_bf16 &&
-                      down_combine_supported(h->wf, h->H, h->I, h->I, h->k);
   if (single) {
     int rc = NKT_OK;
     // routing inside gate_up pays when its workgroups run in about one round
     // (Qwen3: 384, Qwen1.5-MoE: 352 + 352 for the shared expert's chunks);
     // with more (Mixtral-8x7B: 1792) every round would wait for the routing
-    // again, and the routing launch is cheaper
+    // again, and the routing launch is cheaper.  The shared expert's chunk
+    // tiles follow the token's k tiles.
     constexpr int64_t kInlineRouteMaxWorkgroups = 1024;
-    // a shared expert whose intermediate size is a multiple of the routed
-    // one's rides in both launches as Is / I chunks of the routed shape (no
-    // launches of its own); its gate comes from the gate_up launch
-    const int chunks = shared_chunks(h);
     const int route_tiles = L.max_tiles > h->k + chunks ? L.max_tiles : h->k + chunks;
     const bool inline_route =
         logits && h->E <= 128 &&
         gemv_workgroups(h->wf, PHASE_GATE_UP, 2 * h->I, h->H, h->I, route_tiles) <= kInlineRouteMaxWorkgroups;
-    const bool merged = inline_route && chunks > 0;
     if (inline_route) {
       // K1 + K2 inside the gate_up launch (every workgroup routes the token)
       GemmArgs a = expert_args(h, PHASE_GATE_UP, false, x, ws, L, T);
@@ -642,23 +675,15 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
       a.ro_n_tiles = ws_ptr<int32_t>(ws, L, kWsNTiles);
       a.ro_tile_src = ws_ptr<int32_t>(ws, L, kWsTileSrc);
       a.ro_wpos = ws_ptr<float>(ws, L, kWsWpos);
-      if (merged) {
-        a.sh_chunks = chunks;
-        a.sh_I = h->Is;
-        a.sh_w = (const uint8_t*)h->w[NKT_SLOT_SHARED_GATE_UP];
-        a.sh_scales = (const uint16_t*)h->w[NKT_SLOT_SHARED_GATE_UP + 1];
-        a.sh_h = ws_ptr<void>(ws, L, NKT_WS_SHARED_H);
-        a.sh_gate_w = h->w[NKT_SLOT_SHARED_GATE];
-        a.sh_gate = ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE);
-      }
+      if (chunks > 0) set_shared_chunks(h, a, PHASE_GATE_UP, ws, L, T, h->k, chunks);
       if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, L.bm, route_tiles, st), "routing gate_up gemm", err,
                      len))
         return NKT_ERR;
     } else {
       rc = route();
-      if (rc == NKT_OK) rc = do_expert_phase(h, PHASE_GATE_UP, x, T, ws, L, st, err, len);
+      if (rc == NKT_OK) rc = do_expert_phase(h, PHASE_GATE_UP, x, T, ws, L, st, err, len, nullptr, false, chunks);
     }
-    if (rc == NKT_OK && h->Is > 0 && !merged) rc = do_shared(h, x, T, ws, L, st, err, len);
+    if (rc == NKT_OK && h->Is > 0 && chunks == 0) rc = do_shared(h, x, T, ws, L, st, err, len);
     if (rc != NKT_OK) return rc;
     if (!out) {
       set_err(err, len, "null output");
@@ -666,27 +691,22 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
     }
     GemmArgs b = expert_args(h, PHASE_DOWN, false, ws_ptr<void>(ws, L, NKT_WS_H), ws, L, T);
     const bool sh = h->Is > 0;
-    if (merged) {
-      b.sh_chunks = chunks;
-      b.sh_I = h->Is;
-      b.sh_w = (const uint8_t*)h->w[NKT_SLOT_SHARED_DOWN];
-      b.sh_scales = (const uint16_t*)h->w[NKT_SLOT_SHARED_DOWN + 1];
-      b.sh_h = ws_ptr<void>(ws, L, NKT_WS_SHARED_H);
-    }
-    const CombineTail c{ws_ptr<float>(ws, L, kWsWpos), sh && !merged ? ws_ptr<float>(ws, L, NKT_WS_SHARED_Y) : nullptr,
+    if (chunks > 0) set_shared_chunks(h, b, PHASE_DOWN, ws, L, T, 0, chunks);
+    const CombineTail c{ws_ptr<float>(ws, L, kWsWpos),
+                        sh && chunks == 0 ? ws_ptr<float>(ws, L, NKT_WS_SHARED_Y) : nullptr,
                         sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE) : nullptr, residual, out};
     if (!check_hip(launch_down_combine(b, c, h->wf, h->k, st), "down + combine kernel", err, len)) return NKT_ERR;
     return NKT_OK;
   }
   int rc = route();
-  if (rc == NKT_OK) rc = do_experts(h, x, T, ws, L, st, err, len, true);
-  if (rc == NKT_OK && !side && h->Is > 0) rc = do_shared(h, x, T, ws, L, st, err, len);
+  if (rc == NKT_OK) rc = do_experts(h, x, T, ws, L, st, err, len, true, chunks);
+  if (rc == NKT_OK && !side && h->Is > 0 && chunks == 0) rc = do_shared(h, x, T, ws, L, st, err, len);
   if (side) {
     const hipError_t we = hipStreamWaitEvent(st, h->join_ev, 0);
     if (rc == NKT_OK && !check_hip(we, "join wait", err, len)) rc = NKT_ERR;
   }
   if (rc != NKT_OK) return rc;
-  return do_combine(h, T, out, ws, L, st, err, len, nullptr, residual, true);
+  return do_combine(h, T, out, ws, L, st, err, len, nullptr, residual, true, chunks);
 }
 
 // ---------------------------------------------------------------------------

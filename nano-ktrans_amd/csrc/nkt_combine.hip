@@ -66,7 +66,7 @@ __global__ void __launch_bounds__(256) combine_kernel(
     const float* __restrict__ y, const int32_t* __restrict__ ids, const float* __restrict__ w,
     const int32_t* __restrict__ inv, const float* __restrict__ y_shared, const float* __restrict__ shared_gate, const uint8_t* __restrict__ resident,
     const void* __restrict__ extra, const void* __restrict__ residual, int num_tokens, int H,
-    void* __restrict__ out, int out_bf16) {
+    void* __restrict__ out, int out_bf16, int sh_rows) {
   __shared__ f32x4 terms[K][256];
   const int t = blockIdx.x;
   const int c = blockIdx.y * blockDim.x + threadIdx.x;  // float4 column index
@@ -82,7 +82,9 @@ __global__ void __launch_bounds__(256) combine_kernel(
   f32x4 vs = f32x4{0.f, 0.f, 0.f, 0.f};
   float sg = 0.f;
   if (y_shared) {
+    // the shared row (or its chunks' rows, added in chunk order)
     vs = *(const f32x4*)(y_shared + (int64_t)t * H + 4 * c);
+    for (int j = 1; j < sh_rows; ++j) vs += *(const f32x4*)(y_shared + ((int64_t)j * num_tokens + t) * H + 4 * c);
     sg = shared_gate[t];
   }
   int sid[K];
@@ -273,9 +275,10 @@ hipError_t launch_shared_gate(const void* x, const void* gate_w, int act_bf16, i
 
 hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, const int32_t* inv, const float* y_shared, const float* shared_gate, const uint8_t* resident,
                           const void* extra, const void* residual, int T, int k, int H, void* out,
-                          int out_bf16, hipStream_t stream, const uint16_t* y16, const float* yscale) {
+                          int out_bf16, hipStream_t stream, const uint16_t* y16, const float* yscale, int sh_rows) {
   if (T <= 0) return hipSuccess;
   if (y16 && (!yscale || H % 256 != 0)) return hipErrorInvalidValue;
+  if (sh_rows < 1 || sh_rows > kMaxSharedChunks || (sh_rows > 1 && (y16 || !y_shared))) return hipErrorInvalidValue;
   dim3 grid(T, (H / 4 + 255) / 256), grid16(T, (H / 8 + 255) / 256), block(256);
 #define NKT_COMBINE_CASE(KK)                                                                              \
   case KK:                                                                                                \
@@ -284,7 +287,7 @@ hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, co
                          shared_gate, resident, extra, residual, T, H, out, out_bf16);                    \
     else                                                                                                  \
       hipLaunchKernelGGL(combine_kernel<KK>, grid, block, 0, stream, y, ids, w, inv, y_shared, shared_gate,  \
-                         resident, extra, residual, T, H, out, out_bf16);                                 \
+                         resident, extra, residual, T, H, out, out_bf16, sh_rows);                        \
     break;
   switch (k) {
     NKT_COMBINE_CASE(1)

@@ -230,11 +230,11 @@ __device__ __forceinline__ void mma_group(const WSlot<WF, NT>& r, const u32x4 (&
 // Output rows orow0 .. orow0 + 16 RT of the tile's positions: SwiGLU into h
 // (gate_up) or y / bf16 logits (down); int8 row scales applied here.
 // yrow: the output row of this lane's position (down).
-// up: gate_up's first up row (int8 scales); out: h or y.
+// up: gate_up's first up row (int8 scales); out: h (rows hstride apart) or y.
 template <int WF, int PHASE, int RT>
 __device__ __forceinline__ void gemv_epilogue(const GemmArgs& a, const f32x4 (&acc)[PHASE == PHASE_GATE_UP ? 2 * RT : RT],
                                               int rows, int row0, int orow0, const uint16_t* sexp, int up, void* out,
-                                              uint32_t lane, int yrow) {
+                                              int hstride, uint32_t lane, int yrow) {
   const int t_out = lane & 15;
   if (t_out >= rows) return;
   const int64_t pos = row0 + t_out;
@@ -254,7 +254,7 @@ __device__ __forceinline__ void gemv_epilogue(const GemmArgs& a, const f32x4 (&a
       u32x2 pk;
       pk[0] = pack_bf16x2(h[0], h[1]);
       pk[1] = pack_bf16x2(h[2], h[3]);
-      *(u32x2*)((uint16_t*)out + pos * a.I + orow) = pk;
+      *(u32x2*)((uint16_t*)out + pos * hstride + orow) = pk;
     } else {
       if (WF == WF_I8) s0 *= bf16x4_to_f32(*(const u32x2*)(sexp + orow));
       if (a.out_cols > 0) {
@@ -272,22 +272,26 @@ __device__ __forceinline__ void gemv_epilogue(const GemmArgs& a, const f32x4 (&a
 
 // Where one tile's operands live: its weight blocks and scales (expert base),
 // gate_up's first up row, the K extent of a stored weight row (the stride of
-// its 16-row blocks) and the activation rows (row length K).
+// its 16-row blocks), the activation rows (xstride elements apart) and
+// gate_up's output row stride (h).
 struct TileSrc {
   const uint8_t* w;
   const uint16_t* s;
   const uint8_t* x;
   int up;
   int kstride;
+  int xstride;
+  int hstride;
 };
 
 __device__ __forceinline__ TileSrc routed_src(const GemmArgs& a, int expert) {
   return TileSrc{a.w + (int64_t)expert * a.w_expert_bytes, a.scales + (int64_t)expert * a.s_expert_elems,
-                 (const uint8_t*)a.in, a.I, a.K};
+                 (const uint8_t*)a.in, a.I, a.K, a.K, a.I};
 }
 
 // Chunk c of the shared expert (GemmArgs::sh_chunks): gate_up rows [cI, cI + I)
-// of the gate and the up projection (sh_I rows apart); down the K range
+// of the gate and the up projection (sh_I rows apart), output columns
+// [cI, cI + I) of the shared h rows (sh_I apart); down the K range
 // [cI, cI + I) of every row, its input the same columns of the shared h.
 template <int WF, int PHASE>
 __device__ __forceinline__ TileSrc shared_chunk_src(const GemmArgs& a, int c) {
@@ -295,11 +299,11 @@ __device__ __forceinline__ TileSrc shared_chunk_src(const GemmArgs& a, int c) {
     const int r0 = c * a.I;
     return TileSrc{a.sh_w + (int64_t)(r0 >> 4) * (a.K / block_k(WF)) * 1024,
                    WF == WF_BF16 ? a.sh_scales : a.sh_scales + (int64_t)r0 * (WF == WF_I4 ? a.K / 128 : 1),
-                   (const uint8_t*)a.in, a.sh_I, a.K};
+                   (const uint8_t*)a.in, a.sh_I, a.K, a.K, a.sh_I};
   }
   return TileSrc{a.sh_w + (int64_t)c * (a.K / block_k(WF)) * 1024,
                  WF == WF_I4 ? a.sh_scales + (int64_t)c * (a.K / 128) * 16 : a.sh_scales,
-                 (const uint8_t*)a.sh_h + (int64_t)c * a.K * 2, 0, a.sh_I};
+                 (const uint8_t*)a.sh_h + (int64_t)c * a.K * 2, 0, a.sh_I, a.sh_I, 0};
 }
 
 }  // namespace
@@ -364,7 +368,7 @@ __device__ __forceinline__ void gemv_accumulate(const GemmArgs& a, const TileSrc
     __builtin_amdgcn_sched_barrier(0);
     if (rows <= 4) {
       // quad form: one load per group into LDS, the B operands built per step
-      const uint8_t* xq_row = ts.x + (int64_t)srcq * a.K * 2 + 64 * (col >> 2) + 16 * (lane >> 4);
+      const uint8_t* xq_row = ts.x + (int64_t)srcq * ts.xstride * 2 + 64 * (col >> 2) + 16 * (lane >> 4);
 #pragma unroll
       for (int i = 0; i < NG; ++i) load16_to_lds(xq_row + (g_base + S * min(i, n_last)) * 256, region + i * 1024);
       if (WF == WF_I4 && lane < (uint32_t)(NT * NG * 8)) load4_to_lds(s_src, region + kStageX);
@@ -384,7 +388,7 @@ __device__ __forceinline__ void gemv_accumulate(const GemmArgs& a, const TileSrc
       }
     } else {
       // larger tiles: full B operands in registers, one group's at a time
-      const uint8_t* xrow = xbase + (int64_t)src * a.K * 2;
+      const uint8_t* xrow = xbase + (int64_t)src * ts.xstride * 2;
       if (WF == WF_I4 && lane < (uint32_t)(NT * NG * 8)) load4_to_lds(s_src, region + kStageX);
       const DqConst kdq = dq_const();
 #pragma unroll
@@ -403,7 +407,7 @@ __device__ __forceinline__ void gemv_accumulate(const GemmArgs& a, const TileSrc
     }
   } else if (rows <= 4) {
     // the ring with quad-form activations (one register load per group)
-    const uint8_t* xq_row = ts.x + (int64_t)srcq * a.K * 2 + 64 * (col >> 2) + 16 * (lane >> 4);
+    const uint8_t* xq_row = ts.x + (int64_t)srcq * ts.xstride * 2 + 64 * (col >> 2) + 16 * (lane >> 4);
     WSlot<WF, NT> rw[D];
     u32x4 rx[D];
 #pragma unroll
@@ -429,7 +433,7 @@ __device__ __forceinline__ void gemv_accumulate(const GemmArgs& a, const TileSrc
       }
     }
   } else {
-    const uint8_t* xrow = xbase + (int64_t)src * a.K * 2;
+    const uint8_t* xrow = xbase + (int64_t)src * ts.xstride * 2;
     RSlot<WF, NT> ring[D];
 #pragma unroll
     for (int d = 0; d < D; ++d) {
@@ -467,7 +471,10 @@ __host__ __device__ constexpr int gemv_rowsets_per_wg(int S) { return S == 1 ? 4
 // its groups through the D-deep ring.
 // ROUTE (gate_up, one token): the tile record comes from routing the
 // token inside the workgroup (GemmArgs::route_logits) instead of K2's list.
-template <int WF, int PHASE, int RT, int S, int NG, int D, bool FULL, bool ROUTE = false>
+// SH: tiles from GemmArgs::sh_tile0 on may be the shared expert's chunks
+// (a separate instance, so the routed-only launches carry none of it; the
+// ROUTE instance always may).
+template <int WF, int PHASE, int RT, int S, int NG, int D, bool FULL, bool ROUTE = false, bool SH = false>
 __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(GemmArgs a, int n_rowsets) {
   constexpr int P = gemv_rowsets_per_wg(S);
   constexpr int NT = (PHASE == PHASE_GATE_UP) ? 2 * RT : RT;
@@ -486,10 +493,13 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
   const int tile = blockIdx.y;
   const uint32_t lane = threadIdx.x & 63;
   const int col = lane & 15;
+  // a tile of the shared expert's chunks (GemmArgs::sh_chunks): no tile record
+  const int sh_j = tile - a.sh_tile0;
+  const bool sh_batch = SH && a.sh_chunks > 0 && sh_j >= 0;
   // the input row of the lane's column comes straight from the tile index, so
   // this load is issued first and waiting for it never waits for weights
   int src = 0, srcq = 0;
-  if (!ROUTE && a.tile_src) {
+  if (!ROUTE && a.tile_src && !sh_batch) {
     src = a.tile_src[tile * kTileSrcCols + col];
     srcq = a.tile_src[tile * kTileSrcCols + (col & 3)];
   }
@@ -502,13 +512,26 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
 
   // routed tiles: K2 writes every record up to the grid's max_tiles, those
   // past the last tile with no rows (no wait for the tile count)
-  int expert, row0, rows;
-  int shc = -1;  // the shared-expert chunk this tile computes (ROUTE), else -1
+  int expert = 0, row0 = 0, rows = 0;
+  int shc = -1;  // the shared-expert chunk of a shared tile, else -1
+  if (sh_batch) {
+    const int nT = (a.sh_tokens + 15) >> 4;
+    shc = sh_j / nT;
+    row0 = (sh_j - shc * nT) * 16;
+    rows = shc < a.sh_chunks ? min(16, a.sh_tokens - row0) : 0;
+    // K4 for chunk 0's tokens: wave 0 of the tile's workgroups, one token each
+    if (PHASE == PHASE_GATE_UP && shc == 0 && wave == 0) {
+      for (int t = blockIdx.x; t < rows; t += gridDim.x) {
+        const float g = shared_gate_value(a.in, a.sh_gate_w, a.act_bf16, row0 + t, a.K, (int)lane);
+        if (lane == 0) a.sh_gate[row0 + t] = g;
+      }
+    }
+  }
   if (ROUTE) {
     // K1 on the token's logits by wave 0 (the same code and bits as the
     // routing kernels); tile = position = rank of the expert id among the k.
-    // Tiles k .. k + sh_chunks - 1 are the shared expert's chunks: no
-    // routing, and wave 0 of workgroup (0, k) first computes its gate.
+    // Tiles k .. k + sh_chunks - 1 (sh_tile0 = k) are the shared expert's
+    // chunks: no routing, and wave 0 of workgroup (0, k) computes its gate.
     __shared__ float rsv[kMaxTopK];
     __shared__ int rsi[kMaxTopK];
     __shared__ int rids[kMaxTopK];
@@ -569,6 +592,8 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
     rows = tile < k || shc >= 0 ? 1 : 0;
     src = 0;
     srcq = 0;
+  } else if (sh_batch) {
+    // tokens row0 .. row0 + rows - 1 of x (gate_up) or of the shared h (down)
   } else if (a.n_tiles) {
     const int4 rec = *(const int4*)(a.tiles + 4 * tile);
     expert = rec.x;
@@ -591,12 +616,12 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
   }
   // down: the output row of this lane's position, loaded before the K loop
   int yrow = row0 + (lane & 15);
-  if (PHASE == PHASE_DOWN && a.out_rows && (int)(lane & 15) < rows) yrow = a.out_rows[yrow];
-  if (!ROUTE && !a.tile_src) {  // rows read in place
+  const bool sh = (ROUTE || SH) && shc >= 0;
+  if (PHASE == PHASE_DOWN && a.out_rows && !sh && (int)(lane & 15) < rows) yrow = a.out_rows[yrow];
+  if (!ROUTE && (!a.tile_src || sh)) {  // rows read in place
     src = row0 + (col < rows ? col : 0);
     srcq = row0 + ((col & 3) < rows ? (col & 3) : 0);
   }
-  const bool sh = ROUTE && shc >= 0;
   const TileSrc ts = sh ? shared_chunk_src<WF, PHASE>(a, shc) : routed_src(a, expert);
   const int orow0 = rowset * RT * 16;  // first output row of the row set
   f32x4 acc[NT];
@@ -641,8 +666,12 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
     }
   }
   if (!rs_ok) return;
-  gemv_epilogue<WF, PHASE, RT>(a, acc, rows, row0, orow0, ts.s, ts.up,
-                               sh ? (void*)((uint16_t*)a.sh_h + (int64_t)shc * a.I) : a.out, lane, yrow);
+  void* out = a.out;
+  if (sh)
+    out = PHASE == PHASE_GATE_UP ? (void*)((uint16_t*)a.sh_h + (int64_t)shc * a.I)
+                                 : (void*)(a.sh_y + (int64_t)shc * a.sh_tokens * a.N);
+  // (ROUTE: one token, position 0, so the h row stride does not matter)
+  gemv_epilogue<WF, PHASE, RT>(a, acc, rows, row0, orow0, ts.s, ts.up, out, ROUTE ? a.I : ts.hstride, lane, yrow);
 }
 
 // ---------------------------------------------------------------------------
@@ -756,6 +785,15 @@ hipError_t launch_gemv_s(const GemmArgs& a, int max_tiles, int n_rowsets, hipStr
                      n_rowsets);
       return hipGetLastError();
     }
+  }
+  if (a.sh_chunks > 0) {
+    if (full)
+      launch_timed(gemv_kernel<WF, PHASE, RT, S, NG, D, true, false, true>, grid, dim3(S * P * 64), 0, stream, tm,
+                   a, n_rowsets);
+    else
+      launch_timed(gemv_kernel<WF, PHASE, RT, S, NG, D, false, false, true>, grid, dim3(S * P * 64), 0, stream, tm,
+                   a, n_rowsets);
+    return hipGetLastError();
   }
   if (full)
     launch_timed(gemv_kernel<WF, PHASE, RT, S, NG, D, true>, grid, dim3(S * P * 64), 0, stream, tm, a, n_rowsets);
@@ -938,13 +976,17 @@ hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipS
                        const KernelTimer* tm) {
   if (max_tiles <= 0) return hipSuccess;
   if (a.perm && !a.tile_src) return hipErrorInvalidValue;  // gathered rows come from tile_src
-  // shared-expert chunks: only in the single-token gate_up that routes its
-  // token, with a tile slot for each of them
-  if (a.sh_chunks != 0 &&
-      (phase != PHASE_GATE_UP || !a.route_logits || a.sh_chunks < 0 || a.sh_chunks > kMaxSharedChunks ||
-       max_tiles < a.topk + a.sh_chunks || !a.sh_w || !a.sh_h || !a.sh_gate_w || !a.sh_gate ||
-       (wf != WF_BF16 && !a.sh_scales) || (int64_t)a.sh_chunks * a.I != a.sh_I))
-    return hipErrorInvalidValue;
+  // shared-expert chunks: a tile slot for each (chunk, 16-token tile), after
+  // the routed tiles (the single-token routing gate_up: right after its k)
+  if (a.sh_chunks != 0) {
+    const int64_t sh_tiles = (int64_t)a.sh_chunks * ((a.sh_tokens + 15) / 16);
+    if (a.sh_chunks < 0 || a.sh_chunks > kMaxSharedChunks || a.sh_tokens < 1 || a.sh_tile0 < 0 ||
+        a.sh_tile0 + sh_tiles > max_tiles || !a.act_bf16 || !a.sh_w || !a.sh_h ||
+        (wf != WF_BF16 && !a.sh_scales) || (int64_t)a.sh_chunks * a.I != a.sh_I ||
+        (a.route_logits && (a.sh_tokens != 1 || a.sh_tile0 != a.topk)))
+      return hipErrorInvalidValue;
+    if (phase == PHASE_GATE_UP ? (!a.sh_gate_w || !a.sh_gate) : !a.sh_y) return hipErrorInvalidValue;
+  }
   switch (wf) {
     case WF_BF16:
       return launch_gemv_wf<WF_BF16>(a, phase, max_tiles, stream, tm);

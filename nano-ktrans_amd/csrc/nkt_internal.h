@@ -78,21 +78,29 @@ struct GemmArgs {
   int32_t* ro_n_tiles;
   int32_t* ro_tile_src;
   float* ro_wpos;
-  // single-token layer with a shared expert of intermediate size sh_I =
+  // decode form with a shared expert of intermediate size sh_I =
   // sh_chunks x I (sh_chunks > 0): the shared expert rides in the routed
-  // launches as sh_chunks more tiles after the k routed ones.  Chunk c is
-  // an expert of the routed shape cut from the shared one: gate_up rows
-  // [cI, cI + I) of its gate and of its up projection (output h[0][cI ..]),
-  // down the K range [cI, cI + I) of its down projection (input the same h
-  // columns).  sh_w / sh_scales: the shared slot of this phase.  gate_up's
-  // workgroup (0, k) also writes sigmoid(x . sh_gate_w) to sh_gate[0].
+  // launches.  Chunk c is an expert of the routed shape cut from the shared
+  // one: gate_up rows [cI, cI + I) of its gate and of its up projection
+  // (output columns [cI, cI + I) of the shared h), down the K range
+  // [cI, cI + I) of its down projection (input the same shared h columns).
+  // Tile sh_tile0 + c * nT + j (nT = ceil(sh_tokens / 16)) is chunk c on
+  // tokens 16 j .. 16 j + 15, read in place.  sh_w / sh_scales: the shared
+  // slot of this phase.  gate_up: the token tiles of chunk 0 also write
+  // sigmoid(x . sh_gate_w) to sh_gate (K4); down: chunk c's rows go to
+  // sh_y + c sh_tokens H (fp32 [sh_tokens, H]), which the combine adds in
+  // chunk order.  The single-token down + combine launch takes the chunks
+  // as positions instead (GemmArgs::tiles then holds the k routed ones).
   int sh_chunks;
   int sh_I;
+  int sh_tile0;
+  int sh_tokens;
   const uint8_t* sh_w;
   const uint16_t* sh_scales;
-  void* sh_h;  // bf16 [1, sh_I]
+  void* sh_h;  // bf16 [sh_tokens, sh_I]
   const void* sh_gate_w;
   float* sh_gate;
+  float* sh_y;
 };
 
 // most chunks of a shared expert in the single-token layer's launches
@@ -223,11 +231,13 @@ hipError_t launch_shared_gate(const void* x, const void* gate_w, int act_bf16, i
 
 // y: the k expert rows of token t at rows t k .. t k + k - 1 (pair order,
 // inv == nullptr) or at rows inv[t k + j] (position order); y16 != nullptr:
-// the rows are the prefill down's compact y (fp16 + yscale), y unused
+// the rows are the prefill down's compact y (fp16 + yscale), y unused.
+// sh_rows > 1 (fp32 y only): the shared expert's row of token t is the sum
+// of y_shared rows j T + t, j < sh_rows, added in order (its chunks).
 hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, const int32_t* inv, const float* y_shared,
                           const float* shared_gate, const uint8_t* resident, const void* extra, const void* residual,
                           int T, int k, int H, void* out, int out_bf16, hipStream_t stream,
-                          const uint16_t* y16 = nullptr, const float* yscale = nullptr);
+                          const uint16_t* y16 = nullptr, const float* yscale = nullptr, int sh_rows = 1);
 
 // bf16 RMSNorm rows of x [T, H] with weight w [H] (decoder-block form)
 hipError_t launch_rmsnorm(const void* x, const void* w, float eps, int T, int H, void* out, hipStream_t stream);

@@ -52,11 +52,12 @@ class MoEConfig:
         12 for the others."""
         return T * self.k <= {"int8_per_channel": 4, "int4_g128": 16}.get(self.wfmt, 12) * self.E
 
-    def shared_in_single_token_launches(self, T: int) -> bool:
-        """Whether the layer runs the shared expert inside the single-token
-        launches (as Is / I chunks of the routed shape) instead of its own."""
-        return (T == 1 and self.Is > 0 and self.Is % self.I == 0 and self.Is // self.I <= 8
-                and self.act == "bf16" and self.E <= 128)
+    def shared_in_routed_launches(self, T: int) -> bool:
+        """Whether the layer runs the shared expert inside the routed experts'
+        decode-form launches (as Is / I chunks of the routed shape) instead of
+        launches of its own."""
+        return (self.Is > 0 and self.Is % self.I == 0 and self.Is // self.I <= 8 and self.act == "bf16"
+                and self.decode_form(T) and T <= 256)
 
 
 CONFIGS = {

@@ -219,28 +219,31 @@ def test_qwen15_shared_full(gpu_device, T):
     _check(layer, native, T)
 
 
-@pytest.mark.parametrize("name", ["qwen15_int8_shared", "small_int8_shared"])
-def test_single_token_shared_expert_in_routed_launches(gpu_device, name):
-    """One token, a shared expert whose intermediate size is a multiple of the
-    routed one's (Qwen1.5-MoE: 4 chunks of 1408, the small case: 1 chunk):
-    the shared expert runs as Is / I chunks inside the routing gate_up launch
-    and the down + combine launch.  The gate and h that launch leaves equal
-    the shared stage's (K4, then the shared expert's gate_up) bit for bit,
-    and the output matches the oracle."""
+@pytest.mark.parametrize("name,T", [("qwen15_int8_shared", 1), ("qwen15_int8_shared", 5),
+                                    ("qwen15_int8_shared", 16), ("qwen15_int8_shared", 60),
+                                    ("small_int8_shared", 1), ("small_int8_shared", 16)])
+def test_shared_expert_in_routed_launches(gpu_device, name, T):
+    """A decode-form batch and a shared expert whose intermediate size is a
+    multiple of the routed one's (Qwen1.5-MoE: 4 chunks of 1408, the small
+    case: 1 chunk): the shared expert runs as Is / I chunks inside the routed
+    gate_up and down launches (one token: the routing gate_up and the down +
+    combine launch).  The gate and h they leave equal the shared stage's (K4,
+    then the shared expert's gate_up) bit for bit, and the output matches the
+    oracle."""
     from nano_ktrans_amd import _native as N
 
     layer, native = _layer(name)
-    assert layer.cfg.shared_in_single_token_launches(1)
+    assert layer.cfg.shared_in_routed_launches(T)
     Is = layer.cfg.Is
-    for seed in (71, 72, 73):
-        announce(f"single-token shared chunks {name} seed={seed}")
-        x, logits = build_inputs(layer, 1, seed=seed, device="cuda")
+    for seed in (71, 72):
+        announce(f"shared chunks in the routed launches {name} T={T} seed={seed}")
+        x, logits = build_inputs(layer, T, seed=seed, device="cuda")
         out = native.forward(x, logits).clone()
         torch.cuda.synchronize()
-        gate_layer = native.region(1, N.WS_SHARED_GATE, torch.float32, (1,)).clone()
-        h_layer = native.region(1, N.WS_SHARED_H, torch.bfloat16, (1, Is)).clone()
+        gate_layer = native.region(T, N.WS_SHARED_GATE, torch.float32, (T,)).clone()
+        h_layer = native.region(T, N.WS_SHARED_H, torch.bfloat16, (T, Is)).clone()
         gate_stage, _ = native.shared(x)
-        h_stage = native.region(1, N.WS_SHARED_H, torch.bfloat16, (1, Is))
+        h_stage = native.region(T, N.WS_SHARED_H, torch.bfloat16, (T, Is))
         torch.cuda.synchronize()
         assert torch.equal(gate_layer, gate_stage)
         assert torch.equal(h_layer, h_stage)
@@ -258,7 +261,10 @@ def test_forward_deterministic(gpu_device):
 
 
 def test_stages_match_forward(gpu_device):
-    """route -> experts -> shared -> combine through the separate entry points equals forward."""
+    """route -> experts -> shared -> combine through the separate entry points
+    equals forward, up to the order of the shared expert's down sums (the
+    layer adds its Is / I chunks one by one): within 2^-12 of the largest
+    |y_shared| plus one bf16 step."""
     announce("stages vs forward qwen15_int8_shared T=16")
     layer, native = _layer("qwen15_int8_shared")
     x, logits = build_inputs(layer, 16, seed=9, device="cuda")
@@ -268,7 +274,8 @@ def test_stages_match_forward(gpu_device):
     gate, ysh = native.shared(x)
     b = native.combine(16)
     torch.cuda.synchronize()
-    assert torch.equal(a, b)
+    bound = 2.0 ** -12 * ysh.abs().max().item() + 2.0 ** -7 * torch.maximum(a.float().abs(), b.float().abs())
+    assert bool(((a.float() - b.float()).abs() <= bound).all())
     # K4 alone: sigmoid(x . g)
     ref_gate = torch.sigmoid(x.float().cpu() @ layer.shared_gate.cpu())
     assert torch.allclose(gate.cpu(), ref_gate, rtol=1e-5, atol=1e-6)
@@ -458,10 +465,10 @@ def test_forward_matches_stages_and_leaves_sync_area_zero(gpu_device, name, E, T
     separate entry points bit for bit (at T = 1 the layer runs the down GEMV
     and the combine as one launch) in the decode form; in the prefill form
     the layer keeps y as fp16 with a power-of-two scale per position and
-    256-column slab (the stages keep fp32 y), and a single token's shared
-    expert runs as Is / I chunks whose down sums are added chunk by chunk
-    (the stage sums all of K at once), so there every output element is
-    within 2^-12 of the largest |y| plus one bf16 step of the stages'.
+    256-column slab (the stages keep fp32 y), and a decode-form layer runs
+    the shared expert as Is / I chunks whose down sums are added chunk by
+    chunk (the stage sums all of K at once), so there every output element
+    is within 2^-12 of the largest |y| plus one bf16 step of the stages'.
     The layer leaves the workspace's sync area (the NKT_SYNC_AREA_BYTES
     before NKT_WS_TOPK_IDS) all zero."""
     import ctypes
@@ -491,7 +498,7 @@ def test_forward_matches_stages_and_leaves_sync_area_zero(gpu_device, name, E, T
         ymax = max(ymax, ysh.abs().max().item())
     b = native.combine(T)
     torch.cuda.synchronize()
-    if layer.cfg.decode_form(T) and not layer.cfg.shared_in_single_token_launches(T):
+    if layer.cfg.decode_form(T) and not layer.cfg.shared_in_routed_launches(T):
         assert torch.equal(a, b)
     else:
         # the sums differ by at most 2^-12 ymax; each is then rounded to bf16
