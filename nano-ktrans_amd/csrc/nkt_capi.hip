@@ -321,8 +321,12 @@ GemmArgs expert_args(const Handle* h, int phase, bool shared, const void* in, vo
   return a;
 }
 
+// prep (nullable): the int8 gate_up's fp16 input to make in the routing
+// launch when routing takes the large-batch path (*prep_done says whether it
+// did)
 int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, hipStream_t st,
-             char* err, size_t len) {
+             char* err, size_t len, const GemmArgs* prep = nullptr, bool* prep_done = nullptr) {
+  if (prep_done) *prep_done = false;
   if (!logits) {
     set_err(err, len, "null router_logits");
     return NKT_ERR;
@@ -344,9 +348,16 @@ int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, 
       return NKT_ERR;
     return NKT_OK;
   }
-  if (!check_hip(launch_route(logits, h->act_bf16, T, h->E, h->k, h->flags, ids, wts, st),
-                 "route kernel", err, len))
+  if (prep && h->act_bf16) {
+    if (!check_hip(launch_route_prep_f16(logits, T, h->E, h->k, h->flags, ids, wts, prep->in, T, prep->K,
+                                         const_cast<float*>(prep->xsum), prep->in16, prep->xinv, st),
+                   "route + input kernel", err, len))
+      return NKT_ERR;
+    if (prep_done) *prep_done = true;
+  } else if (!check_hip(launch_route(logits, h->act_bf16, T, h->E, h->k, h->flags, ids, wts, st),
+                        "route kernel", err, len)) {
     return NKT_ERR;
+  }
   if (!check_hip(launch_group_multi(ids, T, h->k, h->E, L.bm, L.max_tiles, ws_ptr<int32_t>(ws, L, kWsHist), counts,
                                     offsets, perm, inv, tiles, n_tiles, tile_src, h->resident, st),
                  "group kernels", err, len))
@@ -425,8 +436,10 @@ int do_route_hidden(Handle* h, const void* x, int T, void* ws, const WsLayout& L
 // positions, the prefill form for its tiles, the tiled form otherwise.
 // The prefill form's gate_up first sums the activations per 128-wide group
 // (int formats; the down projection reads the sums gate_up writes).
+// prep_done: the int8 gate_up's fp16 input copy and group sums are already
+// made (by the routing launch).
 hipError_t launch_expert_gemm(const Handle* h, const GemmArgs& a, int phase, int bm, int tiles,
-                              hipStream_t st, const KernelTimer* tm = nullptr) {
+                              hipStream_t st, const KernelTimer* tm = nullptr, bool prep_done = false) {
   if (bm == 16 && gemv_supported(h->wf, phase, a.N, a.K, a.I)) return launch_gemv(a, h->wf, phase, tiles, st, tm);
   if (bm == kPrefillTileM && gemm2_supported(h->wf, phase, a.N, a.K, a.I)) {
     GemmArgs b = a;
@@ -434,7 +447,7 @@ hipError_t launch_expert_gemm(const Handle* h, const GemmArgs& a, int phase, int
       const int rows_in = a.perm ? a.num_rows / a.topk : a.num_rows;
       hipError_t e;
       if (a.in16 && a.xinv && gemm2_i8_pipeline(a, h->wf)) {
-        e = launch_prep_f16(a.in, rows_in, a.K, const_cast<float*>(a.xsum), a.in16, a.xinv, st);
+        e = prep_done ? hipSuccess : launch_prep_f16(a.in, rows_in, a.K, const_cast<float*>(a.xsum), a.in16, a.xinv, st);
         b.in = a.in16;
       } else {
         e = launch_group_sums(a.in, rows_in, a.K, const_cast<float*>(a.xsum), st);
@@ -483,7 +496,7 @@ void set_shared_chunks(const Handle* h, GemmArgs& a, int phase, void* ws, const 
 // chunks > 0: the shared expert's chunks ride along (after the routed tiles)
 int do_expert_phase(Handle* h, int phase, const void* x, int T, void* ws, const WsLayout& L,
                     hipStream_t st, char* err, size_t len, const KernelTimer* tm = nullptr, bool compact = false,
-                    int chunks = 0) {
+                    int chunks = 0, bool prep_done = false) {
   if (phase == PHASE_GATE_UP && !x) {
     set_err(err, len, "null hidden_states");
     return NKT_ERR;
@@ -493,7 +506,7 @@ int do_expert_phase(Handle* h, int phase, const void* x, int T, void* ws, const 
   if (phase == PHASE_GATE_UP) {
     GemmArgs a = expert_args(h, PHASE_GATE_UP, false, x, ws, L, T);
     if (chunks > 0) set_shared_chunks(h, a, PHASE_GATE_UP, ws, L, T, L.max_tiles, chunks);
-    if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, L.bm, tiles, st, tm), "gate_up gemm", err, len))
+    if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, L.bm, tiles, st, tm, prep_done), "gate_up gemm", err, len))
       return NKT_ERR;
   } else {
     GemmArgs b = expert_args(h, PHASE_DOWN, false, ws_ptr<void>(ws, L, NKT_WS_H), ws, L, T);
@@ -509,13 +522,14 @@ int do_expert_phase(Handle* h, int phase, const void* x, int T, void* ws, const 
 }
 
 int do_experts(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipStream_t st,
-               char* err, size_t len, bool compact = false, int chunks = 0) {
-  if (do_expert_phase(h, PHASE_GATE_UP, x, T, ws, L, st, err, len, nullptr, false, chunks) != NKT_OK) return NKT_ERR;
+               char* err, size_t len, bool compact = false, int chunks = 0, bool prep_done = false) {
+  if (do_expert_phase(h, PHASE_GATE_UP, x, T, ws, L, st, err, len, nullptr, false, chunks, prep_done) != NKT_OK)
+    return NKT_ERR;
   return do_expert_phase(h, PHASE_DOWN, x, T, ws, L, st, err, len, nullptr, compact, chunks);
 }
 
 int do_shared(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipStream_t st,
-              char* err, size_t len) {
+              char* err, size_t len, bool prep_done = false) {
   if (h->Is <= 0) {
     set_err(err, len, "handle has no shared expert");
     return NKT_ERR;
@@ -532,7 +546,8 @@ int do_shared(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipS
   const int bm = L.bm_shared;
   const int tiles = (T + bm - 1) / bm;
   GemmArgs a = expert_args(h, PHASE_GATE_UP, true, x, ws, L, T);
-  if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, bm, tiles, st), "shared gate_up gemm", err, len))
+  if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, bm, tiles, st, nullptr, prep_done), "shared gate_up gemm",
+                 err, len))
     return NKT_ERR;
   GemmArgs b = expert_args(h, PHASE_DOWN, true, ws_ptr<void>(ws, L, NKT_WS_SHARED_H), ws, L, T);
   if (!check_hip(launch_expert_gemm(h, b, PHASE_DOWN, bm, tiles, st), "shared down gemm", err, len))
@@ -698,9 +713,15 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
     if (!check_hip(launch_down_combine(b, c, h->wf, h->k, st), "down + combine kernel", err, len)) return NKT_ERR;
     return NKT_OK;
   }
-  int rc = route();
-  if (rc == NKT_OK) rc = do_experts(h, x, T, ws, L, st, err, len, true, chunks);
-  if (rc == NKT_OK && !side && h->Is > 0 && chunks == 0) rc = do_shared(h, x, T, ws, L, st, err, len);
+  // given logits and the int8 prefill gate_up on the fp16 matrix cores: its
+  // input copy is made in the routing launch
+  const GemmArgs g = expert_args(h, PHASE_GATE_UP, false, x, ws, L, T);
+  const bool prep_in_route = logits && L.bm == kPrefillTileM && g.in16 && g.xinv &&
+                             gemm2_supported(h->wf, PHASE_GATE_UP, g.N, g.K, g.I) && gemm2_i8_pipeline(g, h->wf);
+  bool prep_done = false;
+  int rc = prep_in_route ? do_route(h, logits, T, ws, L, st, err, len, &g, &prep_done) : route();
+  if (rc == NKT_OK) rc = do_experts(h, x, T, ws, L, st, err, len, true, chunks, prep_done);
+  if (rc == NKT_OK && !side && h->Is > 0 && chunks == 0) rc = do_shared(h, x, T, ws, L, st, err, len, prep_done);
   if (side) {
     const hipError_t we = hipStreamWaitEvent(st, h->join_ev, 0);
     if (rc == NKT_OK && !check_hip(we, "join wait", err, len)) rc = NKT_ERR;

@@ -36,6 +36,7 @@
 // which the down projection consumes.
 #include "nkt_common.h"
 #include "nkt_internal.h"
+#include "nkt_route_token.h"
 
 namespace nkt {
 
@@ -934,11 +935,12 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
 // [2^14, 2^15), and every bf16 value down to 2^-32 of it is exact in fp16
 // (normal down to 2^-14, subnormal with 8 significant bits down to 2^-17).
 // xinv = 1 / s.  Lane l holds 8 values of group 4c + l / 16 per chunk c.
+// block: this launch's index of the workgroup (four rows).
 template <int NCH>
-__global__ void __launch_bounds__(256) prep_f16_kernel(const uint16_t* __restrict__ x, int rows, int K,
-                                                       float* __restrict__ sums, uint16_t* __restrict__ x16,
-                                                       float* __restrict__ xinv) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+__device__ __forceinline__ void prep_f16_rows(const uint16_t* __restrict__ x, int rows, int K,
+                                              float* __restrict__ sums, uint16_t* __restrict__ x16,
+                                              float* __restrict__ xinv, int block) {
+  const int row = block * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
   const uint16_t* xr = x + (int64_t)row * K;
@@ -987,6 +989,78 @@ __global__ void __launch_bounds__(256) prep_f16_kernel(const uint16_t* __restric
     *(u32x4*)(xo + g * 128 + (lane & 15) * 8) = o;
   }
   if (lane == 0) xinv[row] = __builtin_ldexpf(1.0f, -e);
+}
+
+template <int NCH>
+__global__ void __launch_bounds__(256) prep_f16_kernel(const uint16_t* __restrict__ x, int rows, int K,
+                                                       float* __restrict__ sums, uint16_t* __restrict__ x16,
+                                                       float* __restrict__ xinv) {
+  prep_f16_rows<NCH>(x, rows, K, sums, x16, xinv, blockIdx.x);
+}
+
+// K1 (one wave per token, as route_kernel) and the fp16 input of the int8
+// gate_up (as prep_f16_kernel) in one launch: workgroups 0 .. ceil(T / 4) - 1
+// route four tokens each, the rest prepare four rows of x each.  The two
+// are independent; one launch instead of two in the prefill layer.
+template <int VPL, int NCH>
+__global__ void __launch_bounds__(256) route_prep_f16_kernel(const uint16_t* __restrict__ logits, int T, int E,
+                                                             int k, unsigned flags, int32_t* __restrict__ ids_out,
+                                                             float* __restrict__ w_out, int route_blocks,
+                                                             const uint16_t* __restrict__ x, int rows, int K,
+                                                             float* __restrict__ sums, uint16_t* __restrict__ x16,
+                                                             float* __restrict__ xinv) {
+  __shared__ float sv[4][kMaxTopK];
+  __shared__ int si[4][kMaxTopK];
+  if ((int)blockIdx.x >= route_blocks) {
+    prep_f16_rows<NCH>(x, rows, K, sums, x16, xinv, blockIdx.x - route_blocks);
+    return;
+  }
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  int id;
+  float w;
+  route_token<VPL, true>(logits, t, E, k, flags, sv[wave], si[wave], &id, &w);
+  if (lane < k) {
+    ids_out[(int64_t)t * k + lane] = id;
+    w_out[(int64_t)t * k + lane] = w;
+  }
+}
+
+hipError_t launch_route_prep_f16(const void* logits, int T, int E, int k, unsigned flags, int32_t* ids, float* w,
+                                 const void* x, int rows, int K, float* sums, uint16_t* x16, float* xinv,
+                                 hipStream_t stream) {
+  if (T <= 0 || rows <= 0) return hipErrorInvalidValue;
+  if (K % 128 != 0 || K > 4096 || E <= 0 || E > 256) return hipErrorInvalidValue;
+  const int route_blocks = (T + 3) / 4;
+  const dim3 grid(route_blocks + (rows + 3) / 4), block(256);
+  const uint16_t* lg = (const uint16_t*)logits;
+  const uint16_t* xb = (const uint16_t*)x;
+#define NKT_RP_LAUNCH(V, C)                                                                                    \
+  hipLaunchKernelGGL((route_prep_f16_kernel<V, C>), grid, block, 0, stream, lg, T, E, k, flags, ids, w,       \
+                     route_blocks, xb, rows, K, sums, x16, xinv)
+#define NKT_RP_CASE(V)                                          \
+  case V:                                                       \
+    switch ((K + 511) / 512) {                                  \
+      case 1: NKT_RP_LAUNCH(V, 1); break;                       \
+      case 2: NKT_RP_LAUNCH(V, 2); break;                       \
+      case 3:                                                   \
+      case 4: NKT_RP_LAUNCH(V, 4); break;                       \
+      default: NKT_RP_LAUNCH(V, 8); break;                      \
+    }                                                           \
+    break;
+  switch ((E + 63) / 64) {
+    NKT_RP_CASE(1)
+    NKT_RP_CASE(2)
+    NKT_RP_CASE(3)
+    NKT_RP_CASE(4)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef NKT_RP_CASE
+#undef NKT_RP_LAUNCH
+  return hipGetLastError();
 }
 
 hipError_t launch_prep_f16(const void* x, int rows, int K, float* sums, uint16_t* x16, float* xinv,

@@ -215,6 +215,11 @@ hipError_t launch_group_sums(const void* x, int rows, int K, float* out, hipStre
 // (x16, same layout) and 1 / scale per row (xinv); K <= 4096
 hipError_t launch_prep_f16(const void* x, int rows, int K, float* sums, uint16_t* x16, float* xinv,
                            hipStream_t stream);
+// K1 for T tokens (bf16 logits, as launch_route) and launch_prep_f16 of
+// rows rows of x in one launch.
+hipError_t launch_route_prep_f16(const void* logits, int T, int E, int k, unsigned flags, int32_t* ids, float* w,
+                                 const void* x, int rows, int K, float* sums, uint16_t* x16, float* xinv,
+                                 hipStream_t stream);
 // whether launch_gemm2 runs a on the int8 pipeline kernel (which then takes
 // gate_up's input as the fp16 copy when a.xinv is set)
 bool gemm2_i8_pipeline(const GemmArgs& a, int wf);
