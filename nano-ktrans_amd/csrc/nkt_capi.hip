@@ -579,6 +579,8 @@ int do_combine(Handle* h, int T, void* out, void* ws, const WsLayout& L, hipStre
 }
 
 constexpr int kSharedSideMinTokens = 8;
+// the few-token layer (down + combine in one launch) never forks the shared expert
+static_assert(kSharedSideMinTokens > kDcMaxTokens, "side stream and the down + combine launch");
 
 
 // Whether the shared expert can run on the side stream beside the routed
@@ -634,14 +636,20 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
     return NKT_ERR;
   }
   if (!check_weights(h, h->Is > 0, err, len)) return NKT_ERR;
-  // one token (decode form, every expert HBM-resident): the down GEMV and
-  // the combine run as one launch
-  const bool single = T == 1 && L.bm == kTileSrcCols && !h->resident && h->act_bf16 &&
-                      down_combine_supported(h->wf, h->H, h->I, h->I, h->k);
+  // one token, or a few tokens whose pairs rarely share an expert (T k at
+  // most E / 4) with int4 weights (decode form, every expert HBM-resident):
+  // the down GEMV and the combine run as one launch, whose workgroups each
+  // read the weight rows of one token's pairs.  Measured: Qwen3 int4 T = 2 /
+  // 3 / 4 24 / 28 / 29.5 -> 21 / 27 / 29 us; where tokens share experts
+  // (Mixtral-8x7B T = 4: 104 -> 117 us) or the rows are int8 (Qwen3 int8
+  // T = 4: 29.3 -> 30.1 us) the separate launches win.
+  const bool few = L.bm == kTileSrcCols && !h->resident && h->act_bf16 &&
+                   (T == 1 || (T <= kDcMaxTokens && h->wf == WF_I4 && 4 * T * h->k <= h->E)) &&
+                   down_combine_supported(h->wf, h->H, h->I, h->I, h->k);
   // the shared expert as chunks of the routed launches (no launches of its
-  // own); the single-token down + combine takes them as more positions
+  // own); the down + combine launch takes them as more items
   int chunks = shared_chunk_count(h, L);
-  if (single && chunks > 0 && !down_combine_supported(h->wf, h->H, h->I, h->I, h->k + chunks)) chunks = 0;
+  if (few && chunks > 0 && !down_combine_supported(h->wf, h->H, h->I, h->I, h->k + chunks)) chunks = 0;
   std::unique_lock<std::mutex> lk(h->side_mu, std::defer_lock);
   const bool side = allow_side && chunks == 0 && shared_side_ready(h, T, L, st);
   if (side) {
@@ -661,7 +669,7 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
       return NKT_ERR;
     }
   }
-  if (single) {
+  if (few) {
     int rc = NKT_OK;
     // routing inside gate_up pays when its workgroups run in about one round
     // (Qwen3: 384, Qwen1.5-MoE: 352 + 352 for the shared expert's chunks);
@@ -671,7 +679,7 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
     constexpr int64_t kInlineRouteMaxWorkgroups = 1024;
     const int route_tiles = L.max_tiles > h->k + chunks ? L.max_tiles : h->k + chunks;
     const bool inline_route =
-        logits && h->E <= 128 &&
+        T == 1 && logits && h->E <= 128 &&
         gemv_workgroups(h->wf, PHASE_GATE_UP, 2 * h->I, h->H, h->I, route_tiles) <= kInlineRouteMaxWorkgroups;
     if (inline_route) {
       // K1 + K2 inside the gate_up launch (every workgroup routes the token)
@@ -707,9 +715,14 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
     GemmArgs b = expert_args(h, PHASE_DOWN, false, ws_ptr<void>(ws, L, NKT_WS_H), ws, L, T);
     const bool sh = h->Is > 0;
     if (chunks > 0) set_shared_chunks(h, b, PHASE_DOWN, ws, L, T, 0, chunks);
-    const CombineTail c{ws_ptr<float>(ws, L, kWsWpos),
+    const CombineTail c{ws_ptr<float>(ws, L, NKT_WS_TOPK_WEIGHTS),
+                        ws_ptr<int32_t>(ws, L, NKT_WS_TOPK_IDS),
+                        ws_ptr<int32_t>(ws, L, NKT_WS_INV),
                         sh && chunks == 0 ? ws_ptr<float>(ws, L, NKT_WS_SHARED_Y) : nullptr,
-                        sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE) : nullptr, residual, out};
+                        sh ? ws_ptr<float>(ws, L, NKT_WS_SHARED_GATE) : nullptr,
+                        residual,
+                        out,
+                        T};
     if (!check_hip(launch_down_combine(b, c, h->wf, h->k, st), "down + combine kernel", err, len)) return NKT_ERR;
     return NKT_OK;
   }

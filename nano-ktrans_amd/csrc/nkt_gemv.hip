@@ -675,18 +675,21 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
 }
 
 // ---------------------------------------------------------------------------
-// Down projection + combine for one token (T = 1).  Every routed expert has
-// one position (tile p = position p = the p-th of the token's experts in
-// ascending id, its h row p), so the k expert rows of an output row set can
-// be added inside one workgroup: its waves take the (position, K part) pairs,
-// each through gemv_accumulate exactly as the down GEMV does for that tile,
-// and leave the column-0 partial sums in LDS; then y_p = the K parts added in
-// order (x the int8 row scale) and out = sum over p in order of w(p) y_p,
-// + gate x shared expert row, + residual, one rounding -- the arithmetic of
-// the down GEMV followed by combine_kernel, so the same bits, with no y
-// round trip through HBM and no combine launch.
+// Down projection + combine for a few tokens (T <= kDcMaxTokens).  Workgroup
+// (row set, t) owns 16 output rows of token t: its waves take the (pair,
+// K part) items of the token's k pairs -- pair j's position inv[t k + j] (its
+// h row) and expert ids[t k + j], computed as a one-position tile through
+// gemv_accumulate exactly as the down GEMV computes that position's column
+// (with at most 4 tokens every decode tile holds at most 4 positions, so the
+// down GEMV takes the same quad form) -- and leave the column-0 partial sums
+// in LDS at the rank of the position among the token's (ascending position =
+// ascending expert id); then y = the K parts added in order (x the int8 row
+// scale) and out = sum over the ranks in order of w y, + gate x shared expert
+// row, + residual, one rounding -- the arithmetic of the down GEMV followed
+// by combine_kernel, so the same bits, with no y round trip through HBM and
+// no combine launch.
 // With a.sh_chunks = C > 0 the shared expert's down projection rides along
-// as C more positions n_pos .. n_pos + C - 1, chunk c the K range
+// as C more items n_pos .. n_pos + C - 1 (its h row t), chunk c the K range
 // [cI, cI + I) of the shared down rows (its input the same columns of the
 // shared h the gate_up launch wrote); its row is the C chunk rows added in
 // chunk order (each x the int8 row scale), times the gate that launch wrote.
@@ -702,35 +705,40 @@ __global__ void __launch_bounds__(64 * kDcWaves) gemv_down_combine_kernel(GemmAr
   constexpr int kStageS = (WF == WF_I4) ? NT * NG * 32 : 0;
   constexpr int kRegion = kStageX + kStageS > 16 ? kStageX + kStageS : 16;
   __shared__ __attribute__((aligned(16))) uint8_t lds[kDcWaves][kRegion];
-  __shared__ f32x4 part[kDcMaxItems][4];  // [position x S + K part][lane / 16]: rows 4 (l / 16) .. + 3, column 0
-  __shared__ float wpos[kMaxTopK];                         // routing weight of each position
-  __shared__ float spos[kMaxTopK + kMaxSharedChunks][16];  // int8: row scales of each position's expert
+  __shared__ f32x4 part[kDcMaxItems][4];  // [rank x S + K part][lane / 16]: rows 4 (l / 16) .. + 3, column 0
+  __shared__ float wrank[kMaxTopK];                         // routing weight of each rank
+  __shared__ float spos[kMaxTopK + kMaxSharedChunks][16];  // int8: row scales of each rank's expert
   const uint32_t lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int rowset = blockIdx.x;
+  const int t = blockIdx.y;  // the token
   const int n_sh = a.sh_chunks;
   const int n_items = (n_pos + n_sh) * S;
+  const int32_t* tinv = c.inv + (int64_t)t * n_pos;
   for (int q = wave; q < n_items; q += kDcWaves) {
-    const int p = q / S, kpart = q % S;
-    const bool sh = p >= n_pos;
-    // the combine's operands of position p ride with its K part 0: its
-    // routing weight (in position order, independent of the tile record) and
-    // the int8 row scales of its expert (issued with the weights)
+    const int slot = q / S, kpart = q % S;
+    const bool sh = slot >= n_pos;
+    // the pair's position (its h row) and expert, its routing weight with
+    // K part 0 (the combine's operand), and, in lanes < k, the positions of
+    // the token's pairs for the rank (ascending position = ascending id)
+    const int p = sh ? 0 : tinv[slot];
+    const int expert = sh ? 0 : c.ids[(int64_t)t * n_pos + slot];
+    const int pm = (!sh && (int)lane < n_pos) ? tinv[lane] : 0;
     float wv = 0.f;
-    if (!sh && kpart == 0 && lane == 0) wv = c.wpos[p];
-    const int expert = sh ? 0 : a.tiles[4 * p];
+    if (!sh && kpart == 0 && lane == 0) wv = c.w[(int64_t)t * n_pos + slot];
     float sc = 0.f;
     if (WF == WF_I8 && kpart == 0 && lane < 16u)
       sc = bf16_bits_to_f32(sh ? a.sh_scales[rowset * 16 + lane]
                                : a.scales[(int64_t)expert * a.s_expert_elems + rowset * 16 + lane]);
-    const TileSrc ts = sh ? shared_chunk_src<WF, PHASE_DOWN>(a, p - n_pos) : routed_src(a, expert);
-    const int src = sh ? 0 : p;
+    const TileSrc ts = sh ? shared_chunk_src<WF, PHASE_DOWN>(a, slot - n_pos) : routed_src(a, expert);
+    const int src = sh ? t : p;
     f32x4 acc[NT];
     gemv_accumulate<WF, PHASE_DOWN, RT, S, NG, D, FULL>(a, ts, 1, src, src, kpart, rowset, lds[wave], lane, acc);
-    if ((lane & 15) == 0) part[q][lane >> 4] = acc[0];
+    const int rank = sh ? slot : (int)__popcll(__ballot((int)lane < n_pos && pm < p));
+    if ((lane & 15) == 0) part[rank * S + kpart][lane >> 4] = acc[0];
     if (kpart == 0) {
-      if (!sh && lane == 0) wpos[p] = wv;
-      if (WF == WF_I8 && lane < 16u) spos[p][lane] = sc;
+      if (!sh && lane == 0) wrank[rank] = wv;
+      if (WF == WF_I8 && lane < 16u) spos[rank][lane] = sc;
     }
   }
   __syncthreads();
@@ -738,12 +746,13 @@ __global__ void __launch_bounds__(64 * kDcWaves) gemv_down_combine_kernel(GemmAr
   // thread r: output row orow0 + r (tile row r = 4 (r / 4) + r % 4 of lane group r / 4)
   const int r = threadIdx.x;
   const int orow = rowset * 16 + r;
+  const int64_t o = (int64_t)t * a.N + orow;
   float acc = 0.f;
   for (int p = 0; p < n_pos; ++p) {
     float y = part[p * S][r >> 2][r & 3];
     for (int kp = 1; kp < S; ++kp) y += part[p * S + kp][r >> 2][r & 3];
     if (WF == WF_I8) y *= spos[p][r];
-    const float term = wpos[p] * y;
+    const float term = wrank[p] * y;
     acc = p == 0 ? term : acc + term;
   }
   if (n_sh > 0) {
@@ -755,12 +764,12 @@ __global__ void __launch_bounds__(64 * kDcWaves) gemv_down_combine_kernel(GemmAr
       if (WF == WF_I8) y *= spos[p][r];
       ys = j == 0 ? y : ys + y;
     }
-    acc += c.shared_gate[0] * ys;
+    acc += c.shared_gate[t] * ys;
   } else if (c.y_shared) {
-    acc += c.shared_gate[0] * c.y_shared[orow];
+    acc += c.shared_gate[t] * c.y_shared[o];
   }
-  if (c.residual) acc += bf16_bits_to_f32(((const uint16_t*)c.residual)[orow]);
-  ((uint16_t*)c.out)[orow] = (uint16_t)f32_to_bf16_bits(acc);
+  if (c.residual) acc += bf16_bits_to_f32(((const uint16_t*)c.residual)[o]);
+  ((uint16_t*)c.out)[o] = (uint16_t)f32_to_bf16_bits(acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -857,7 +866,7 @@ hipError_t launch_gemv_rt(const GemmArgs& a, int max_tiles, hipStream_t stream, 
 template <int WF, int S, int NG>
 hipError_t launch_down_combine_s(const GemmArgs& a, const CombineTail& c, int n_pos, hipStream_t stream) {
   constexpr int D = (WF == WF_BF16) ? 2 : 3;
-  dim3 grid(a.N / 16), block(64 * kDcWaves);
+  dim3 grid(a.N / 16, c.tokens), block(64 * kDcWaves);
   if (NG > 0 && a.K / 128 == S * NG)
     hipLaunchKernelGGL((gemv_down_combine_kernel<WF, S, NG, D, true>), grid, block, 0, stream, a, c, n_pos);
   else
@@ -954,7 +963,9 @@ bool down_combine_supported(int wf, int N, int K, int I, int n_pos) {
 }
 
 hipError_t launch_down_combine(const GemmArgs& a, const CombineTail& c, int wf, int n_pos, hipStream_t stream) {
-  if (!a.tiles || !c.wpos || !c.out || n_pos > kMaxTopK) return hipErrorInvalidValue;
+  if (!c.w || !c.ids || !c.inv || !c.out || n_pos < 1 || n_pos > kMaxTopK || c.tokens < 1 ||
+      c.tokens > kDcMaxTokens || (a.sh_chunks > 0 && a.sh_tokens != c.tokens))
+    return hipErrorInvalidValue;
   if (a.sh_chunks < 0 || a.sh_chunks > kMaxSharedChunks ||
       (a.sh_chunks > 0 && (!a.sh_w || !a.sh_h || !c.shared_gate || (wf != WF_BF16 && !a.sh_scales) ||
                            (int64_t)a.sh_chunks * a.K != a.sh_I)))

@@ -193,15 +193,21 @@ int64_t gemv_workgroups(int wf, int phase, int N, int K, int I, int max_tiles);
 // expert (y_shared [H] fp32 and its gate [1], nullable), residual [H] (act
 // dtype, nullable), out [H] bf16.
 struct CombineTail {
-  const float* wpos;
+  const float* w;       // routing weights [T, k]
+  const int32_t* ids;   // expert ids [T, k]
+  const int32_t* inv;   // position (h row) of each pair [T, k]
   const float* y_shared;
   const float* shared_gate;
   const void* residual;
   void* out;
+  int tokens;  // T
 };
 
-// Down GEMV + combine in one launch for one token (n_pos = its k expert
-// positions, tiles 0 .. n_pos - 1 from K2, h rows by position, bf16).
+// most tokens of the down GEMV + combine launch
+constexpr int kDcMaxTokens = 4;
+
+// Down GEMV + combine in one launch for up to kDcMaxTokens tokens (n_pos =
+// k pairs per token, h rows by position, bf16).
 bool down_combine_supported(int wf, int N, int K, int I, int n_pos);
 hipError_t launch_down_combine(const GemmArgs& a, const CombineTail& c, int wf, int n_pos, hipStream_t stream);
 

@@ -462,8 +462,9 @@ def test_decode_outlier_channels(gpu_device, name, E, T):
                                       ("qwen3_int8", 32, 7), ("small_int8_shared", None, 1)])
 def test_forward_matches_stages_and_leaves_sync_area_zero(gpu_device, name, E, T):
     """The layer equals route -> experts -> shared -> combine through the
-    separate entry points bit for bit (at T = 1 the layer runs the down GEMV
-    and the combine as one launch) in the decode form; in the prefill form
+    separate entry points bit for bit (at T = 1, and at T = 2 / 4 for the
+    int4 Qwen3 shape, the layer runs the down GEMV and the combine as one
+    launch) in the decode form; in the prefill form
     the layer keeps y as fp16 with a power-of-two scale per position and
     256-column slab (the stages keep fp32 y), and a decode-form layer runs
     the shared expert as Is / I chunks whose down sums are added chunk by
