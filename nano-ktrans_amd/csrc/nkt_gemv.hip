@@ -812,12 +812,14 @@ hipError_t launch_gemv_s(const GemmArgs& a, int max_tiles, int n_rowsets, hipStr
 }
 
 // Every wave takes NG K groups and issues all of their loads at once (many
-// short waves stream HBM better than few long ones): about 8 KiB of weights
-// per wave, i.e. a target of 4 groups of int4 and 2 of int8 or bf16 for two
-// row tiles.  The S = ceil(G / target) K parts (at most 8) then split the G
-// groups as evenly as they go, NG = ceil(G / S) each; K too long for eight
-// parts of four groups streams through the ring instead.
-__host__ __device__ constexpr int gemv_target_groups(int wf) { return wf == WF_I4 ? 4 : 2; }
+// short waves stream HBM better than few long ones): a target of 4 groups
+// of int4 (8 KiB of weights for two row tiles) or int8 (16 KiB; measured
+// against 2 groups: Qwen1.5-MoE T = 4 / 16 48.7 / 95 -> 45.5 / 89 us, Qwen3
+// int8 T = 16 45.5 -> 44.1 us) and 2 of bf16.  The S = ceil(G / target) K
+// parts (at most 8) then split the G groups as evenly as they go,
+// NG = ceil(G / S) each; K too long for eight parts of four groups streams
+// through the ring instead.
+__host__ __device__ constexpr int gemv_target_groups(int wf) { return wf == WF_BF16 ? 2 : 4; }
 
 template <int WF, int PHASE, int RT, int NG>
 hipError_t launch_gemv_ng(const GemmArgs& a, int S, int max_tiles, int n_rowsets, hipStream_t stream,
