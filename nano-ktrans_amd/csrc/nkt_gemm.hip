@@ -357,26 +357,27 @@ int gemm_tile_m(int num_tokens, int topk, int num_experts, int wf, bool prefill_
   return 64;
 }
 
-// waves per block and row tiles per wave for each token-tile height
-struct Cfg {
-  int nw, rt;
-};
-static Cfg cfg_for(int bm) {
-  if (bm == 16) return Cfg{8, 2};
-  return Cfg{4, 4};
+// Waves per block and row tiles per wave for each token-tile height: 16
+// positions take 8 waves of 2 row tiles, except fp32 weights (the tiny
+// layers: few tiles, long fp32 MFMA chains), which take 4 waves of one
+// output row tile so the grid has four times the workgroups (Mixtral-style
+// H = 256, I = 512, T = 16: 10 down workgroups instead of 40); larger tiles 4
+// waves of 4.
+constexpr int gemm_waves(int wf, int bm) { return bm == 16 && wf != WF_F32 ? 8 : 4; }
+constexpr int gemm_row_tiles(int wf, int bm, int phase) {
+  return bm != 16 ? 4 : (wf == WF_F32 && phase == PHASE_DOWN) ? 1 : 2;
 }
 
 int gemm_rows_per_block(int wf, int phase, int bm) {
-  (void)wf;
-  const Cfg c = cfg_for(bm);
-  return c.nw * (phase == PHASE_GATE_UP ? c.rt / 2 : c.rt) * 16;
+  const int rt = gemm_row_tiles(wf, bm, phase);
+  return gemm_waves(wf, bm) * (phase == PHASE_GATE_UP ? rt / 2 : rt) * 16;
 }
 
 template <int WF, int BM, int PHASE>
 static hipError_t launch_gemm_t(const GemmArgs& a, int grid_tiles, hipStream_t stream,
                                 const KernelTimer* tm) {
-  constexpr int NW = (BM == 16) ? 8 : 4;
-  constexpr int RT = (BM == 16) ? 2 : 4;
+  constexpr int NW = gemm_waves(WF, BM);
+  constexpr int RT = gemm_row_tiles(WF, BM, PHASE);
   // LDS stage: BM x KC activations (~33 KiB); fp32 activations take half the K
   constexpr int KC0 = (BM == 16) ? 1024 : (BM == 32 ? 512 : 256);
   constexpr int KC = (WF == WF_F32) ? KC0 / 2 : KC0;
