@@ -338,7 +338,7 @@ def test_timed_phases_match_untimed(gpu_device, name, T):
 
 
 @pytest.mark.parametrize("name,E,T", [("qwen3_int4", 32, 16), ("qwen3_int8", 32, 512), ("mixtral_int4", None, 1),
-                                      ("qwen15_int8_shared", None, 16)])
+                                      ("qwen15_int8_shared", None, 16), ("qwen3_int4", None, 4)])
 def test_forward_hidden_fused_router(gpu_device, name, E, T):
     """The layer from hidden states alone (router GEMV fused): logits checked
     against the oracle's (check_router_logits), the output equal to the
