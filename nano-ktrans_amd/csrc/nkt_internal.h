@@ -89,8 +89,8 @@ struct GemmArgs {
   // slot of this phase.  gate_up: the token tiles of chunk 0 also write
   // sigmoid(x . sh_gate_w) to sh_gate (K4); down: chunk c's rows go to
   // sh_y + c sh_tokens H (fp32 [sh_tokens, H]), which the combine adds in
-  // chunk order.  The single-token down + combine launch takes the chunks
-  // as positions instead (GemmArgs::tiles then holds the k routed ones).
+  // chunk order.  The down + combine launch (up to kDcMaxTokens tokens)
+  // takes the chunks as more items of each token instead.
   int sh_chunks;
   int sh_I;
   int sh_tile0;
@@ -103,7 +103,7 @@ struct GemmArgs {
   float* sh_y;
 };
 
-// most chunks of a shared expert in the single-token layer's launches
+// most chunks of a shared expert in the routed decode launches
 constexpr int kMaxSharedChunks = 8;
 
 enum GemmPhase : int { PHASE_GATE_UP = 0, PHASE_DOWN = 1 };
@@ -188,10 +188,10 @@ hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipS
 // launch at its two-tile row sets).
 int64_t gemv_workgroups(int wf, int phase, int N, int K, int I, int max_tiles);
 
-// The combine's inputs beyond y for the single-token down + combine kernel:
-// routing weights by position wpos [k] (written by K2), the gated shared
-// expert (y_shared [H] fp32 and its gate [1], nullable), residual [H] (act
-// dtype, nullable), out [H] bf16.
+// The combine's inputs beyond y for the down + combine kernel of T tokens:
+// routing weights w, expert ids and pair positions inv [T, k] (written by
+// K1 / K2), the gated shared expert (y_shared [T, H] fp32 and its gate [T],
+// nullable), residual [T, H] (act dtype, nullable), out [T, H] bf16.
 struct CombineTail {
   const float* w;       // routing weights [T, k]
   const int32_t* ids;   // expert ids [T, k]
