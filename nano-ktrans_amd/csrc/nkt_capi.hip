@@ -587,10 +587,7 @@ static_assert(kSharedSideMinTokens > kDcMaxTokens, "side stream and the down + c
 // experts: its decode form (T up to kSharedDecodeMaxTokens) touches no
 // workspace region the routed experts use; the stream and events are made on
 // the first call outside graph capture, on the current device.
-bool shared_side_ready(Handle* h, int T, const WsLayout& L, hipStream_t st) {
-  // a single token's layer is too short for the fork and join to pay
-  // (measured: Qwen1.5-MoE T=1 slower by 1 us, T=16 faster by 6 us)
-  if (h->Is <= 0 || L.bm_shared != kTileSrcCols || T < kSharedSideMinTokens) return false;
+bool side_stream_ready(Handle* h, hipStream_t st) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess) return false;
   if (!h->side) {
@@ -611,6 +608,13 @@ bool shared_side_ready(Handle* h, int T, const WsLayout& L, hipStream_t st) {
     h->side_device = dev;
   }
   return dev == h->side_device;
+}
+
+bool shared_side_ready(Handle* h, int T, const WsLayout& L, hipStream_t st) {
+  // a single token's layer is too short for the fork and join to pay
+  // (measured: Qwen1.5-MoE T=1 slower by 1 us, T=16 faster by 6 us)
+  if (h->Is <= 0 || L.bm_shared != kTileSrcCols || T < kSharedSideMinTokens) return false;
+  return side_stream_ready(h, st);
 }
 
 // Routing (route(st)), the routed experts, the shared expert and the combine
@@ -733,9 +737,34 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
                              gemm2_supported(h->wf, PHASE_GATE_UP, g.N, g.K, g.I) && gemm2_i8_pipeline(g, h->wf);
   bool prep_done = false;
   int rc = prep_in_route ? do_route(h, logits, T, ws, L, st, err, len, &g, &prep_done) : route();
+  // a shared expert in the prefill form forks here, once the routing launch
+  // has made the fp16 input copy both expert GEMMs read: its launches (a
+  // dense down of few workgroups among them) run beside the routed experts'
+  // on the side stream and fill what those leave idle
+  bool late = false;
+  if (rc == NKT_OK && prep_done && allow_side && !side && h->Is > 0 && chunks == 0 &&
+      L.bm_shared != kTileSrcCols && side_stream_ready(h, st)) {
+    lk.lock();
+    if (!check_hip(hipEventRecord(h->fork_ev, st), "fork event", err, len) ||
+        !check_hip(hipStreamWaitEvent(h->side, h->fork_ev, 0), "fork wait", err, len))
+      return NKT_ERR;
+    const int rs = do_shared(h, x, T, ws, L, h->side, err, len, true);
+    const hipError_t je = hipEventRecord(h->join_ev, h->side);
+    if (je != hipSuccess) {
+      if (rs == NKT_OK) check_hip(je, "join event", err, len);
+      (void)hipStreamSynchronize(h->side);  // no event to wait on: drain the branch instead
+      return NKT_ERR;
+    }
+    if (rs != NKT_OK) {
+      (void)hipStreamWaitEvent(st, h->join_ev, 0);
+      return NKT_ERR;
+    }
+    late = true;
+  }
   if (rc == NKT_OK) rc = do_experts(h, x, T, ws, L, st, err, len, true, chunks, prep_done);
-  if (rc == NKT_OK && !side && h->Is > 0 && chunks == 0) rc = do_shared(h, x, T, ws, L, st, err, len, prep_done);
-  if (side) {
+  if (rc == NKT_OK && !side && !late && h->Is > 0 && chunks == 0)
+    rc = do_shared(h, x, T, ws, L, st, err, len, prep_done);
+  if (side || late) {
     const hipError_t we = hipStreamWaitEvent(st, h->join_ev, 0);
     if (rc == NKT_OK && !check_hip(we, "join wait", err, len)) rc = NKT_ERR;
   }

@@ -283,12 +283,13 @@ def test_stages_match_forward(gpu_device):
 
 @pytest.mark.parametrize("name,E,T", [("qwen15_int8_shared", None, 16), ("qwen15_int8_shared", None, 1),
                                       ("qwen3_int4", 32, 16), ("qwen3_int8", 32, 512), ("mixtral_int4", None, 300),
-                                      ("qwen3_int4", None, 8), ("mixtral_int4", None, 16)])
+                                      ("qwen3_int4", None, 8), ("mixtral_int4", None, 16),
+                                      ("qwen15_int8_shared", None, 1024)])
 def test_graph_replay_matches_eager(gpu_device, name, E, T):
-    """The layer captured in a HIP graph (the shared expert, or in the prefill
-    form gate_up's pre-pass over x, as a branch forked beside the routing)
-    replays bit for bit like the eager call, replay after replay, with eager
-    calls on the same workspace in between."""
+    """The layer captured in a HIP graph (Qwen1.5-MoE at 1024 tokens: the
+    prefill-form shared expert as a branch forked onto the handle's side
+    stream after the routing launch) replays bit for bit like the eager call,
+    replay after replay, with eager calls on the same workspace in between."""
     announce(f"graph replay {name} T={T}")
     layer, native = _layer(name, E=E)
     x, logits = build_inputs(layer, T, seed=21, device="cuda")
