@@ -99,7 +99,7 @@ def test_empty_and_max_token_batches(gpu_device, max_tokens):
         native.forward(x, logits)
 
 
-@pytest.mark.parametrize("T", [1, 16])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 16])
 def test_qwen3_int4_full(gpu_device, T):
     announce(f"forward qwen3_int4 full T={T}")
     layer, native = _layer("qwen3_int4")
