@@ -18,13 +18,15 @@ Printed JSON fields beyond the standard ones:
                  activations in/out) / its average event-timed duration vs 8 TB/s;
                  traffic (and, for the prefill form, MFMA busy %) from rocprofv3
                  counters on nano-ktrans_amd/nkt_probe (profiles/pmc_moe_layer_counters.md);
-                 beside the rated peak, the practical one measured in the same run:
-                 vendor_copy (a 256 MB torch device copy, read + write bytes/s) for
-                 the HBM bound, vendor_gemm (torch.matmul in fp16 of the same
+                 beside the rated peak, the practical ones measured in the same run:
+                 vendor_read (torch.sum over 512 MB, bytes read/s) and vendor_copy
+                 (a 256 MB torch device copy, read + write bytes/s) for the HBM bound, vendor_gemm (torch.matmul in fp16 of the same
                  multiply-adds as one dense [T k, N, K] GEMM) for the MFMA bound
   cpu_baseline   the reference CPU expert loop (oracle/cpu_loop.py, a torch
                  restatement of nano_ktrans/kernels/cpu_moe.py:491-539) on this
-                 host's cores for the headline; cpu_baselines: every config
+                 host's cores for the headline; cpu_baselines: every config at
+                 every token count the bench reports (Mixtral T=2048 on a
+                 512-token sample)
   secondary      other token counts (T=1, 4), the layer from hidden states
                  (router GEMV inside; plus RMSNorm and residual), the tiny
                  fp32 Mixtral-style layer (T=16), the int8 per-channel prefill
@@ -427,6 +429,22 @@ def vendor_copy_gbps(nbytes=256 << 20):
     return _CEILINGS[key]
 
 
+def vendor_read_gbps(nbytes=512 << 20):
+    """Rate (GB/s, bytes read) of torch.sum over an nbytes fp16 tensor on this
+    GPU: a read-only streaming ceiling, the fair comparator for kernels that
+    only read weights (a copy also writes, and on HBM3E writes cost reads
+    bandwidth)."""
+    key = ("read", nbytes)
+    if key not in _CEILINGS:
+        import torch
+
+        src = torch.empty(nbytes // 2, device="cuda", dtype=torch.float16).normal_()
+        ms = _event_ms(lambda: torch.sum(src), 20)
+        _CEILINGS[key] = nbytes / (ms * 1e-3) / 1e9
+        del src
+    return _CEILINGS[key]
+
+
 def roofline_for(res, bound=None):
     """Roofline of the dominant kernel (the longer of the two expert-GEMM kernels),
     its duration from the dispatch-stamped events of time_kernel.  bound None:
@@ -442,12 +460,17 @@ def roofline_for(res, bound=None):
     if bound == "hbm":
         achieved = d["bytes"] / sec / 1e9
         copy = vendor_copy_gbps()
+        read = vendor_read_gbps()
         return dict(kernel=name, bound="hbm", achieved=round(achieved, 1),
                     peak=HBM_PEAK / 1e9, unit="GB/s", frac=round(achieved * 1e9 / HBM_PEAK, 4),
                     traffic=traffic, algorithmic_bytes_per_launch=round(d["bytes"]),
                     us_per_launch=round(d["us"], 2),
+                    vendor_read=dict(GBps=round(read, 1), frac_of_peak=round(read * 1e9 / HBM_PEAK, 4),
+                                     kernel_frac_of_read=round(achieved / read, 4),
+                                     what="torch.sum over 512 MB fp16, bytes read / s"),
                     vendor_copy=dict(GBps=round(copy, 1), frac_of_peak=round(copy * 1e9 / HBM_PEAK, 4),
-                                     kernel_frac_of_copy=round(achieved / copy, 4)))
+                                     kernel_frac_of_copy=round(achieved / copy, 4),
+                                     what="256 MB device copy, bytes read + written / s"))
     peak = MFMA_F32_PEAK if res["wfmt"] == "f32" else MFMA_BF16_PEAK
     achieved = d["flops"] / sec / 1e12
     out = dict(kernel=name, bound="mfma", achieved=round(achieved, 1),
@@ -491,7 +514,7 @@ def host_info():
     return dict(os_cpu_count=os.cpu_count(), affinity_cores=affinity, cpu_model=model, kt_kernel=kt)
 
 
-def cpu_baseline(w, T, src, x, logits, sample=None, budget_s=12.0):
+def cpu_baseline(w, T, src, x, logits, sample=None, budget_s=8.0):
     """The reference CPU expert loop (oracle/cpu_loop.py: the torch restatement of
     nano_ktrans/kernels/cpu_moe.py:491-539 with quantized_ops.py:86-124, dense
     fp32 experts through linear) on this host's cores, torch threads = the cores
@@ -706,11 +729,12 @@ def main():
     head_inputs = res.pop("inputs")
     log(json.dumps({k: v for k, v in res.items()}))
     secondary = []
+    head_small = {}
     if not args.no_secondary:
         for T in (1, 4):
             log(f"secondary: {head.name} T={T}")
             r = bench_workload(head, T, layers, router, args.steps, args.warmup, dev)
-            r.pop("inputs")
+            head_small[T] = tuple(t.cpu() for t in r.pop("inputs"))
             r["roofline"] = roofline_for(r, "hbm")
             log(json.dumps(r))
             secondary.append(r)
@@ -742,6 +766,11 @@ def main():
         cpu = cpu_baseline(head, args.tokens, src, *head_inputs)
         log(json.dumps(cpu))
         cpu_all.append(cpu)
+        for T, inp in head_small.items():
+            log(f"cpu baseline: {head.name} T={T}")
+            c = cpu_baseline(head, T, src, *inp)
+            log(json.dumps(c))
+            cpu_all.append(c)
     del src
     if not args.no_secondary:
         # the other configurations: (workload, weight copies, [(T, steps, warmup, bounds)],
@@ -751,13 +780,13 @@ def main():
              [(16, 200, 20, ("hbm",))], [(16, None)]),
             (Workload("qwen3_30b_a3b_moe_layer_int8_pc_prefill_zipf", tokens=4096, **QWEN3_INT8), 2,
              [(4096, 20, 4, ("mfma",)), (512, 100, 10, ("mfma", "hbm")), (2048, 40, 6, ("mfma", "hbm"))],
-             [(4096, None)]),
+             [(512, None), (2048, None), (4096, None)]),
             (Workload("mixtral_8x7b_moe_layer_int4_g128", tokens=16, **MIXTRAL_INT4), 4,
              [(1, 200, 20, ("hbm",)), (16, 200, 20, ("hbm",)), (2048, 20, 4, ("mfma",))],
-             [(16, None), (2048, 512)]),
+             [(1, None), (16, None), (2048, 512)]),
             (Workload("qwen15_moe_a27b_layer_int8_pc_shared", tokens=16, **QWEN15_INT8), 4,
              [(1, 200, 20, ("hbm",)), (16, 200, 20, ("hbm",)), (1024, 40, 6, ("hbm", "mfma"))],
-             [(16, None), (1024, None)]),
+             [(1, None), (16, None), (1024, None)]),
         ]
         for w, copies, runs, cpu_runs in plan:
             max_t = max(T for T, *_ in runs)

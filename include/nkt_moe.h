@@ -89,9 +89,21 @@ extern "C" {
                                  activations, up to 256 tokens) */
 #define NKT_WS_ROUTER_LOGITS 11 /* bf16 [T, E] router logits of the *_hidden entry points */
 #define NKT_WS_NORMED 12        /* bf16 [T, H] RMSNorm output of nkt_moe_forward_block    */
-#define NKT_WS_SYNC 13          /* uint32 [32]: word 31 is the status of the last single-launch router
-                                   call, 0 unless a cross-workgroup wait gave up (a library fault) */
+#define NKT_WS_SYNC 13          /* uint32 [32] status words, 0 unless a fault was seen since the caller
+                                   last cleared them (no entry point clears them):
+                                   NKT_STATUS_BAD_ROUTING, NKT_STATUS_ROUTER_WAIT */
 #define NKT_WS_NUM_REGIONS 14
+
+/* Status words (uint32 indices into NKT_WS_SYNC).  Set to 1 by the call
+ * that sees the fault, left alone otherwise; the caller reads them after
+ * synchronising and writes 0 to clear them. */
+/* nkt_moe_route_given / nkt_moe_forward_routed dropped a slot whose id was
+ * outside [0, E) or repeated an earlier slot's id of the same token */
+#define NKT_STATUS_BAD_ROUTING 30
+/* the single-launch router (nkt_moe_route_hidden and the layers built on it,
+ * up to 64 tokens) gave up waiting for a logit workgroup: a library fault;
+ * that call's routing weights are NaN, so its layer output is NaN */
+#define NKT_STATUS_ROUTER_WAIT 31
 
 /* Create a handle for one layer shape.
  * Replaces the construction of HybridMoE's expert state
@@ -127,7 +139,8 @@ int nkt_moe_bind_weights(void* handle, const void* const* ptrs, char* err, size_
  * The sync area -- the first NKT_SYNC_AREA_BYTES bytes of every workspace,
  * the same for every handle and token count (the NKT_WS_SYNC words and the
  * single-launch router's tagged logit words) -- must be zero before a
- * workspace's first use; every call of every handle leaves it zero, so one
+ * workspace's first use; every call of every handle leaves the tagged words
+ * zero and the status words zero unless it reports a fault, so one
  * workspace may serve several handles in turn. */
 #define NKT_SYNC_AREA_BYTES 65792
 int nkt_moe_workspace_bytes(void* handle, int num_tokens, size_t* bytes, char* err, size_t err_len);
@@ -141,6 +154,20 @@ int nkt_moe_workspace_region(void* handle, int num_tokens, int region, size_t* o
  * workspace regions NKT_WS_TOPK_IDS .. NKT_WS_INV. */
 int nkt_moe_route(void* handle, const void* router_logits, int num_tokens, void* workspace,
                   size_t workspace_bytes, void* stream, char* err, size_t err_len);
+
+/* K2 from routing the caller computed (K1 is not run): topk_ids int64
+ * [T, k] and topk_weights fp32 [T, k] (device).  The expert side of the
+ * reference's offload contract: ExpertOffloadBackend.submit_forward(
+ * hidden_states, topk_ids, topk_weights, cuda_stream)
+ * (nano_ktrans/kernels/offload_backend.py:40-52) and kt-kernel's
+ * forward_task(bsz, k, expert_ids int64*, weights fp32*, ...)
+ * (nano_ktrans/kernels/cpu_moe.py:570-592).  The slots of a token may come
+ * in any order (the combine adds experts in ascending id).  Every id must be
+ * in [0, E) and a token's k ids distinct: a slot breaking that is dropped (it
+ * adds nothing) and status word NKT_STATUS_BAD_ROUTING is set.  Results land
+ * in NKT_WS_TOPK_IDS .. NKT_WS_INV as after nkt_moe_route. */
+int nkt_moe_route_given(void* handle, const int64_t* topk_ids, const float* topk_weights, int num_tokens,
+                        void* workspace, size_t workspace_bytes, void* stream, char* err, size_t err_len);
 
 /* K3: grouped SwiGLU expert GEMM for the routed experts (needs a prior
  * nkt_moe_route on the same workspace).  Replaces the per-expert loop
@@ -200,6 +227,19 @@ int nkt_moe_forward(void* handle, const void* hidden_states, const void* router_
                     int num_tokens, void* out, void* workspace, size_t workspace_bytes,
                     void* stream, char* err, size_t err_len);
 
+/* The whole layer from the caller's routing: nkt_moe_route_given, then the
+ * experts, shared expert (when the handle has one) and combine of
+ * nkt_moe_forward.  out[t] = sum over the token's slots, in ascending expert
+ * id, of topk_weights[t, j] * expert_{topk_ids[t, j]}(x_t), in fp32 with one
+ * rounding (experts that nkt_moe_bind_residency marks non-resident add
+ * nothing), plus the gated shared expert.  Replaces the offload backend's
+ * submit_forward / sync_forward pair (nano_ktrans/kernels/offload_backend.py:
+ * 40-52, nano_ktrans/kernels/cpu_moe.py:491-539, 570-630): with residency
+ * set to the experts a backend serves, out is that backend's sum. */
+int nkt_moe_forward_routed(void* handle, const void* hidden_states, const int64_t* topk_ids,
+                           const float* topk_weights, int num_tokens, void* out, void* workspace,
+                           size_t workspace_bytes, void* stream, char* err, size_t err_len);
+
 /* Router GEMV + K1 + K2: router_logits = hidden_states . gate^T (fp32
  * accumulation, rounded to bf16 as nn.Linear(H, E, bias=False) does in bf16),
  * written to NKT_WS_ROUTER_LOGITS, then routed as by nkt_moe_route.  Fuses the
@@ -244,7 +284,9 @@ int nkt_moe_forward_block(void* handle, const void* hidden_states, const void* n
  * scratch: calls that overlap on one GPU (two streams, two handles, two
  * threads) race and must be serialised by the caller.  Nothing in the
  * scratch has to start at zero: each call writes every region before it
- * reads it. */
+ * reads it, and this entry point routes from given logits, so it never runs
+ * the single-launch router and never reads or writes the sync area (the
+ * NKT_WS_SYNC status words and the tagged logit words). */
 int nkt_moe_forward_noalloc(void* handle, const void* hidden_states, const void* router_logits,
                             int num_tokens, void* out, void* stream, char* err, size_t err_len);
 

@@ -365,6 +365,28 @@ int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, 
   return NKT_OK;
 }
 
+// K2 from the caller's routing: topk_ids int64 [T, k], topk_weights fp32
+// [T, k] (sanitised into NKT_WS_TOPK_IDS / NKT_WS_TOPK_WEIGHTS; a dropped
+// slot sets status word NKT_STATUS_BAD_ROUTING)
+int do_route_given(Handle* h, const int64_t* ids, const float* w, int T, void* ws, const WsLayout& L, hipStream_t st,
+                   char* err, size_t len) {
+  if (!ids || !w) {
+    set_err(err, len, "null topk_ids or topk_weights");
+    return NKT_ERR;
+  }
+  if (!check_hip(launch_given_group(ids, w, T, h->E, h->k, L.bm, L.max_tiles, ws_ptr<int32_t>(ws, L, kWsHist),
+                                    ws_ptr<int32_t>(ws, L, NKT_WS_TOPK_IDS), ws_ptr<float>(ws, L, NKT_WS_TOPK_WEIGHTS),
+                                    ws_ptr<int32_t>(ws, L, NKT_WS_COUNTS), ws_ptr<int32_t>(ws, L, NKT_WS_OFFSETS),
+                                    ws_ptr<int32_t>(ws, L, NKT_WS_PERM), ws_ptr<int32_t>(ws, L, NKT_WS_INV),
+                                    ws_ptr<int32_t>(ws, L, kWsTiles), ws_ptr<int32_t>(ws, L, kWsNTiles),
+                                    L.bm == kTileSrcCols ? ws_ptr<int32_t>(ws, L, kWsTileSrc) : nullptr, h->resident,
+                                    ws_ptr<float>(ws, L, kWsWpos),
+                                    ws_ptr<uint32_t>(ws, L, NKT_WS_SYNC) + NKT_STATUS_BAD_ROUTING, st),
+                 "given routing + group kernel", err, len))
+    return NKT_ERR;
+  return NKT_OK;
+}
+
 // Router GEMV (decode-form GEMM over dense 16-token tiles, bf16 gate rows)
 // into the bf16 logits region, then K1 + K2 on those logits.
 bool check_route_hidden(const Handle* h, const void* x, char* err, size_t len) {
@@ -1099,6 +1121,32 @@ int nkt_moe_forward(void* handle, const void* hidden_states, const void* router_
                    true, router_logits);
 }
 
+int nkt_moe_route_given(void* handle, const int64_t* topk_ids, const float* topk_weights, int num_tokens,
+                        void* workspace, size_t workspace_bytes, void* stream, char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!check_call(h, num_tokens, workspace, workspace_bytes, err, err_len)) return NKT_ERR;
+  if (num_tokens == 0) return NKT_OK;
+  const WsLayout L = ws_layout(h, num_tokens);
+  return do_route_given(h, topk_ids, topk_weights, num_tokens, workspace, L, (hipStream_t)stream, err, err_len);
+}
+
+int nkt_moe_forward_routed(void* handle, const void* hidden_states, const int64_t* topk_ids,
+                           const float* topk_weights, int num_tokens, void* out, void* workspace,
+                           size_t workspace_bytes, void* stream, char* err, size_t err_len) {
+  Handle* h = (Handle*)handle;
+  if (!check_call(h, num_tokens, workspace, workspace_bytes, err, err_len)) return NKT_ERR;
+  if (num_tokens == 0) return NKT_OK;
+  if (!topk_ids || !topk_weights) {
+    set_err(err, err_len, "null topk_ids or topk_weights");
+    return NKT_ERR;
+  }
+  const WsLayout L = ws_layout(h, num_tokens);
+  hipStream_t st = (hipStream_t)stream;
+  return run_layer(h, hidden_states, num_tokens, out, workspace, L, st, err, err_len, [&] {
+    return do_route_given(h, topk_ids, topk_weights, num_tokens, workspace, L, st, err, err_len);
+  });
+}
+
 int nkt_moe_forward_noalloc(void* handle, const void* hidden_states, const void* router_logits, int num_tokens,
                             void* out, void* stream, char* err, size_t err_len) {
   Handle* h = (Handle*)handle;
@@ -1181,6 +1229,6 @@ int nkt_moe_forward_block(void* handle, const void* hidden_states, const void* n
                    [&] { return do_route_hidden(h, x, num_tokens, workspace, L, st, err, err_len); }, hidden_states);
 }
 
-const char* nkt_moe_version(void) { return "nkt_moe 0.3.0 gfx950"; }
+const char* nkt_moe_version(void) { return "nkt_moe 0.4.0 gfx950"; }
 
 }  // extern "C"

@@ -164,6 +164,17 @@ hipError_t launch_group_multi(const int32_t* ids, int T, int k, int E, int bm, i
                               int32_t* n_tiles, int32_t* tile_src, const uint8_t* resident,
                               hipStream_t stream);
 
+// K2 from given routing: ids_in int64 [T, k] and w_in fp32 [T, k] (the
+// caller's top-k), sanitised into ids / w (a slot with an id outside [0, E)
+// or repeating an earlier slot's id of its token is dropped: it takes the
+// smallest unused id with weight 0, and *status becomes 1), then grouped as
+// launch_route_group / launch_group_multi group K1's output (one launch when
+// route_group_fused(T, k), else three; hist as for launch_group_multi).
+hipError_t launch_given_group(const int64_t* ids_in, const float* w_in, int T, int E, int k, int bm, int max_tiles,
+                              int32_t* hist, int32_t* ids, float* w, int32_t* counts, int32_t* offsets, int32_t* perm,
+                              int32_t* inv, int32_t* tiles, int32_t* n_tiles, int32_t* tile_src,
+                              const uint8_t* resident, float* wpos, uint32_t* status, hipStream_t stream);
+
 // Tokens per expert up to which the decode form runs (by weight format).
 double decode_form_max_avg(int wf);
 

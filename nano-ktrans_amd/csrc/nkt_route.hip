@@ -459,21 +459,31 @@ __global__ void __launch_bounds__(kGroupThreads) route_group_kernel(
 // 8 (l / 16) ..), every wave multiplying its blocks by the token tiles of x on
 // the matrix cores (A = gate block, B = x columns, fp32 accumulation); the 16
 // partial tiles are added in wave order (fixed) and rounded once to bf16.
-// Each pair of logits goes out as one 64-bit device-coherent store of
+// Each pair of logits goes out as one 64-bit device-coherent word of
 // (call generation << 32 | the two bf16 logits): the word carries its own
-// "written by this call" tag, so the reader needs no separate flag.
+// "written by this call" tag, so the reader needs no separate flag.  Every
+// word is 0 when a call starts, and every call leaves it 0.
 //
 // Workgroup 0 is dispatched before the others (workgroups of a grid start in
 // order), so its wait cannot keep them from running.  Each of its threads
 // polls its words (device-coherent loads) until their tags hold this call's
-// generation -- a bounded wait: past kSyncSpinLimit polls it goes on anyway
-// and the status word (NKT_WS_SYNC word 31) says 1, otherwise 0 -- keeps the
-// logits, and clears the tags (a graph replay reuses the same generation;
-// nothing else writes tag 0).  Then it writes the bf16 logits region and
-// routes and groups exactly as route_group_kernel does, from LDS.
+// generation, keeps the logits and clears the words (a graph replay reuses
+// the same generation).  Then it writes the bf16 logits region and routes and
+// groups exactly as route_group_kernel does, from LDS.
+//
+// The wait is bounded (kSyncSpinLimit polls).  Past it, workgroup 0 claims
+// each word still empty with a compare-and-swap 0 -> kTagPoison and goes on:
+// it routes from what it has, writes NaN routing weights (the layer's output
+// is NaN, not silently wrong) and sets status word NKT_WS_SYNC[31] to 1 (never
+// cleared here).  A logit workgroup publishes its word by a compare-and-swap
+// 0 -> value; finding the poison instead, it knows the collector has given up
+// on that word and clears it.  Either way the word ends at 0 before the
+// kernel ends, so no later call -- a graph replay with the same generation
+// included -- can take a stale word for a fresh one.
 // ---------------------------------------------------------------------------
 constexpr int kRouterRowsPerBlock = 16;
 constexpr uint32_t kSyncSpinLimit = 1u << 20;
+constexpr uint64_t kTagPoison = ~0ull;
 
 struct RouteHiddenLds {
   int32_t ids_s[kFusedRouteMaxPairs];
@@ -554,8 +564,15 @@ __global__ void __launch_bounds__(kGroupThreads) route_hidden_kernel(
       if (t < T && e0 < E) {  // E % 4 == 0: the four experts are all real
         uint64_t* dst = tagged + ((size_t)t * E + e0) / 2;
         const uint64_t tag = (uint64_t)gen << 32;
-        __hip_atomic_store(dst, tag | pack_bf16x2(s[0], s[1]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(dst + 1, tag | pack_bf16x2(s[2], s[3]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t val[2] = {tag | pack_bf16x2(s[0], s[1]), tag | pack_bf16x2(s[2], s[3])};
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          uint64_t expect = 0ull;
+          // the word is 0 unless the collector gave up on it (kTagPoison): then clear it
+          if (!__hip_atomic_compare_exchange_strong(dst + j, &expect, val[j], __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT))
+            __hip_atomic_store(dst + j, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
     }
     return;
@@ -583,18 +600,30 @@ __global__ void __launch_bounds__(kGroupThreads) route_hidden_kernel(
         v = __hip_atomic_load(tagged + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         ++spins;
       }
-      ok = ok && (uint32_t)(v >> 32) == gen;
+      if ((uint32_t)(v >> 32) != gen) {
+        // give up on this word: claim it (0 -> poison, which its writer will
+        // clear), unless the writer's value landed since the last poll
+        uint64_t expect = 0ull;
+        if (__hip_atomic_compare_exchange_strong(tagged + i, &expect, kTagPoison, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT)) {
+          ok = false;
+          v = 0ull;
+        } else {
+          v = expect;
+        }
+      }
       L.logits[i] = (uint32_t)v;
       ((uint32_t*)logits)[i] = (uint32_t)v;
-      __hip_atomic_store(tagged + i, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (v != 0ull) __hip_atomic_store(tagged + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   const bool all_ok = __syncthreads_and(ok);
-  if (threadIdx.x == 0) sync[31] = all_ok ? 0u : 1u;
+  if (threadIdx.x == 0 && !all_ok) __hip_atomic_store(sync + 31, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   for (int t = wave; t < T; t += kGroupWaves) {
     int id;
     float w;
     route_token<VPL, true>(L.logits, t, E, k, flags, L.sv[wave], L.si[wave], &id, &w, L.selmask[t]);
+    if (!all_ok) w = __builtin_nanf("");
     if (lane < k) {
       L.ids_s[t * k + lane] = id;
       L.w_s[t * k + lane] = w;
@@ -607,6 +636,149 @@ __global__ void __launch_bounds__(kGroupThreads) route_hidden_kernel(
   __syncthreads();
   group_write(L.g, L.ids_s, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, tile_src, L.w_s,
               wpos);
+}
+
+// ---------------------------------------------------------------------------
+// K2 from routing the caller computed: the expert side of the reference's
+// offload contract (ExpertOffloadBackend.submit_forward(hidden_states,
+// topk_ids, topk_weights, stream), nano_ktrans/kernels/offload_backend.py:
+// 40-52; kt-kernel's forward_task(bsz, k, expert_ids int64*, weights fp32*,
+// input, output, ...), nano_ktrans/kernels/cpu_moe.py:570-592).  Slot j of
+// token t names expert ids[t k + j] with weight w[t k + j]; K1 is not run.
+// Every later kernel takes a token's k experts to be distinct ids in [0, E),
+// as top-k leaves them.  A slot whose id is outside [0, E) or repeats an
+// earlier slot's id of the same token is dropped: it takes the smallest
+// expert id the token leaves unused, with weight 0 (so the selection stays k
+// distinct experts and every later access stays in bounds), and the status
+// word gets 1 (it is never cleared here).
+// ---------------------------------------------------------------------------
+
+// One wave per token.  Lanes < k return the slot's (sanitised) id and weight;
+// *dropped (uniform) says whether a slot was dropped.  selmask (nullable,
+// LDS): the token's experts as bits, bit e of word e / 32, words < 2 VPL
+// written by lane 0.
+template <int VPL>
+__device__ __forceinline__ void given_token(const int64_t* __restrict__ ids_in, const float* __restrict__ w_in, int t,
+                                            int E, int k, int* out_id, float* out_w, bool* dropped,
+                                            uint32_t* selmask = nullptr) {
+  const int lane = threadIdx.x & 63;
+  int64_t v = -1;
+  float w = 0.f;
+  if (lane < k) {
+    v = ids_in[(int64_t)t * k + lane];
+    w = w_in[(int64_t)t * k + lane];
+  }
+  int id = (v >= 0 && v < E) ? (int)v : -1;
+  bool dup = false;
+  for (int i = 0; i < k; ++i) {
+    const int o = __builtin_amdgcn_readlane(id, i);
+    dup = dup || (i < lane && o == id);
+  }
+  const uint64_t dm = ballot64(lane < k && (id < 0 || dup));
+  if (dm) {
+    // the kept ids as a 256-bit set, then the dropped slots in slot order each
+    // take the smallest free id (at most k - 1 ids are taken and k <= E, so
+    // it is below E)
+    uint64_t u[4] = {0ull, 0ull, 0ull, 0ull};
+    for (int i = 0; i < k; ++i) {
+      const int e = __builtin_amdgcn_readlane(id, i);
+      if (!((dm >> i) & 1ull)) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) u[q] |= (e >> 6) == q ? 1ull << (e & 63) : 0ull;
+      }
+    }
+    for (int i = 0; i < k; ++i) {
+      if (!((dm >> i) & 1ull)) continue;
+      int f = 0;
+#pragma unroll
+      for (int q = 3; q >= 0; --q)
+        if (~u[q]) f = 64 * q + __builtin_ctzll(~u[q]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) u[q] |= (f >> 6) == q ? 1ull << (f & 63) : 0ull;
+      if (lane == i) {
+        id = f;
+        w = 0.f;
+      }
+    }
+  }
+  if (selmask) {
+#pragma unroll
+    for (int wi = 0; wi < 2 * VPL; ++wi) {
+      uint32_t word = 0u;
+      for (int i = 0; i < k; ++i) {
+        const int e = __builtin_amdgcn_readlane(id, i);
+        word |= (e >> 5) == wi ? 1u << (e & 31) : 0u;
+      }
+      if (lane == 0) selmask[wi] = word;
+    }
+  }
+  *out_id = lane < k ? id : -1;
+  *out_w = w;
+  *dropped = dm != 0ull;
+}
+
+// large batches: one wave per token writes the sanitised ids and weights
+template <int VPL>
+__global__ void __launch_bounds__(256) given_kernel(const int64_t* __restrict__ ids_in, const float* __restrict__ w_in,
+                                                    int T, int E, int k, int32_t* __restrict__ ids_out,
+                                                    float* __restrict__ w_out, uint32_t* __restrict__ status) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= T) return;
+  int id;
+  float w;
+  bool dropped;
+  given_token<VPL>(ids_in, w_in, t, E, k, &id, &w, &dropped);
+  if (lane < k) {
+    ids_out[(int64_t)t * k + lane] = id;
+    w_out[(int64_t)t * k + lane] = w;
+  }
+  if (dropped && lane == 0) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// small batches (route_group_fused): the given routing and K2 in one
+// workgroup, as route_group_kernel does from logits
+template <int VPL>
+__global__ void __launch_bounds__(kGroupThreads) given_group_kernel(
+    const int64_t* __restrict__ ids_in, const float* __restrict__ w_in, int T, int E, int k, int bm, int max_tiles,
+    int32_t* __restrict__ ids_out, float* __restrict__ w_out, int32_t* __restrict__ counts,
+    int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ inv,
+    int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles, int32_t* __restrict__ tile_src,
+    const uint8_t* __restrict__ resident, float* __restrict__ wpos, uint32_t* __restrict__ status) {
+  __shared__ int32_t ids_s[kFusedRouteMaxPairs];
+  __shared__ float w_s[kFusedRouteMaxPairs];
+  __shared__ uint32_t selmask[kFusedRouteMaxTokens][8];
+  __shared__ GroupLds g;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  unsigned res = 0;
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int e = VPL * lane + i;
+      res |= (unsigned)(!resident || (e < E && resident[e])) << i;
+    }
+  }
+  bool any_dropped = false;
+  for (int t = wave; t < T; t += kGroupWaves) {
+    int id;
+    float w;
+    bool dropped;
+    given_token<VPL>(ids_in, w_in, t, E, k, &id, &w, &dropped, selmask[t]);
+    any_dropped = any_dropped || dropped;
+    if (lane < k) {
+      ids_s[t * k + lane] = id;
+      w_s[t * k + lane] = w;
+      ids_out[(int64_t)t * k + lane] = id;
+      w_out[(int64_t)t * k + lane] = w;
+    }
+  }
+  if (any_dropped && lane == 0) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (wave == 0) group_scan<VPL>(selmask, T, E, bm, res, g);
+  __syncthreads();
+  group_write(g, ids_s, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, tile_src, w_s, wpos);
 }
 
 #define NKT_VPL_SWITCH(E, CASE) \
@@ -691,6 +863,38 @@ hipError_t launch_route_group(const void* logits, int act_bf16, int T, int E, in
   NKT_VPL_SWITCH(E, NKT_RG_CASE)
 #undef NKT_RG_CASE
   return hipGetLastError();
+}
+
+hipError_t launch_given_group(const int64_t* ids_in, const float* w_in, int T, int E, int k, int bm, int max_tiles,
+                              int32_t* hist, int32_t* ids, float* w, int32_t* counts, int32_t* offsets, int32_t* perm,
+                              int32_t* inv, int32_t* tiles, int32_t* n_tiles, int32_t* tile_src,
+                              const uint8_t* resident, float* wpos, uint32_t* status, hipStream_t stream) {
+  if (T <= 0) return hipSuccess;
+  if (bm <= 0 || (bm & (bm - 1)) != 0) return hipErrorInvalidValue;
+  if (tile_src && bm != kTileSrcCols) return hipErrorInvalidValue;
+  if (!ids_in || !w_in || !status) return hipErrorInvalidValue;
+  if (route_group_fused(T, k)) {
+#define NKT_GG_CASE(V)                                                                                          \
+  case V:                                                                                                       \
+    hipLaunchKernelGGL((given_group_kernel<V>), dim3(1), dim3(kGroupThreads), 0, stream, ids_in, w_in, T, E, k, \
+                       bm, max_tiles, ids, w, counts, offsets, perm, inv, tiles, n_tiles, tile_src, resident,   \
+                       wpos, status);                                                                           \
+    break;
+    NKT_VPL_SWITCH(E, NKT_GG_CASE)
+#undef NKT_GG_CASE
+    return hipGetLastError();
+  }
+#define NKT_GV_CASE(V)                                                                                      \
+  case V:                                                                                                   \
+    hipLaunchKernelGGL((given_kernel<V>), dim3((T + 3) / 4), dim3(256), 0, stream, ids_in, w_in, T, E, k, ids, \
+                       w, status);                                                                          \
+    break;
+  NKT_VPL_SWITCH(E, NKT_GV_CASE)
+#undef NKT_GV_CASE
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_group_multi(ids, T, k, E, bm, max_tiles, hist, counts, offsets, perm, inv, tiles, n_tiles, tile_src,
+                            resident, stream);
 }
 
 }  // namespace nkt

@@ -55,7 +55,12 @@ WS_ROUTER_LOGITS = 11
 WS_NORMED = 12
 WS_SYNC = 13
 
-# leading bytes of every workspace that must start at zero (every call leaves them zero)
+# status words inside WS_SYNC (uint32 indices): 1 after a fault, cleared by the caller
+STATUS_BAD_ROUTING = 30
+STATUS_ROUTER_WAIT = 31
+
+# leading bytes of every workspace that must start at zero (every call leaves
+# the tagged words zero, and the status words zero unless it reports a fault)
 SYNC_AREA_BYTES = 65792
 
 EXPORTED_SYMBOLS = (
@@ -67,6 +72,7 @@ EXPORTED_SYMBOLS = (
     "nkt_moe_workspace_bytes",
     "nkt_moe_workspace_region",
     "nkt_moe_route",
+    "nkt_moe_route_given",
     "nkt_moe_experts",
     "nkt_moe_experts_phase",
     "nkt_moe_experts_phase_timed",
@@ -75,6 +81,7 @@ EXPORTED_SYMBOLS = (
     "nkt_moe_combine_extra",
     "nkt_moe_bind_residency",
     "nkt_moe_forward",
+    "nkt_moe_forward_routed",
     "nkt_moe_route_hidden",
     "nkt_moe_forward_hidden",
     "nkt_moe_forward_block",
@@ -121,6 +128,8 @@ def lib() -> ctypes.CDLL:
     L.nkt_moe_workspace_region.restype = i
     L.nkt_moe_route.argtypes = [vp, vp, i, vp, sz, vp, cp, sz]
     L.nkt_moe_route.restype = i
+    L.nkt_moe_route_given.argtypes = [vp, vp, vp, i, vp, sz, vp, cp, sz]
+    L.nkt_moe_route_given.restype = i
     L.nkt_moe_experts.argtypes = [vp, vp, i, vp, sz, vp, cp, sz]
     L.nkt_moe_experts.restype = i
     L.nkt_moe_experts_phase.argtypes = [vp, i, vp, i, vp, sz, vp, cp, sz]
@@ -133,6 +142,8 @@ def lib() -> ctypes.CDLL:
     L.nkt_moe_combine.restype = i
     L.nkt_moe_forward.argtypes = [vp, vp, vp, i, vp, vp, sz, vp, cp, sz]
     L.nkt_moe_forward.restype = i
+    L.nkt_moe_forward_routed.argtypes = [vp, vp, vp, vp, i, vp, vp, sz, vp, cp, sz]
+    L.nkt_moe_forward_routed.restype = i
     L.nkt_moe_combine_extra.argtypes = [vp, i, vp, vp, vp, sz, vp, cp, sz]
     L.nkt_moe_combine_extra.restype = i
     L.nkt_moe_bind_residency.argtypes = [vp, vp, cp, sz]

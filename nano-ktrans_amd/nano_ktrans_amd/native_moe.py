@@ -263,6 +263,83 @@ class NativeMoE:
                 self.region(T, N.WS_PERM, torch.int32, (T * k,)),
                 self.region(T, N.WS_INV, torch.int32, (T * k,)))
 
+    def _check_routing(self, topk_ids: torch.Tensor, topk_weights: torch.Tensor, T: int):
+        """The caller's routing as the C ABI takes it: int64 ids and fp32 weights, [T, k], contiguous."""
+        k = self.top_k
+        for name, t in (("topk_ids", topk_ids), ("topk_weights", topk_weights)):
+            if t.device != self.device:
+                raise ValueError(f"{name} on {t.device}, layer on {self.device}")
+            if t.numel() != T * k:
+                raise ValueError(f"{name} has {t.numel()} entries, expected [{T}, {k}]")
+        if topk_ids.dtype not in (torch.int64, torch.int32):
+            raise ValueError(f"topk_ids must be an integer tensor, got {topk_ids.dtype}")
+        if not topk_weights.dtype.is_floating_point:
+            raise ValueError(f"topk_weights must be floating point, got {topk_weights.dtype}")
+        ids = topk_ids.reshape(T, k).to(torch.int64).contiguous()
+        w = topk_weights.reshape(T, k).to(torch.float32).contiguous()
+        self._routing = (ids, w)  # kept alive while the kernels read them
+        return ids, w
+
+    def route_given(self, topk_ids: torch.Tensor, topk_weights: torch.Tensor):
+        """K2 from the caller's routing (K1 not run): ``topk_ids`` [T, k] (int64 or int32) and
+        ``topk_weights`` [T, k].  Returns the same workspace views as ``route``.  A slot whose id is
+        outside [0, E) or repeats an earlier slot's id of its token is dropped and sets the
+        STATUS_BAD_ROUTING word (``check_status``)."""
+        T = topk_ids.reshape(-1, self.top_k).shape[0] if topk_ids.numel() else 0
+        ids, w = self._check_routing(topk_ids, topk_weights, T)
+        ws = self.workspace(T)
+        with torch.cuda.device(self.device):
+            self.err.check(self.lib.nkt_moe_route_given(self.handle, ids.data_ptr(), w.data_ptr(), T, ws.data_ptr(),
+                                                        ws.numel(), self._stream(), self.err.buf, self.err.size),
+                           "nkt_moe_route_given")
+        k, E = self.top_k, self.num_experts
+        return (self.region(T, N.WS_TOPK_IDS, torch.int32, (T, k)),
+                self.region(T, N.WS_TOPK_WEIGHTS, torch.float32, (T, k)),
+                self.region(T, N.WS_COUNTS, torch.int32, (E,)),
+                self.region(T, N.WS_OFFSETS, torch.int32, (E + 1,)),
+                self.region(T, N.WS_PERM, torch.int32, (T * k,)),
+                self.region(T, N.WS_INV, torch.int32, (T * k,)))
+
+    def forward_routed(self, hidden_states: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
+                       out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """The layer on the caller's routing: out[t] = sum over the token's slots (ascending expert id)
+        of topk_weights[t, j] * expert_{topk_ids[t, j]}(x_t), plus the gated shared expert when the
+        layer has one; experts marked non-resident (``set_residency``) add nothing."""
+        x = self._check_input(hidden_states, self.hidden_size, "hidden_states")
+        T = x.shape[0]
+        ids, w = self._check_routing(topk_ids, topk_weights, T)
+        if out is None:
+            out = torch.empty(T, self.hidden_size, dtype=self.act_dtype, device=self.device)
+        if T == 0:
+            return out
+        ws = self.workspace(T)
+        with torch.cuda.device(self.device):
+            self.err.check(self.lib.nkt_moe_forward_routed(self.handle, x.data_ptr(), ids.data_ptr(), w.data_ptr(), T,
+                                                           out.data_ptr(), ws.data_ptr(), ws.numel(), self._stream(),
+                                                           self.err.buf, self.err.size), "nkt_moe_forward_routed")
+        return out
+
+    # ------------------------------------------------------------------ status
+    def status(self) -> Dict[str, int]:
+        """The workspace's status words (synchronises the device): bad_routing (a given-routing call
+        dropped a slot) and router_wait (the single-launch router gave up waiting; its call's routing
+        weights were NaN).  0 = no fault since they were last cleared."""
+        if self._ws is None:
+            return {"bad_routing": 0, "router_wait": 0}
+        torch.cuda.synchronize(self.device)
+        words = self._ws[:128].view(torch.int32).cpu()
+        return {"bad_routing": int(words[N.STATUS_BAD_ROUTING]), "router_wait": int(words[N.STATUS_ROUTER_WAIT])}
+
+    def check_status(self, clear: bool = True) -> None:
+        """Raise ``NativeError`` if a status word reports a fault (after clearing it when ``clear``)."""
+        st = self.status()
+        bad = {k: v for k, v in st.items() if v}
+        if bad and clear:
+            self._ws[:128].view(torch.int32)[N.STATUS_BAD_ROUTING:N.STATUS_ROUTER_WAIT + 1].zero_()
+            torch.cuda.synchronize(self.device)
+        if bad:
+            raise N.NativeError(f"MoE layer status: {bad}")
+
     def route_hidden(self, hidden_states: torch.Tensor):
         """Router GEMV + K1 + K2 from hidden states (after ``load_router``).  Returns
         (router_logits bf16 [T, E], ids, weights, counts, offsets, perm, inv) as views."""

@@ -326,10 +326,25 @@ def moe_forward(x: np.ndarray, logits: np.ndarray, experts: List[Expert], top_k:
 
     x [T, H] and logits [T, E] hold the activation-dtype values as float32.
     h_bf16: every expert's SwiGLU output rounded to bf16 (``expert_forward``)."""
-    x = np.ascontiguousarray(x, dtype=np.float32)
-    T, H = x.shape
-    E = len(experts)
     ids, w = route(logits, top_k, use_softmax, renorm, bf16)
+    return moe_forward_given(x, ids, w, experts, shared, shared_gate, return_parts, h_bf16)
+
+
+def moe_forward_given(x: np.ndarray, ids: np.ndarray, w: np.ndarray, experts: List[Expert],
+                      shared: Optional[Expert] = None, shared_gate: Optional[np.ndarray] = None,
+                      return_parts: bool = False, h_bf16: bool = False):
+    """The expert loop on routing the caller computed: ids [T, k] (distinct
+    ids in [0, E) per token, any slot order) and weights w [T, k] (fp32),
+    as the offload backend's loop takes them (nano_ktrans/kernels/cpu_moe.py:
+    491-539: for each expert in ascending id, the tokens that picked it in
+    ascending order, y * w accumulated in fp32).  Same outputs as
+    ``moe_forward``."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    T, H = x.shape
+    top_k = ids.shape[1]
+    E = len(experts)
     counts, offsets, perm, inv = group(ids, E)
     out = np.zeros((T, H), dtype=np.float32)
     y_pairs = np.zeros((T * top_k, H), dtype=np.float32)

@@ -163,10 +163,15 @@ def test_qwen3_shape_bf16_weights(gpu_device, T):
     _check(layer, native_layer(layer, torch.device("cuda")), T)
 
 
-def test_qwen3_int8_full_prefill(gpu_device):
-    announce("forward qwen3_int8 full T=2048")
+@pytest.mark.parametrize("T", [512, 2048, 4096])
+def test_qwen3_int8_full_prefill(gpu_device, T):
+    """The Qwen3-30B-A3B int8 prefill layer at its full shape (E = 128) and
+    Zipf(1.1)-skewed routing, every row of every token count against the
+    oracle: at T = 4096 that is all 32768 positions, the last tiles of every
+    expert and the far end of the XCD work order included."""
+    announce(f"forward qwen3_int8 full T={T}")
     layer, native = _layer("qwen3_int8")
-    _check(layer, native, 2048)
+    _check(layer, native, T)
 
 
 def test_qwen3_int8_batch_invariance_at_4096(gpu_device):
@@ -210,6 +215,41 @@ def test_small_int8_short_k(gpu_device, T):
     announce(f"forward small_int8_shared T={T}")
     layer, native = _layer("small_int8_shared")
     _check(layer, native, T)
+
+
+@pytest.mark.parametrize("wfmt,T", [("int4_g128", 1), ("int4_g128", 2), ("int4_g128", 3), ("int4_g128", 16),
+                                    ("bf16", 1), ("bf16", 16)])
+def test_shared_chunks_int4_and_bf16(gpu_device, wfmt, T):
+    """The shared expert as chunks of the routed launches for every weight
+    format: Qwen1.5-MoE's shape (E = 60, k = 4, I = 1408, shared 5632 = 4 x
+    1408) with int4 g128 and bf16 weights.  One token: the chunks ride in the
+    routing gate_up and the down + combine launch; int4 at T = 2 and 3
+    (4 T k <= E): the few-token down + combine launch with chunk items (the
+    int4 chunk scale addressing of gate_up and down); T = 16: chunk tiles of
+    the routed decode launches.  Against the oracle, and the chunk gate and h
+    against the shared stage's bit for bit."""
+    from dataclasses import replace
+
+    from nano_ktrans_amd import _native as N
+    announce(f"shared chunks qwen15 shape {wfmt} T={T}")
+    key = ("qwen15_" + wfmt, None, None)
+    if key not in _LAYERS:
+        cfg = replace(CONFIGS["qwen15_int8_shared"], name="qwen15_" + wfmt, wfmt=wfmt)
+        _LAYERS.clear()
+        layer = build_layer(cfg, device="cuda")
+        _LAYERS[key] = (layer, native_layer(layer, torch.device("cuda")))
+    layer, native = _LAYERS[key]
+    assert layer.cfg.shared_in_routed_launches(T)
+    out = _check(layer, native, T, seed=73).clone()
+    Is = layer.cfg.Is
+    gate_layer = native.region(T, N.WS_SHARED_GATE, torch.float32, (T,)).clone()
+    h_layer = native.region(T, N.WS_SHARED_H, torch.bfloat16, (T, Is)).clone()
+    x, _ = build_inputs(layer, T, seed=73, device="cuda")
+    gate_stage, _ = native.shared(x)
+    h_stage = native.region(T, N.WS_SHARED_H, torch.bfloat16, (T, Is))
+    torch.cuda.synchronize()
+    assert torch.equal(gate_layer, gate_stage)
+    assert torch.equal(h_layer, h_stage)
 
 
 @pytest.mark.parametrize("T", [1, 16, 200])
@@ -362,6 +402,8 @@ def test_forward_hidden_fused_router(gpu_device, name, E, T):
     again = native.forward(x, g_logits)
     torch.cuda.synchronize()
     assert torch.equal(out, again)
+    assert not native.workspace(T)[:N.SYNC_AREA_BYTES].any()
+    native.check_status()
 
 
 def _spread_rows(T, ids, n_edge=32, n_hot=16):
@@ -457,7 +499,8 @@ def test_decode_outlier_channels(gpu_device, name, E, T):
                                       ("qwen3_int4", None, 1), ("qwen15_int8_shared", None, 1),
                                       ("qwen3_int4", None, 16), ("qwen3_int4", None, 4), ("mixtral_int4", None, 16),
                                       ("qwen3_int8", 32, 16), ("qwen3_int8", 32, 512), ("qwen15_int8_shared", None, 1024),
-                                      # 2 .. 16 tokens: routed inside the gate_up launch
+                                      # 2 .. 16 tokens: the routing launch, then the decode launches
+                                      # (2 Qwen3 int4 tokens: the down + combine launch)
                                       ("qwen3_int4", None, 2), ("qwen3_int4", None, 8), ("qwen3_int4", 32, 13),
                                       ("qwen15_int8_shared", None, 5), ("mixtral_int4", None, 3),
                                       ("qwen3_int8", 32, 7), ("small_int8_shared", None, 1)])

@@ -127,7 +127,8 @@ def test_route_hidden_matches_oracle(gpu_device, name, T):
     """Router GEMV fused with K1 + K2 (one launch up to 64 tokens, three past
     it): bf16 logits against the oracle's single rounding of the exact dot
     products (check_router_logits), and routing / grouping of those logits
-    bit-exact; the single launch's flags are reset and its status word is 0."""
+    bit-exact; the workspace's whole sync area (status words and the single
+    launch's tagged logit words) is left zero."""
     from nano_ktrans_amd import _native as N
     cfg = CONFIGS[name]
     announce(f"route_hidden {name} T={T}")
@@ -148,9 +149,10 @@ def test_route_hidden_matches_oracle(gpu_device, name, T):
     assert np.array_equal(offsets.cpu().numpy(), ooffsets)
     assert np.array_equal(perm.cpu().numpy(), operm)
     assert np.array_equal(inv.cpu().numpy(), oinv)
-    if T <= 64:  # the single launch: flags of its ceil(E / 16) logit workgroups consumed
-        sync = native.region(T, N.WS_SYNC, torch.int32, (32,)).cpu().numpy()
-        assert sync[31] == 0 and not sync[:(cfg.E + 15) // 16].any()
+    # the whole sync area (status words and the single launch's tagged logit
+    # words) is left zero
+    assert not native.workspace(T)[:N.SYNC_AREA_BYTES].any()
+    native.check_status()
 
 
 def test_route_hidden_single_launch_replays(gpu_device):
@@ -189,8 +191,8 @@ def test_route_hidden_single_launch_replays(gpu_device):
         torch.cuda.synchronize()
         for a, b in zip(views, ref_a):
             assert torch.equal(a, b), f"replay {r}"
-    sync = native.region(T, N.WS_SYNC, torch.int32, (32,)).cpu().numpy()
-    assert sync[31] == 0 and not sync[:(cfg.E + 15) // 16].any()
+    assert not native.workspace(T)[:N.SYNC_AREA_BYTES].any()
+    native.check_status()
 
 
 def test_route_hidden_rejects_missing_router_and_fp32(gpu_device):

@@ -417,6 +417,47 @@ def test_moe_forward_matches_independent_torch_loop():
     assert O.rel_l2(out, ref.numpy()) < 1e-5
 
 
+def test_moe_forward_given_matches_independent_torch_loop():
+    """The loop on caller-given routing (the offload backend's side of the
+    contract): ids in shuffled slot order, weights that neither sum to one
+    nor descend by slot, the same expert picked by many tokens.  Against the
+    reference loop's torch float64 restatement (cpu_moe.py:515-538: experts
+    ascending, torch.where per expert, index_add_), and against moe_forward
+    where the given routing is the oracle's own."""
+    rng = np.random.default_rng(12)
+    T, H, E, k, I = 11, 128, 6, 3, 128
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    experts = [O.Expert(*(rng.standard_normal(s).astype(np.float32) * 0.05 for s in ((I, H), (I, H), (H, I))))
+               for _ in range(E)]
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    ids[:5, 0] = 4  # a hot expert
+    for t in range(5):
+        rest = [e for e in range(E) if e != 4]
+        ids[t, 1:] = rng.permutation(rest)[: k - 1]
+    w = (rng.random((T, k)) * 2.0 - 0.5).astype(np.float32)
+    out = O.moe_forward_given(x, ids, w, experts)
+    tid = torch.from_numpy(ids.astype(np.int64))
+    tw = torch.from_numpy(w.astype(np.float64))
+    ref = torch.zeros(T, H, dtype=torch.float64)
+    for e in range(E):
+        rows, slots = torch.where(tid == e)
+        if rows.numel() == 0:
+            continue
+        ex = experts[e]
+        y = torch.from_numpy(_torch_swiglu64(x[rows.numpy()], ex.gate, ex.up, ex.down))
+        ref.index_add_(0, rows, y * tw[rows, slots].unsqueeze(1))
+    assert O.rel_l2(out, ref.numpy()) < 1e-5
+    # the slot order of a token does not matter
+    perm = np.stack([rng.permutation(k) for _ in range(T)])
+    shuf = O.moe_forward_given(x, np.take_along_axis(ids, perm, 1), np.take_along_axis(w, perm, 1), experts)
+    assert np.array_equal(shuf, out)
+    # given the oracle's own routing, it is moe_forward
+    logits = rng.standard_normal((T, E)).astype(np.float32)
+    rid, rw = O.route(logits, k, True, True, False)
+    assert np.array_equal(O.moe_forward_given(x, rid, rw, experts),
+                          O.moe_forward(x, logits, experts, k, True, True, False))
+
+
 def test_moe_forward_single_expert_reduces_to_dense_mlp():
     rng = np.random.default_rng(4)
     T, H, I = 7, 128, 128

@@ -37,6 +37,45 @@ def test_noalloc_matches_forward(gpu_device, name, E):
         compare(out.float().cpu().numpy(), oracle_forward(layer, x, logits), layer.cfg)
 
 
+@pytest.mark.parametrize("name,E,T", [("qwen3_int4", 32, 16), ("small_int8_shared", None, 1)])
+def test_noalloc_captures_in_a_graph(gpu_device, name, E, T):
+    """The call is capture-safe: captured in a HIP graph in global capture
+    mode (where a hipMalloc, hipFree or stream creation anywhere in the
+    process fails the capture), it replays bit for bit like the eager call,
+    replay after replay, with eager calls of other inputs on the shared
+    scratch in between; and the device's free memory (hipMemGetInfo, which
+    sees the library's own allocations, unlike torch's allocator counters)
+    is the same before and after eager calls."""
+    announce(f"noalloc graph capture {name} T={T}")
+    layer = build_layer(CONFIGS[name], device="cuda", num_experts=E)
+    native = native_layer(layer, torch.device("cuda"), max_tokens=64)
+    x, logits = build_inputs(layer, T, seed=55, device="cuda")
+    x2, l2 = build_inputs(layer, T, seed=56, device="cuda")
+    ref = native.forward(x, logits).clone()
+    ref2 = native.forward(x2, l2).clone()
+    out = torch.empty_like(ref)
+    out2 = torch.empty_like(ref)
+    native.forward_noalloc(x, logits, out)  # first call on the device: the scratch address lookup
+    torch.cuda.synchronize()
+    free_before = torch.cuda.mem_get_info()[0]
+    for _ in range(3):
+        native.forward_noalloc(x2, l2, out2)
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free_before
+    assert torch.equal(out2, ref2)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, capture_error_mode="global"):
+        native.forward_noalloc(x, logits, out)
+    for r in range(3):
+        out.zero_()
+        native.forward_noalloc(x2, l2, out2)  # eager work on the same scratch
+        torch.cuda.synchronize()
+        assert torch.equal(out2, ref2)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {r}"
+
+
 def test_noalloc_rejects_batches_beyond_the_scratch(gpu_device):
     from nano_ktrans_amd import _native as N
 
