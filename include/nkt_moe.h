@@ -89,21 +89,17 @@ extern "C" {
                                  activations, up to 256 tokens) */
 #define NKT_WS_ROUTER_LOGITS 11 /* bf16 [T, E] router logits of the *_hidden entry points */
 #define NKT_WS_NORMED 12        /* bf16 [T, H] RMSNorm output of nkt_moe_forward_block    */
-#define NKT_WS_SYNC 13          /* uint32 [32] status words, 0 unless a fault was seen since the caller
-                                   last cleared them (no entry point clears them):
-                                   NKT_STATUS_BAD_ROUTING, NKT_STATUS_ROUTER_WAIT */
+#define NKT_WS_SYNC 13          /* uint32 [32]: words 0 .. 16 the single-launch router's counters (zero
+                                   between calls), word NKT_STATUS_BAD_ROUTING a status word */
 #define NKT_WS_NUM_REGIONS 14
 
-/* Status words (uint32 indices into NKT_WS_SYNC).  Set to 1 by the call
- * that sees the fault, left alone otherwise; the caller reads them after
- * synchronising and writes 0 to clear them. */
-/* nkt_moe_route_given / nkt_moe_forward_routed dropped a slot whose id was
- * outside [0, E) or repeated an earlier slot's id of the same token */
+/* Status word (uint32 index into NKT_WS_SYNC), 0 unless a fault was seen
+ * since the caller last cleared it: set to 1 by the call that sees the fault
+ * (no entry point clears it); the caller reads it after synchronising and
+ * writes 0 to clear it.  nkt_moe_route_given / nkt_moe_forward_routed
+ * dropped a slot whose id was outside [0, E) or repeated an earlier slot's id
+ * of the same token. */
 #define NKT_STATUS_BAD_ROUTING 30
-/* the single-launch router (nkt_moe_route_hidden and the layers built on it,
- * up to 64 tokens) gave up waiting for a logit workgroup: a library fault;
- * that call's routing weights are NaN, so its layer output is NaN */
-#define NKT_STATUS_ROUTER_WAIT 31
 
 /* Create a handle for one layer shape.
  * Replaces the construction of HybridMoE's expert state
@@ -138,9 +134,9 @@ int nkt_moe_bind_weights(void* handle, const void* const* ptrs, char* err, size_
 /* Workspace size for num_tokens tokens, and the byte offset of each region.
  * The sync area -- the first NKT_SYNC_AREA_BYTES bytes of every workspace,
  * the same for every handle and token count (the NKT_WS_SYNC words and the
- * single-launch router's tagged logit words) -- must be zero before a
- * workspace's first use; every call of every handle leaves the tagged words
- * zero and the status words zero unless it reports a fault, so one
+ * single-launch router's counters and published selection masks) -- must be
+ * zero before a workspace's first use; every call of every handle leaves it
+ * zero (the status word aside, when a call reports a fault), so one
  * workspace may serve several handles in turn. */
 #define NKT_SYNC_AREA_BYTES 65792
 int nkt_moe_workspace_bytes(void* handle, int num_tokens, size_t* bytes, char* err, size_t err_len);
@@ -245,8 +241,10 @@ int nkt_moe_forward_routed(void* handle, const void* hidden_states, const int64_
  * written to NKT_WS_ROUTER_LOGITS, then routed as by nkt_moe_route.  Fuses the
  * decoder layer's gate (nano_ktrans/models/mixtral.py:127, 212) into the
  * expert path; needs bf16 activations and a packed NKT_SLOT_ROUTER.  Up to
- * 64 tokens (and top_k * tokens <= 1024, num_experts % 4 == 0) the GEMV,
- * routing and grouping are one launch; larger batches take three. */
+ * 64 tokens (and top_k * tokens <= 1024, num_experts % 4 == 0, hidden_size <=
+ * 8192) the GEMV, routing and grouping are one launch whose workgroups hand
+ * their results on through counters in the sync area without waiting for
+ * each other; larger batches take three launches. */
 int nkt_moe_route_hidden(void* handle, const void* hidden_states, int num_tokens, void* workspace,
                          size_t workspace_bytes, void* stream, char* err, size_t err_len);
 
@@ -260,9 +258,11 @@ int nkt_moe_forward_hidden(void* handle, const void* hidden_states, int num_toke
 
 /* The decoder layer's MoE half (nano_ktrans/models/mixtral.py:206-223):
  * x = RMSNorm(hidden_states) with norm_weight [H] (bf16, device) and eps as
- * nano_ktrans/layers/norm.py:11-17 computes it (written to NKT_WS_NORMED),
- * then the layer from x as nkt_moe_forward_hidden, and out = hidden_states +
- * that output (the residual add inside the combine's fp32 sum).  bf16 only. */
+ * nano_ktrans/layers/norm.py:11-17 computes it (written to NKT_WS_NORMED;
+ * inside the routing launch when nkt_moe_route_hidden's one-launch form takes
+ * the batch), then the layer from x as nkt_moe_forward_hidden, and out =
+ * hidden_states + that output (the residual add inside the combine's fp32
+ * sum).  bf16 only. */
 int nkt_moe_forward_block(void* handle, const void* hidden_states, const void* norm_weight, float eps,
                           int num_tokens, void* out, void* workspace, size_t workspace_bytes, void* stream,
                           char* err, size_t err_len);
@@ -286,7 +286,7 @@ int nkt_moe_forward_block(void* handle, const void* hidden_states, const void* n
  * scratch has to start at zero: each call writes every region before it
  * reads it, and this entry point routes from given logits, so it never runs
  * the single-launch router and never reads or writes the sync area (the
- * NKT_WS_SYNC status words and the tagged logit words). */
+ * NKT_WS_SYNC words and the router's published masks). */
 int nkt_moe_forward_noalloc(void* handle, const void* hidden_states, const void* router_logits,
                             int num_tokens, void* out, void* stream, char* err, size_t err_len);
 

@@ -43,7 +43,7 @@ constexpr int kWsHist = NKT_WS_NUM_REGIONS + 5;   // int32 [blocks, E] per-block
 constexpr int kWsTileSrc = NKT_WS_NUM_REGIONS + 6; // int32 [max_tiles, 16] decode tiles' input rows
 constexpr int kWsX16 = NKT_WS_NUM_REGIONS + 7;     // fp16 [T, H] scaled copy of x (int8 prefill gate_up)
 constexpr int kWsXInv = NKT_WS_NUM_REGIONS + 8;    // fp32 [T] 1 / scale of each row of that copy
-constexpr int kWsTagged = NKT_WS_NUM_REGIONS + 9; // u64 [T, E / 2] tagged logit pairs (single-launch router)
+constexpr int kWsTagged = NKT_WS_NUM_REGIONS + 9; // u32 [T, 8] the single-launch router's published selection masks
 constexpr int kWsWpos = NKT_WS_NUM_REGIONS + 10;  // fp32 [T k] routing weights by position (fused route + group)
 constexpr int kWsShChunkY = NKT_WS_NUM_REGIONS + 11;  // fp32 [Is / I, T, H] the shared expert's chunk rows
 constexpr int kWsAll = NKT_WS_NUM_REGIONS + 12;
@@ -133,8 +133,9 @@ bool prefill_form_ok(const Handle* h, bool shared) {
 
 size_t align_up(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Sync area sizes: 32 status words (padded), then kFusedRouteMaxTokens x
-// kMaxExperts / 2 tagged logit words of 8 bytes.
+// Sync area sizes: 32 words (the single-launch router's counters, the status
+// word; padded), then the router's mask area (64 KiB, of which it uses
+// T x 8 words: the published size of the area is kept).
 constexpr size_t kSyncStatusBytes = 256;
 constexpr size_t kSyncTaggedBytes = (size_t)kFusedRouteMaxTokens * kMaxExperts * 4;
 static_assert(kSyncStatusBytes + kSyncTaggedBytes == NKT_SYNC_AREA_BYTES, "the sync area's published size");
@@ -198,7 +199,7 @@ WsLayout ws_layout(const Handle* h, int T) {
   sz[kWsWpos] = P * 4;
   sz[kWsShChunkY] = (size_t)shared_chunk_count(h, L) * T * h->H * 4;
   // The sync area first, the same size and place for every handle and
-  // token count (status words, the router's tagged logit words): it must be
+  // token count (counters and status, the router's published masks): it must be
   // zero before a workspace's first use, every call of every handle leaves
   // it zero, and so no region's old contents -- of this handle or of another
   // sharing the workspace -- ever land there.
@@ -321,6 +322,8 @@ GemmArgs expert_args(const Handle* h, int phase, bool shared, const void* in, vo
   return a;
 }
 
+constexpr int kSpreadMinTokens = 16;
+
 // prep (nullable): the int8 gate_up's fp16 input to make in the routing
 // launch when routing takes the large-batch path (*prep_done says whether it
 // did)
@@ -340,6 +343,18 @@ int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, 
   int32_t* tiles = ws_ptr<int32_t>(ws, L, kWsTiles);
   int32_t* n_tiles = ws_ptr<int32_t>(ws, L, kWsNTiles);
   int32_t* tile_src = L.bm == kTileSrcCols ? ws_ptr<int32_t>(ws, L, kWsTileSrc) : nullptr;
+  // more than 16 tokens: K1 on one wave per token over several workgroups,
+  // the last to finish groups (Qwen3 int4 T = 64: 90 -> 83 us per layer);
+  // up to 16 the one-workgroup route + group is as fast (measured T = 8 / 16)
+  if (T > kSpreadMinTokens && route_spread_ok(T, h->k, h->E, h->H, false)) {
+    if (!check_hip(launch_route_spread(logits, h->act_bf16, nullptr, nullptr, nullptr, 0.f, nullptr, h->H, T, h->E,
+                                       h->k, h->flags, L.bm, L.max_tiles, nullptr, ws_ptr<uint32_t>(ws, L, NKT_WS_SYNC),
+                                       ws_ptr<uint32_t>(ws, L, kWsTagged), ids, wts, counts, offsets, perm, inv, tiles,
+                                       n_tiles, tile_src, h->resident, ws_ptr<float>(ws, L, kWsWpos), st),
+                   "route + group kernel", err, len))
+      return NKT_ERR;
+    return NKT_OK;
+  }
   if (route_group_fused(T, h->k)) {
     if (!check_hip(launch_route_group(logits, h->act_bf16, T, h->E, h->k, h->flags, L.bm, L.max_tiles,
                                       ids, wts, counts, offsets, perm, inv, tiles, n_tiles, tile_src,
@@ -409,34 +424,31 @@ bool check_route_hidden(const Handle* h, const void* x, char* err, size_t len) {
   return true;
 }
 
-// Generation numbers of the single-launch kernels' flags: unique per call
-// across the process (never 0, the value a consumed flag is reset to).
-// The tag is a bijective hash of the counter (an odd multiplier mod 2^32), so
-// consecutive calls' tags share no low-value pattern with integer data.
-std::atomic<uint32_t> g_generation{0};
-uint32_t next_generation() {
-  uint32_t g = 0;
-  while (g == 0u) g = (++g_generation) * 0x9E3779B1u;
-  return g;
-}
-
+// norm_w (nullable): x is RMS-normalised first (bf16 weight [H], eps) into
+// NKT_WS_NORMED, which then feeds the router GEMV -- inside the routing
+// launch when it takes the batch, else by a launch of its own.
 int do_route_hidden(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipStream_t st, char* err,
-                    size_t len) {
+                    size_t len, const void* norm_w = nullptr, float eps = 0.f) {
   if (!check_route_hidden(h, x, err, len)) return NKT_ERR;
-  if (route_hidden_fused(T, h->k, h->E, h->H)) {
-    if (!check_hip(launch_route_hidden(x, h->w[NKT_SLOT_ROUTER], h->H, T, h->E, h->k, h->flags, L.bm, L.max_tiles,
-                                       ws_ptr<void>(ws, L, NKT_WS_ROUTER_LOGITS), ws_ptr<void>(ws, L, kWsTagged),
-                                       ws_ptr<uint32_t>(ws, L, NKT_WS_SYNC),
-                                       next_generation(), ws_ptr<int32_t>(ws, L, NKT_WS_TOPK_IDS),
+  void* normed = ws_ptr<void>(ws, L, NKT_WS_NORMED);
+  if (route_spread_ok(T, h->k, h->E, h->H, true)) {
+    if (!check_hip(launch_route_spread(nullptr, 1, x, h->w[NKT_SLOT_ROUTER], norm_w, eps, norm_w ? normed : nullptr,
+                                       h->H, T, h->E, h->k, h->flags, L.bm, L.max_tiles,
+                                       ws_ptr<void>(ws, L, NKT_WS_ROUTER_LOGITS), ws_ptr<uint32_t>(ws, L, NKT_WS_SYNC),
+                                       ws_ptr<uint32_t>(ws, L, kWsTagged), ws_ptr<int32_t>(ws, L, NKT_WS_TOPK_IDS),
                                        ws_ptr<float>(ws, L, NKT_WS_TOPK_WEIGHTS), ws_ptr<int32_t>(ws, L, NKT_WS_COUNTS),
                                        ws_ptr<int32_t>(ws, L, NKT_WS_OFFSETS), ws_ptr<int32_t>(ws, L, NKT_WS_PERM),
                                        ws_ptr<int32_t>(ws, L, NKT_WS_INV), ws_ptr<int32_t>(ws, L, kWsTiles),
                                        ws_ptr<int32_t>(ws, L, kWsNTiles),
-                                       L.bm == kTileSrcCols ? ws_ptr<int32_t>(ws, L, kWsTileSrc) : nullptr,
-                                       h->resident, ws_ptr<float>(ws, L, kWsWpos), st),
-                   "router + route + group kernel", err, len))
+                                       L.bm == kTileSrcCols ? ws_ptr<int32_t>(ws, L, kWsTileSrc) : nullptr, h->resident,
+                                       ws_ptr<float>(ws, L, kWsWpos), st),
+                   norm_w ? "rmsnorm + router + route + group kernel" : "router + route + group kernel", err, len))
       return NKT_ERR;
     return NKT_OK;
+  }
+  if (norm_w) {
+    if (!check_hip(launch_rmsnorm(x, norm_w, eps, T, h->H, normed, st), "rmsnorm kernel", err, len)) return NKT_ERR;
+    x = normed;
   }
   const int Ep = router_rows(h);
   GemmArgs r;
@@ -653,10 +665,12 @@ bool shared_side_ready(Handle* h, int T, const WsLayout& L, hipStream_t st) {
 // allow_side false: the shared expert stays on st (no side stream is made).
 // logits (nullable): the router logits when the caller gave them; a single
 // token then is routed inside its gate_up launch instead of by route().
+// x_from_route: the routing launch writes x (the decoder block's folded
+// RMSNorm), so the shared expert forks only after it.
 template <typename Route>
 int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayout& L, hipStream_t st, char* err,
               size_t len, Route route, const void* residual = nullptr, bool allow_side = true,
-              const void* logits = nullptr) {
+              const void* logits = nullptr, bool x_from_route = false) {
   if (!x || !out) {
     set_err(err, len, "null hidden_states or output");
     return NKT_ERR;
@@ -677,7 +691,7 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
   int chunks = shared_chunk_count(h, L);
   if (few && chunks > 0 && !down_combine_supported(h->wf, h->H, h->I, h->I, h->k + chunks)) chunks = 0;
   std::unique_lock<std::mutex> lk(h->side_mu, std::defer_lock);
-  const bool side = allow_side && chunks == 0 && shared_side_ready(h, T, L, st);
+  const bool side = allow_side && !x_from_route && chunks == 0 && shared_side_ready(h, T, L, st);
   if (side) {
     lk.lock();
     if (!check_hip(hipEventRecord(h->fork_ev, st), "fork event", err, len) ||
@@ -764,13 +778,14 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
   // dense down of few workgroups among them) run beside the routed experts'
   // on the side stream and fill what those leave idle
   bool late = false;
-  if (rc == NKT_OK && prep_done && allow_side && !side && h->Is > 0 && chunks == 0 &&
-      L.bm_shared != kTileSrcCols && side_stream_ready(h, st)) {
+  const bool late_ok = (prep_done && L.bm_shared != kTileSrcCols && side_stream_ready(h, st)) ||
+                       (x_from_route && shared_side_ready(h, T, L, st));
+  if (rc == NKT_OK && allow_side && !side && h->Is > 0 && chunks == 0 && late_ok) {
     lk.lock();
     if (!check_hip(hipEventRecord(h->fork_ev, st), "fork event", err, len) ||
         !check_hip(hipStreamWaitEvent(h->side, h->fork_ev, 0), "fork wait", err, len))
       return NKT_ERR;
-    const int rs = do_shared(h, x, T, ws, L, h->side, err, len, true);
+    const int rs = do_shared(h, x, T, ws, L, h->side, err, len, prep_done);
     const hipError_t je = hipEventRecord(h->join_ev, h->side);
     if (je != hipSuccess) {
       if (rs == NKT_OK) check_hip(je, "join event", err, len);
@@ -1222,11 +1237,14 @@ int nkt_moe_forward_block(void* handle, const void* hidden_states, const void* n
   hipStream_t st = (hipStream_t)stream;
   void* x = ws_ptr<void>(workspace, L, NKT_WS_NORMED);
   if (!check_route_hidden(h, x, err, err_len) || !check_weights(h, h->Is > 0, err, err_len)) return NKT_ERR;
-  if (!check_hip(launch_rmsnorm(hidden_states, norm_weight, eps, num_tokens, h->H, x, st), "rmsnorm kernel", err,
-                 err_len))
-    return NKT_ERR;
+  // the routing launch normalises x itself (and writes NKT_WS_NORMED, which
+  // the experts read) whenever it takes the batch
   return run_layer(h, x, num_tokens, out, workspace, L, st, err, err_len,
-                   [&] { return do_route_hidden(h, x, num_tokens, workspace, L, st, err, err_len); }, hidden_states);
+                   [&] {
+                     return do_route_hidden(h, hidden_states, num_tokens, workspace, L, st, err, err_len, norm_weight,
+                                            eps);
+                   },
+                   hidden_states, true, nullptr, true);
 }
 
 const char* nkt_moe_version(void) { return "nkt_moe 0.4.0 gfx950"; }

@@ -142,20 +142,23 @@ hipError_t launch_route_group(const void* logits, int act_bf16, int T, int E, in
                               int32_t* tiles, int32_t* n_tiles, int32_t* tile_src,
                               const uint8_t* resident, float* wpos, hipStream_t stream);
 
-// Router GEMV + K1 + K2 in one launch (bf16 activations) when
-// route_hidden_fused(T, k, E, H): gate_packed is the router weight in the
-// bf16 block layout (rows padded to 32); logits [T, E] bf16 are written as
-// well.  tagged: T E / 2 words of 8 bytes (the logit pairs with their
-// generation tags; every call leaves the tags 0); sync: 32 words of
-// workspace, word 31 the status (1 when a cross-workgroup wait gave up);
-// gen: this call's generation number (never 0).
-bool route_hidden_fused(int T, int k, int E, int H);
-hipError_t launch_route_hidden(const void* x, const void* gate_packed, int H, int T, int E, int k, unsigned flags,
-                               int bm, int max_tiles, void* logits, void* tagged, uint32_t* sync, uint32_t gen,
-                               int32_t* ids,
-                               float* w, int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
-                               int32_t* tiles, int32_t* n_tiles, int32_t* tile_src, const uint8_t* resident,
-                               float* wpos, hipStream_t stream);
+// Router (optional) + K1 + K2 as one launch of several workgroups that hand
+// their results on without waiting (route_spread_ok(T, k, E, H, gemv)).
+// x == nullptr: routing of the given logits_in [T, E] (act dtype).  Else the
+// router GEMV first, logits [T, E] bf16 = x . gate^T written to logits_out
+// (gate_packed: the router weight in the bf16 block layout, rows padded to
+// 32), with norm_w != nullptr x RMS-normalised first (bf16 weight [H], eps;
+// the normalised rows written to normed).  sync: the workspace's status words
+// (the counters use words 0 .. 16, zero before and after every call); masks:
+// T x 8 words of the sync area (zero before and after).  The remaining
+// outputs are launch_route_group's.
+bool route_spread_ok(int T, int k, int E, int H, bool gemv);
+hipError_t launch_route_spread(const void* logits_in, int act_bf16, const void* x, const void* gate_packed,
+                               const void* norm_w, float eps, void* normed, int H, int T, int E, int k,
+                               unsigned flags, int bm, int max_tiles, void* logits_out, uint32_t* sync,
+                               uint32_t* masks, int32_t* ids, float* w, int32_t* counts, int32_t* offsets,
+                               int32_t* perm, int32_t* inv, int32_t* tiles, int32_t* n_tiles, int32_t* tile_src,
+                               const uint8_t* resident, float* wpos, hipStream_t stream);
 
 // K2 over many workgroups (large batches): hist holds group_hist_blocks(T*k) x E int32.
 int group_hist_blocks(int P);

@@ -151,6 +151,7 @@ __device__ __forceinline__ int nth_set_bit(uint64_t m, int r) {
 // barrier that follows group_scan.
 // ws (LDS) / wpos (nullable): the pairs' routing weights, and their copy in
 // position order.
+template <int kThreads = kGroupThreads>
 __device__ __forceinline__ void group_write(const GroupLds& g, const int32_t* ids, int T, int k, int E, int bm,
                                             int max_tiles, int32_t* __restrict__ counts,
                                             int32_t* __restrict__ offsets, int32_t* __restrict__ perm,
@@ -161,7 +162,7 @@ __device__ __forceinline__ void group_write(const GroupLds& g, const int32_t* id
   const int P = T * k;
   const int n_tile_all = g.n_tile_all;
   const int nt_out = min(n_tile_all, max_tiles);
-  for (int e = tid; e < E; e += kGroupThreads) {
+  for (int e = tid; e < E; e += kThreads) {
     counts[e] = g.cnt[e];
     offsets[e] = g.off[e];
   }
@@ -171,7 +172,7 @@ __device__ __forceinline__ void group_write(const GroupLds& g, const int32_t* id
   }
   // tile records; records past the last tile say "no rows" (the decode form
   // reads every record up to max_tiles)
-  for (int ti = tid; ti < max_tiles; ti += kGroupThreads) {
+  for (int ti = tid; ti < max_tiles; ti += kThreads) {
     int4 rec = int4{0, 0, 0, 0};
     if (ti < n_tile_all) {
       const int e = g.tmap[ti];
@@ -182,7 +183,7 @@ __device__ __forceinline__ void group_write(const GroupLds& g, const int32_t* id
   }
   if (tile_src) {
     // column c of tile ti: the expert's token of rank (ti - first tile) * 16 + c, unused columns 0
-    for (int i = tid; i < nt_out * kTileSrcCols; i += kGroupThreads) {
+    for (int i = tid; i < nt_out * kTileSrcCols; i += kThreads) {
       const int ti = i / kTileSrcCols;
       const int e = g.tmap[ti];
       const int r = (ti - g.toff[e]) * kTileSrcCols + (i & (kTileSrcCols - 1));
@@ -192,7 +193,7 @@ __device__ __forceinline__ void group_write(const GroupLds& g, const int32_t* id
   }
   // positions of the pairs; the token of pair p is p / k = (p ceil(2^32 / k)) >> 32
   const uint64_t kmagic = ((1ull << 32) + (uint64_t)k - 1) / (uint64_t)k;
-  for (int p = tid; p < P; p += kGroupThreads) {
+  for (int p = tid; p < P; p += kThreads) {
     const int e = ids[p];
     const int t = (int)(((uint64_t)p * kmagic) >> 32);
     const uint32_t below_lo = t >= 32 ? 0xffffffffu : ((1u << t) - 1u);
@@ -450,192 +451,269 @@ __global__ void __launch_bounds__(kGroupThreads) route_group_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Router GEMV + K1 + K2 in one launch (bf16, T <= 64): logits = x . gate^T
-// (nano_ktrans/models/mixtral.py:127, 212) computed by workgroups 1 .. NB, one
-// 16-expert row block each, then routed and grouped by workgroup 0.
+// Router (optionally RMSNorm + GEMV), K1 and K2 for up to 64 tokens in one
+// launch of several workgroups that pass their results on without waiting
+// for each other ("last arriver"): a workgroup publishes its part, then
+// counts itself in on an agent-scope counter; the one that arrives last --
+// the returned count says so -- has every part and goes on with the next
+// step; the others end.  Nothing polls, so nothing can wait for ever.
 //
-// Workgroup b >= 1: its 16 waves split the K blocks of the packed gate
-// (bf16 blocks of 16 rows x 32 columns, lane l = row l % 16, columns
-// 8 (l / 16) ..), every wave multiplying its blocks by the token tiles of x on
-// the matrix cores (A = gate block, B = x columns, fp32 accumulation); the 16
-// partial tiles are added in wave order (fixed) and rounded once to bf16.
-// Each pair of logits goes out as one 64-bit device-coherent word of
-// (call generation << 32 | the two bf16 logits): the word carries its own
-// "written by this call" tag, so the reader needs no separate flag.  Every
-// word is 0 when a call starts, and every call leaves it 0.
-//
-// Workgroup 0 is dispatched before the others (workgroups of a grid start in
-// order), so its wait cannot keep them from running.  Each of its threads
-// polls its words (device-coherent loads) until their tags hold this call's
-// generation, keeps the logits and clears the words (a graph replay reuses
-// the same generation).  Then it writes the bf16 logits region and routes and
-// groups exactly as route_group_kernel does, from LDS.
-//
-// The wait is bounded (kSyncSpinLimit polls).  Past it, workgroup 0 claims
-// each word still empty with a compare-and-swap 0 -> kTagPoison and goes on:
-// it routes from what it has, writes NaN routing weights (the layer's output
-// is NaN, not silently wrong) and sets status word NKT_WS_SYNC[31] to 1 (never
-// cleared here).  A logit workgroup publishes its word by a compare-and-swap
-// 0 -> value; finding the poison instead, it knows the collector has given up
-// on that word and clears it.  Either way the word ends at 0 before the
-// kernel ends, so no later call -- a graph replay with the same generation
-// included -- can take a stale word for a fresh one.
+// Grid: token blocks of 4 tokens (one wave each) x expert blocks of 16 router
+// rows (1 when the logits are given):
+//   A (router GEMV, bf16): workgroup (tb, eb) computes the logits of experts
+//     16 eb .. 16 eb + 15 for the tokens of block tb: the 4 rows of x (with
+//     NORM first RMS-normalised as nano_ktrans/layers/norm.py:11-17 computes
+//     it, the same arithmetic and order as rmsnorm_kernel; block eb == 0
+//     writes the normalised rows out) sit in LDS as the B operand, the gate
+//     rows are the A operand of v_mfma_f32_16x16x32_bf16, the 4 waves split
+//     K and their partial tiles are added in wave order, rounded once to bf16
+//     and stored (nano_ktrans/models/mixtral.py:127, 212).  Last arriver of
+//     block tb's counter goes on to B.
+//   B (K1): one wave per token, route_token on the block's rows of logits;
+//     ids, weights and the selection mask are published.  Last arriver of the
+//     all-blocks counter goes on to C.
+//   C (K2): the selection masks, ids and weights of every token into LDS,
+//     group_scan and group_write as route_group_kernel; the counters and the
+//     published masks are reset to zero for the next call (so a graph replay
+//     finds them as every call does).
+// Data that crosses workgroups (logits, ids, weights, masks) moves by
+// agent-scope stores and loads (coherent across the XCDs' L2s); a workgroup's
+// waves wait for their stores to complete (vmcnt(0)) and meet at a barrier
+// before its one counter increment, so a count that names the last arriver is
+// only returned after every part it counts is readable.
 // ---------------------------------------------------------------------------
-constexpr int kRouterRowsPerBlock = 16;
-constexpr uint32_t kSyncSpinLimit = 1u << 20;
-constexpr uint64_t kTagPoison = ~0ull;
+constexpr int kSpTokens = 4;                  // tokens per token block: one wave each
+constexpr int kSpThreads = 64 * kSpTokens;
+constexpr int kSpExperts = 16;                // router rows per GEMV workgroup (one MFMA row tile)
+constexpr int kSpMaxBlocks = kFusedRouteMaxTokens / kSpTokens;
+constexpr int kSpMaxH = 8192;                 // rows of x held in LDS: 4 x 8192 bf16
+constexpr int kSpKbBatch = 16;                // K blocks of gate weights in flight per wave
 
-struct RouteHiddenLds {
+enum SpreadMode : int { SP_LOGITS = 0, SP_GEMV = 1, SP_GEMV_NORM = 2 };
+
+struct SpreadArgs {
+  const void* logits_in;    // SP_LOGITS: [T, E] act dtype
+  const uint16_t* x;        // SP_GEMV*: hidden states [T, H] bf16
+  const uint8_t* gate;      // SP_GEMV*: the packed router rows (bf16 blocks)
+  const uint16_t* norm_w;   // SP_GEMV_NORM: RMSNorm weight [H] bf16
+  float eps;
+  uint16_t* normed;         // SP_GEMV_NORM: normalised rows [T, H]
+  uint16_t* logits_out;     // SP_GEMV*: [T, E] bf16
+  int T, E, k, H;
+  unsigned flags;
+  int bm, max_tiles;
+  int32_t* ids;
+  float* w;
+  int32_t* counts;
+  int32_t* offsets;
+  int32_t* perm;
+  int32_t* inv;
+  int32_t* tiles;
+  int32_t* n_tiles;
+  int32_t* tile_src;
+  const uint8_t* resident;
+  float* wpos;
+  uint32_t* cnt;      // sync words: [0, kSpMaxBlocks) per token block, [kSpMaxBlocks] all blocks
+  uint32_t* masks;    // [T][8] published selection masks (zero between calls)
+};
+
+template <typename Tv>
+__device__ __forceinline__ void agent_store(Tv* p, Tv v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename Tv>
+__device__ __forceinline__ Tv agent_load(const Tv* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Every wave's stores complete, the workgroup meets, thread 0 counts it in on
+// *c; returns (to every thread) whether this workgroup arrived last of n.
+__device__ __forceinline__ bool arrive_last(uint32_t* c, uint32_t n, uint32_t* flag_lds) {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores are complete
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag_lds = old == n - 1 ? 1u : 0u;
+  }
+  __syncthreads();
+  return *flag_lds != 0u;
+}
+
+// RMSNorm of one bf16 row with the whole wave (rmsnorm_kernel's order: lane
+// l adds its 8-column chunks l, l + 64, ... in order, then a fixed
+// butterfly); the result to dst0 (LDS) and, when non-null, dst1.
+__device__ __forceinline__ void rms_norm_row(const uint16_t* __restrict__ xr, const uint16_t* __restrict__ wr,
+                                             float eps, int H, uint16_t* dst0, uint16_t* dst1) {
+  const int lane = threadIdx.x & 63;
+  float ss = 0.f;
+  for (int c = lane * 8; c < H; c += 512) {
+    const u32x4 v = *(const u32x4*)(xr + c);
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const float a = __uint_as_float(v[h] << 16), b = __uint_as_float(v[h] & 0xffff0000u);
+      ss += a * a;
+      ss += b * b;
+    }
+  }
+  ss = wave_sum_butterfly(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)H + eps);
+  for (int c = lane * 8; c < H; c += 512) {
+    const u32x4 v = *(const u32x4*)(xr + c);
+    const u32x4 g = *(const u32x4*)(wr + c);
+    u32x4 o;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const float a = bf16_round(__uint_as_float(v[h] << 16) * inv);
+      const float b = bf16_round(__uint_as_float(v[h] & 0xffff0000u) * inv);
+      o[h] = pack_bf16x2(a * __uint_as_float(g[h] << 16), b * __uint_as_float(g[h] & 0xffff0000u));
+    }
+    *(u32x4*)(dst0 + c) = o;
+    if (dst1) *(u32x4*)(dst1 + c) = o;
+  }
+}
+
+struct SpreadGemvLds {
+  uint16_t xs[kSpTokens * kSpMaxH];  // the block's rows of x (normalised)
+  f32x4 red[kSpTokens][64];          // the waves' partial logit tiles
+};
+struct SpreadRouteLds {
+  uint32_t lg[kSpTokens * kMaxExperts / 2];  // the block's rows of bf16 logits
+  float sv[kSpTokens][kMaxTopK];
+  int si[kSpTokens][kMaxTopK];
+  uint32_t sel[kSpTokens][8];
+};
+struct SpreadGroupLds {
   int32_t ids_s[kFusedRouteMaxPairs];
   float w_s[kFusedRouteMaxPairs];
   uint32_t selmask[kFusedRouteMaxTokens][8];
   GroupLds g;
-  float sv[kGroupWaves][kMaxTopK];
-  int si[kGroupWaves][kMaxTopK];
-  uint32_t logits[kFusedRouteMaxTokens * kMaxExperts / 2];  // bf16 pairs [T][E]
 };
 
-template <int VPL>
-__global__ void __launch_bounds__(kGroupThreads) route_hidden_kernel(
-    const uint16_t* __restrict__ x, const uint8_t* __restrict__ gate, int H, int T, int E, int k, unsigned flags,
-    int bm, int max_tiles, uint16_t* __restrict__ logits, uint64_t* __restrict__ tagged, uint32_t* __restrict__ sync,
-    uint32_t gen, int32_t* __restrict__ ids_out, float* __restrict__ w_out, int32_t* __restrict__ counts,
-    int32_t* __restrict__ offsets, int32_t* __restrict__ perm, int32_t* __restrict__ inv,
-    int32_t* __restrict__ tiles, int32_t* __restrict__ n_tiles, int32_t* __restrict__ tile_src,
-    const uint8_t* __restrict__ resident, float* __restrict__ wpos) {
-  constexpr int kRedBytes = kGroupWaves * 4 * 1024;  // partial tiles: [wave][column tile][64 lanes x 16 B]
-  constexpr int kLdsBytes = sizeof(RouteHiddenLds) > kRedBytes ? sizeof(RouteHiddenLds) : kRedBytes;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kLdsBytes];
+template <int VPL, int MODE, bool BF16>
+__global__ void __launch_bounds__(kSpThreads) route_spread_kernel(SpreadArgs a) {
+  constexpr int kBytes = sizeof(SpreadGemvLds) > sizeof(SpreadGroupLds) ? sizeof(SpreadGemvLds) : sizeof(SpreadGroupLds);
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kBytes > sizeof(SpreadRouteLds) ? kBytes : sizeof(SpreadRouteLds)];
+  __shared__ uint32_t flag;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
+  const int n_tb = (a.T + kSpTokens - 1) / kSpTokens;
+  const int n_eb = MODE == SP_LOGITS ? 1 : (a.E + kSpExperts - 1) / kSpExperts;
+  const int tb = blockIdx.x / n_eb;
+  const int t0 = tb * kSpTokens;
+  const int nt = min(kSpTokens, a.T - t0);
 
-  if (blockIdx.x > 0) {
-    // ---- logits of experts 16 (b - 1) .. + 15 for every token ------------
-    const int rb = blockIdx.x - 1;
+  if (MODE != SP_LOGITS) {
+    // ---- A: logits of experts 16 eb .. for the block's tokens -----------
+    SpreadGemvLds& L = *(SpreadGemvLds*)smem;
+    const int eb = blockIdx.x - tb * n_eb;
+    const int H = a.H;
     const int NKB = H / 32;
-    const int CT = (T + 15) / 16;
-    const int col = lane & 15;
-    const uint8_t* ablk = gate + (size_t)rb * NKB * 1024 + lane * 16;
-    const uint16_t* xcol[4];
+    const int nkbw = (NKB - wave + kSpTokens - 1) / kSpTokens;  // this wave's K blocks: wave, wave + 4, ...
+    const uint8_t* ablk = a.gate + (size_t)eb * NKB * 1024 + lane * 16;
+    // the first batch of gate blocks before anything else (HBM latency)
+    u32x4 av[kSpKbBatch];
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      const int t = ct * 16 + col;
-      xcol[ct] = x + (size_t)(t < T ? t : 0) * H + 8 * (lane >> 4);
-    }
-    f32x4 acc[4];
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // four K blocks per wave at a time, every load issued before the first
-    // MFMA (one memory round trip per four blocks, not one per block); K
-    // blocks past the end re-read the last one and add nothing, column tiles
-    // past CT load nothing (their sums are never stored)
-    constexpr int kKbBatch = 4;
-    for (int kb0 = wave; kb0 < NKB; kb0 += kKbBatch * kGroupWaves) {
-      u32x4 a[kKbBatch], xv[kKbBatch][4];
-#pragma unroll
-      for (int i = 0; i < kKbBatch; ++i) {
-        const int kb = min(kb0 + i * kGroupWaves, NKB - 1);
-        a[i] = *(const u32x4*)(ablk + (size_t)kb * 1024);
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
-          xv[i][ct] = ct < CT ? *(const u32x4*)(xcol[ct] + kb * 32) : u32x4{0u, 0u, 0u, 0u};
-      }
-      // keep the loads ahead of the MFMAs (the scheduler would sink each to
-      // its use, a round trip per block)
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < kKbBatch; ++i) {
-        if (kb0 + i * kGroupWaves >= NKB) a[i] = u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) acc[ct] = mfma_bf16(a[i], xv[i][ct], acc[ct]);
+    for (int i = 0; i < kSpKbBatch; ++i)
+      av[i] = i < nkbw ? *(const u32x4*)(ablk + (size_t)(wave + kSpTokens * i) * 1024) : u32x4{0u, 0u, 0u, 0u};
+    if (wave < nt) {
+      const uint16_t* xr = a.x + (size_t)(t0 + wave) * H;
+      uint16_t* xl = L.xs + wave * H;
+      if (MODE == SP_GEMV_NORM) {
+        rms_norm_row(xr, a.norm_w, a.eps, H, xl, eb == 0 ? a.normed + (size_t)(t0 + wave) * H : nullptr);
+      } else {
+        for (int c = lane * 8; c < H; c += 512) *(u32x4*)(xl + c) = *(const u32x4*)(xr + c);
       }
     }
-    f32x4* red = (f32x4*)smem;
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
-      if (ct < CT) red[(wave * 4 + ct) * 64 + lane] = acc[ct];
     __syncthreads();
-    if (wave < CT) {
-      const int ct = wave;
-      f32x4 s = red[ct * 64 + lane];
-      for (int w = 1; w < kGroupWaves; ++w) s += red[(w * 4 + ct) * 64 + lane];
-      const int t = ct * 16 + col;
-      const int e0 = rb * kRouterRowsPerBlock + 4 * (lane >> 4);
-      if (t < T && e0 < E) {  // E % 4 == 0: the four experts are all real
-        uint64_t* dst = tagged + ((size_t)t * E + e0) / 2;
-        const uint64_t tag = (uint64_t)gen << 32;
-        const uint64_t val[2] = {tag | pack_bf16x2(s[0], s[1]), tag | pack_bf16x2(s[2], s[3])};
+    const int col = lane & 15;
+    const uint16_t* xcol = L.xs + col * H + 8 * (lane >> 4);
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int b0 = 0; b0 < nkbw; b0 += kSpKbBatch) {
+      if (b0 > 0) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          uint64_t expect = 0ull;
-          // the word is 0 unless the collector gave up on it (kTagPoison): then clear it
-          if (!__hip_atomic_compare_exchange_strong(dst + j, &expect, val[j], __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT))
-            __hip_atomic_store(dst + j, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
+        for (int i = 0; i < kSpKbBatch; ++i)
+          av[i] = b0 + i < nkbw ? *(const u32x4*)(ablk + (size_t)(wave + kSpTokens * (b0 + i)) * 1024)
+                                : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int i = 0; i < kSpKbBatch; ++i) {
+        const int kb = wave + kSpTokens * (b0 + i);
+        // columns past the block's tokens multiply zeros (their sums are never stored)
+        const u32x4 bv = (col < nt && b0 + i < nkbw) ? *(const u32x4*)(xcol + kb * 32) : u32x4{0u, 0u, 0u, 0u};
+        acc = mfma_bf16(av[i], bv, acc);
       }
     }
-    return;
+    L.red[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+      f32x4 s = L.red[0][lane];
+#pragma unroll
+      for (int w2 = 1; w2 < kSpTokens; ++w2) s += L.red[w2][lane];
+      const int e0 = eb * kSpExperts + 4 * (lane >> 4);
+      if (col < nt && e0 < a.E) {  // E % 4 == 0: the four experts are all real
+        uint32_t* dst = (uint32_t*)(a.logits_out + (size_t)(t0 + col) * a.E + e0);
+        agent_store(dst, pack_bf16x2(s[0], s[1]));
+        agent_store(dst + 1, pack_bf16x2(s[2], s[3]));
+      }
+    }
+    if (!arrive_last(a.cnt + tb, (uint32_t)n_eb, &flag)) return;
   }
 
-  // ---- workgroup 0: collect the logits, then route and group -------------
-  RouteHiddenLds& L = *(RouteHiddenLds*)smem;
+  // ---- B: K1 for the block's tokens ----------------------------------------
+  {
+    SpreadRouteLds& R = *(SpreadRouteLds*)smem;
+    if (MODE != SP_LOGITS) {
+      const int nw = nt * a.E / 2;
+      const uint32_t* src = (const uint32_t*)(a.logits_out + (size_t)t0 * a.E);
+      for (int i = threadIdx.x; i < nw; i += kSpThreads) R.lg[i] = agent_load(src + i);
+      __syncthreads();
+    }
+    if (wave < nt) {
+      int id;
+      float wt;
+      if (MODE != SP_LOGITS)
+        route_token<VPL, true>(R.lg, wave, a.E, a.k, a.flags, R.sv[wave], R.si[wave], &id, &wt, R.sel[wave]);
+      else
+        route_token<VPL, BF16>(a.logits_in, t0 + wave, a.E, a.k, a.flags, R.sv[wave], R.si[wave], &id, &wt,
+                               R.sel[wave]);
+      const int t = t0 + wave;
+      if (lane < a.k) {
+        agent_store(a.ids + (size_t)t * a.k + lane, id);
+        agent_store((uint32_t*)(a.w + (size_t)t * a.k + lane), __float_as_uint(wt));
+      }
+      wave_lds_sync();
+      if (lane < 2 * VPL) agent_store(a.masks + t * 8 + lane, R.sel[wave][lane]);
+    }
+    if (!arrive_last(a.cnt + kSpMaxBlocks, (uint32_t)n_tb, &flag)) return;
+  }
+
+  // ---- C: K2 over every token --------------------------------------------
+  SpreadGroupLds& G = *(SpreadGroupLds*)smem;
   unsigned res = 0;
   if (wave == 0) {
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int e = VPL * lane + i;
-      res |= (unsigned)(!resident || (e < E && resident[e])) << i;
+      res |= (unsigned)(!a.resident || (e < a.E && a.resident[e])) << i;
     }
   }
-  const int nwords = T * E / 2;
-  bool ok = true;
-  for (int i0 = 0; i0 < nwords; i0 += kGroupThreads) {
-    const int i = i0 + threadIdx.x;
-    if (i < nwords) {
-      uint64_t v = __hip_atomic_load(tagged + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      uint32_t spins = 0;
-      while ((uint32_t)(v >> 32) != gen && spins < kSyncSpinLimit) {
-        __builtin_amdgcn_s_sleep(2);
-        v = __hip_atomic_load(tagged + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        ++spins;
-      }
-      if ((uint32_t)(v >> 32) != gen) {
-        // give up on this word: claim it (0 -> poison, which its writer will
-        // clear), unless the writer's value landed since the last poll
-        uint64_t expect = 0ull;
-        if (__hip_atomic_compare_exchange_strong(tagged + i, &expect, kTagPoison, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT)) {
-          ok = false;
-          v = 0ull;
-        } else {
-          v = expect;
-        }
-      }
-      L.logits[i] = (uint32_t)v;
-      ((uint32_t*)logits)[i] = (uint32_t)v;
-      if (v != 0ull) __hip_atomic_store(tagged + i, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+  const int P = a.T * a.k;
+  for (int i = threadIdx.x; i < P; i += kSpThreads) {
+    G.ids_s[i] = agent_load(a.ids + i);
+    G.w_s[i] = __uint_as_float(agent_load((const uint32_t*)(a.w + i)));
   }
-  const bool all_ok = __syncthreads_and(ok);
-  if (threadIdx.x == 0 && !all_ok) __hip_atomic_store(sync + 31, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  for (int t = wave; t < T; t += kGroupWaves) {
-    int id;
-    float w;
-    route_token<VPL, true>(L.logits, t, E, k, flags, L.sv[wave], L.si[wave], &id, &w, L.selmask[t]);
-    if (!all_ok) w = __builtin_nanf("");
-    if (lane < k) {
-      L.ids_s[t * k + lane] = id;
-      L.w_s[t * k + lane] = w;
-      ids_out[(int64_t)t * k + lane] = id;
-      w_out[(int64_t)t * k + lane] = w;
-    }
+  for (int i = threadIdx.x; i < a.T * 2 * VPL; i += kSpThreads) {
+    const int t = i / (2 * VPL), j = i - t * (2 * VPL);
+    G.selmask[t][j] = agent_load(a.masks + t * 8 + j);
+    agent_store(a.masks + t * 8 + j, 0u);
   }
+  if (threadIdx.x < n_tb) agent_store(a.cnt + threadIdx.x, 0u);
+  if (threadIdx.x == 0) agent_store(a.cnt + kSpMaxBlocks, 0u);
   __syncthreads();
-  if (wave == 0) group_scan<VPL>(L.selmask, T, E, bm, res, L.g);
+  if (wave == 0) group_scan<VPL>(G.selmask, a.T, a.E, a.bm, res, G.g);
   __syncthreads();
-  group_write(L.g, L.ids_s, T, k, E, bm, max_tiles, counts, offsets, perm, inv, tiles, n_tiles, tile_src, L.w_s,
-              wpos);
+  group_write<kSpThreads>(G.g, G.ids_s, a.T, a.k, a.E, a.bm, a.max_tiles, a.counts, a.offsets, a.perm, a.inv, a.tiles,
+                          a.n_tiles, a.tile_src, G.w_s, a.wpos);
 }
 
 // ---------------------------------------------------------------------------
@@ -811,31 +889,68 @@ hipError_t launch_route(const void* logits, int act_bf16, int T, int E, int k, u
 
 bool route_group_fused(int T, int k) { return T <= kFusedRouteMaxTokens && T * k <= kFusedRouteMaxPairs; }
 
-bool route_hidden_fused(int T, int k, int E, int H) {
-  return route_group_fused(T, k) && E % 4 == 0 && E <= kMaxExperts && H % 128 == 0;
+bool route_spread_ok(int T, int k, int E, int H, bool gemv) {
+  if (!route_group_fused(T, k) || E > kMaxExperts) return false;
+  return !gemv || (E % 4 == 0 && H % 128 == 0 && H <= kSpMaxH);
 }
 
-hipError_t launch_route_hidden(const void* x, const void* gate_packed, int H, int T, int E, int k, unsigned flags,
-                               int bm, int max_tiles, void* logits, void* tagged, uint32_t* sync, uint32_t gen,
-                               int32_t* ids,
-                               float* w, int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv,
-                               int32_t* tiles, int32_t* n_tiles, int32_t* tile_src, const uint8_t* resident,
-                               float* wpos, hipStream_t stream) {
+hipError_t launch_route_spread(const void* logits_in, int act_bf16, const void* x, const void* gate_packed,
+                               const void* norm_w, float eps, void* normed, int H, int T, int E, int k,
+                               unsigned flags, int bm, int max_tiles, void* logits_out, uint32_t* sync,
+                               uint32_t* masks, int32_t* ids, float* w, int32_t* counts, int32_t* offsets,
+                               int32_t* perm, int32_t* inv, int32_t* tiles, int32_t* n_tiles, int32_t* tile_src,
+                               const uint8_t* resident, float* wpos, hipStream_t stream) {
   if (T <= 0) return hipSuccess;
-  if (!route_hidden_fused(T, k, E, H) || gen == 0u) return hipErrorInvalidValue;
+  const bool gemv = x != nullptr;
+  if (!route_spread_ok(T, k, E, H, gemv)) return hipErrorInvalidValue;
   if (bm <= 0 || (bm & (bm - 1)) != 0) return hipErrorInvalidValue;
   if (tile_src && bm != kTileSrcCols) return hipErrorInvalidValue;
-  const int NB = (E + kRouterRowsPerBlock - 1) / kRouterRowsPerBlock;
-  dim3 grid(1 + NB), block(64 * kGroupWaves);
-#define NKT_RH_CASE(V)                                                                                   \
-  case V:                                                                                                \
-    hipLaunchKernelGGL((route_hidden_kernel<V>), grid, block, 0, stream, (const uint16_t*)x,              \
-                       (const uint8_t*)gate_packed, H, T, E, k, flags, bm, max_tiles, (uint16_t*)logits,  \
-                       (uint64_t*)tagged, sync, gen, ids, w, counts, offsets, perm, inv, tiles, n_tiles, tile_src, \
-                       resident, wpos);                                                                  \
+  if (!sync || !masks || (gemv ? (!gate_packed || !logits_out || (norm_w && !normed)) : !logits_in))
+    return hipErrorInvalidValue;
+  SpreadArgs a;
+  a.logits_in = logits_in;
+  a.x = (const uint16_t*)x;
+  a.gate = (const uint8_t*)gate_packed;
+  a.norm_w = (const uint16_t*)norm_w;
+  a.eps = eps;
+  a.normed = (uint16_t*)normed;
+  a.logits_out = (uint16_t*)logits_out;
+  a.T = T;
+  a.E = E;
+  a.k = k;
+  a.H = H;
+  a.flags = flags;
+  a.bm = bm;
+  a.max_tiles = max_tiles;
+  a.ids = ids;
+  a.w = w;
+  a.counts = counts;
+  a.offsets = offsets;
+  a.perm = perm;
+  a.inv = inv;
+  a.tiles = tiles;
+  a.n_tiles = n_tiles;
+  a.tile_src = tile_src;
+  a.resident = resident;
+  a.wpos = wpos;
+  a.cnt = sync;
+  a.masks = masks;
+  const int n_tb = (T + kSpTokens - 1) / kSpTokens;
+  const int n_eb = gemv ? (E + kSpExperts - 1) / kSpExperts : 1;
+  dim3 grid(n_tb * n_eb), block(kSpThreads);
+#define NKT_SP_CASE(V)                                                                                       \
+  case V:                                                                                                    \
+    if (!gemv && act_bf16)                                                                                   \
+      hipLaunchKernelGGL((route_spread_kernel<V, SP_LOGITS, true>), grid, block, 0, stream, a);              \
+    else if (!gemv)                                                                                          \
+      hipLaunchKernelGGL((route_spread_kernel<V, SP_LOGITS, false>), grid, block, 0, stream, a);             \
+    else if (norm_w)                                                                                         \
+      hipLaunchKernelGGL((route_spread_kernel<V, SP_GEMV_NORM, true>), grid, block, 0, stream, a);           \
+    else                                                                                                     \
+      hipLaunchKernelGGL((route_spread_kernel<V, SP_GEMV, true>), grid, block, 0, stream, a);                \
     break;
-  NKT_VPL_SWITCH(E, NKT_RH_CASE)
-#undef NKT_RH_CASE
+  NKT_VPL_SWITCH(E, NKT_SP_CASE)
+#undef NKT_SP_CASE
   return hipGetLastError();
 }
 

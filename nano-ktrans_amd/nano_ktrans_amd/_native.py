@@ -55,12 +55,12 @@ WS_ROUTER_LOGITS = 11
 WS_NORMED = 12
 WS_SYNC = 13
 
-# status words inside WS_SYNC (uint32 indices): 1 after a fault, cleared by the caller
+# status word inside WS_SYNC (uint32 index): 1 after a given-routing call dropped a slot,
+# cleared by the caller
 STATUS_BAD_ROUTING = 30
-STATUS_ROUTER_WAIT = 31
 
 # leading bytes of every workspace that must start at zero (every call leaves
-# the tagged words zero, and the status words zero unless it reports a fault)
+# them zero, the status word aside when a call reports a fault)
 SYNC_AREA_BYTES = 65792
 
 EXPORTED_SYMBOLS = (

@@ -321,21 +321,20 @@ class NativeMoE:
 
     # ------------------------------------------------------------------ status
     def status(self) -> Dict[str, int]:
-        """The workspace's status words (synchronises the device): bad_routing (a given-routing call
-        dropped a slot) and router_wait (the single-launch router gave up waiting; its call's routing
-        weights were NaN).  0 = no fault since they were last cleared."""
+        """The workspace's status word (synchronises the device): bad_routing = 1 when a
+        given-routing call dropped a slot since it was last cleared, else 0."""
         if self._ws is None:
-            return {"bad_routing": 0, "router_wait": 0}
+            return {"bad_routing": 0}
         torch.cuda.synchronize(self.device)
         words = self._ws[:128].view(torch.int32).cpu()
-        return {"bad_routing": int(words[N.STATUS_BAD_ROUTING]), "router_wait": int(words[N.STATUS_ROUTER_WAIT])}
+        return {"bad_routing": int(words[N.STATUS_BAD_ROUTING])}
 
     def check_status(self, clear: bool = True) -> None:
         """Raise ``NativeError`` if a status word reports a fault (after clearing it when ``clear``)."""
         st = self.status()
         bad = {k: v for k, v in st.items() if v}
         if bad and clear:
-            self._ws[:128].view(torch.int32)[N.STATUS_BAD_ROUTING:N.STATUS_ROUTER_WAIT + 1].zero_()
+            self._ws[:128].view(torch.int32)[N.STATUS_BAD_ROUTING].zero_()
             torch.cuda.synchronize(self.device)
         if bad:
             raise N.NativeError(f"MoE layer status: {bad}")

@@ -324,7 +324,9 @@ def test_stages_match_forward(gpu_device):
 @pytest.mark.parametrize("name,E,T", [("qwen15_int8_shared", None, 16), ("qwen15_int8_shared", None, 1),
                                       ("qwen3_int4", 32, 16), ("qwen3_int8", 32, 512), ("mixtral_int4", None, 300),
                                       ("qwen3_int4", None, 8), ("mixtral_int4", None, 16),
-                                      ("qwen15_int8_shared", None, 1024)])
+                                      ("qwen15_int8_shared", None, 1024),
+                                      # 17 .. 64 tokens: the several-workgroup route + group launch
+                                      ("qwen3_int4", None, 48), ("qwen15_int8_shared", None, 33)])
 def test_graph_replay_matches_eager(gpu_device, name, E, T):
     """The layer captured in a HIP graph (Qwen1.5-MoE at 1024 tokens: the
     prefill-form shared expert as a branch forked onto the handle's side

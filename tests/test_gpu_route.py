@@ -128,7 +128,7 @@ def test_route_hidden_matches_oracle(gpu_device, name, T):
     it): bf16 logits against the oracle's single rounding of the exact dot
     products (check_router_logits), and routing / grouping of those logits
     bit-exact; the workspace's whole sync area (status words and the single
-    launch's tagged logit words) is left zero."""
+    launch's counters and published masks) is left zero."""
     from nano_ktrans_amd import _native as N
     cfg = CONFIGS[name]
     announce(f"route_hidden {name} T={T}")
@@ -149,15 +149,15 @@ def test_route_hidden_matches_oracle(gpu_device, name, T):
     assert np.array_equal(offsets.cpu().numpy(), ooffsets)
     assert np.array_equal(perm.cpu().numpy(), operm)
     assert np.array_equal(inv.cpu().numpy(), oinv)
-    # the whole sync area (status words and the single launch's tagged logit
-    # words) is left zero
+    # the whole sync area (the single launch's counters and published masks,
+    # the status word) is left zero
     assert not native.workspace(T)[:N.SYNC_AREA_BYTES].any()
     native.check_status()
 
 
 def test_route_hidden_single_launch_replays(gpu_device):
     """The single-launch router + route + group captured in a HIP graph: every
-    replay (the same generation number each time) waits for its own logits --
+    replay (its counters reset by the call before, as every call leaves them) routes its own logits --
     eager calls with other inputs on the same workspace run between replays --
     and equals the eager result bit for bit."""
     from nano_ktrans_amd import _native as N

@@ -88,7 +88,7 @@ def test_forward_routed_matches_oracle(gpu_device, name, E, I, T):
     ref = _oracle_given(layer, x, ids, w)
     err_abs, err_rel = compare(out.float().cpu().numpy(), ref, cfg)
     announce(f"  max_abs={err_abs:.3e} rel_l2={err_rel:.3e}")
-    assert native.status() == {"bad_routing": 0, "router_wait": 0}
+    assert native.status() == {"bad_routing": 0}
 
 
 @pytest.mark.parametrize("name,E,T", [("qwen3_int4", None, 1), ("qwen3_int4", None, 16), ("qwen3_int8", 32, 512),
