@@ -651,6 +651,42 @@ bool shared_side_ready(Handle* h, int T, const WsLayout& L, hipStream_t st) {
   return side_stream_ready(h, st);
 }
 
+// K1 + K2 and the decode gate_up in one launch (launch_gemv_sr): 2 ..
+// kSrMaxTokens tokens from given bf16 logits, no shared-expert chunks,
+// shapes the kernel takes (int4 weights).  Measured (Qwen3 int4 layer,
+// graph replays): T = 2 / 3 / 4 21.0 / 27.0 / 29.1 -> 18.0 / 24.2 / 27.5 us.
+bool sr_ok(const Handle* h, int T, const WsLayout& L, const void* logits, int chunks) {
+  return logits && h->act_bf16 && chunks == 0 && L.bm == kTileSrcCols &&
+         gemv_sr_supported(h->wf, 2 * h->I, h->H, h->I, T, h->E, h->k);
+}
+
+int do_sr_gate_up(Handle* h, const void* x, const void* logits, int T, void* ws, const WsLayout& L,
+                  hipStream_t st, char* err, size_t len) {
+  if (!x) {
+    set_err(err, len, "null hidden_states");
+    return NKT_ERR;
+  }
+  GemmArgs a = expert_args(h, PHASE_GATE_UP, false, x, ws, L, T);
+  a.route_logits = logits;
+  a.route_E = h->E;
+  a.route_flags = h->flags;
+  a.route_T = T;
+  a.ro_resident = h->resident;
+  a.ro_max_tiles = L.max_tiles;
+  a.ro_ids = ws_ptr<int32_t>(ws, L, NKT_WS_TOPK_IDS);
+  a.ro_w = ws_ptr<float>(ws, L, NKT_WS_TOPK_WEIGHTS);
+  a.ro_counts = ws_ptr<int32_t>(ws, L, NKT_WS_COUNTS);
+  a.ro_offsets = ws_ptr<int32_t>(ws, L, NKT_WS_OFFSETS);
+  a.ro_perm = ws_ptr<int32_t>(ws, L, NKT_WS_PERM);
+  a.ro_inv = ws_ptr<int32_t>(ws, L, NKT_WS_INV);
+  a.ro_tiles = ws_ptr<int32_t>(ws, L, kWsTiles);
+  a.ro_n_tiles = ws_ptr<int32_t>(ws, L, kWsNTiles);
+  a.ro_tile_src = ws_ptr<int32_t>(ws, L, kWsTileSrc);
+  a.ro_wpos = ws_ptr<float>(ws, L, kWsWpos);
+  if (!check_hip(launch_gemv_sr(a, h->wf, 0, st), "routing gate_up gemm", err, len)) return NKT_ERR;
+  return NKT_OK;
+}
+
 // Routing (route(st)), the routed experts, the shared expert and the combine
 // of one layer call.  The shared expert forks onto the side stream after
 // everything the caller queued on st (its input is ready) and joins back
@@ -742,6 +778,8 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
       if (!check_hip(launch_expert_gemm(h, a, PHASE_GATE_UP, L.bm, route_tiles, st), "routing gate_up gemm", err,
                      len))
         return NKT_ERR;
+    } else if (sr_ok(h, T, L, logits, chunks)) {
+      rc = do_sr_gate_up(h, x, logits, T, ws, L, st, err, len);
     } else {
       rc = route();
       if (rc == NKT_OK) rc = do_expert_phase(h, PHASE_GATE_UP, x, T, ws, L, st, err, len, nullptr, false, chunks);
@@ -772,7 +810,10 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
   const bool prep_in_route = logits && L.bm == kPrefillTileM && g.in16 && g.xinv &&
                              gemm2_supported(h->wf, PHASE_GATE_UP, g.N, g.K, g.I) && gemm2_i8_pipeline(g, h->wf);
   bool prep_done = false;
-  int rc = prep_in_route ? do_route(h, logits, T, ws, L, st, err, len, &g, &prep_done) : route();
+  // a few tokens from given logits: routing inside the gate_up launch
+  const bool sr = sr_ok(h, T, L, logits, chunks);
+  int rc = sr ? do_sr_gate_up(h, x, logits, T, ws, L, st, err, len)
+              : prep_in_route ? do_route(h, logits, T, ws, L, st, err, len, &g, &prep_done) : route();
   // a shared expert in the prefill form forks here, once the routing launch
   // has made the fp16 input copy both expert GEMMs read: its launches (a
   // dense down of few workgroups among them) run beside the routed experts'
@@ -798,7 +839,9 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
     }
     late = true;
   }
-  if (rc == NKT_OK) rc = do_experts(h, x, T, ws, L, st, err, len, true, chunks, prep_done);
+  if (rc == NKT_OK)
+    rc = sr ? do_expert_phase(h, PHASE_DOWN, x, T, ws, L, st, err, len, nullptr, true, chunks)
+            : do_experts(h, x, T, ws, L, st, err, len, true, chunks, prep_done);
   if (rc == NKT_OK && !side && !late && h->Is > 0 && chunks == 0)
     rc = do_shared(h, x, T, ws, L, st, err, len, prep_done);
   if (side || late) {

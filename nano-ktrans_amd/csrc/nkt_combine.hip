@@ -37,6 +37,7 @@ __global__ void __launch_bounds__(256) shared_gate_kernel(const void* __restrict
 // the row stays in registers)
 __device__ __forceinline__ void combine_tail(f32x4 acc, int t, int col, int H, const void* extra, bool shared,
                                              f32x4 vs, float sg, const void* residual, void* out, int out_bf16) {
+#pragma clang fp contract(off)
   const int64_t o = (int64_t)t * H + col;
   if (extra) {
     if (out_bf16)

@@ -32,6 +32,7 @@
 // the offset times the group's activation sum is removed per group, the bf16
 // scale multiplies each group's fp32 partial (int4) or the row total (int8).
 #include "nkt_common.h"
+#include "nkt_group.h"
 #include "nkt_internal.h"
 #include "nkt_route_token.h"
 
@@ -175,6 +176,9 @@ __device__ __forceinline__ void pin_slot(WSlot<WF, NT>& r) {
 template <int WF, int NT, class BOp>
 __device__ __forceinline__ void mma_group_b(const WSlot<WF, NT>& r, BOp bop, float xs, f32x4 (&acc)[NT], bool use,
                                             const DqConst& k) {
+  // scale x partial, then + acc, each rounded: never fused, so every kernel
+  // that accumulates a tile here gets the same bits
+#pragma clang fp contract(off)
   const float c = WF == WF_I4 ? -136.0f * xs : WF == WF_I8 ? -128.0f * xs : 0.0f;
   f32x4 tmp[NT];
 #pragma unroll
@@ -202,6 +206,7 @@ __device__ __forceinline__ void mma_group_b(const WSlot<WF, NT>& r, BOp bop, flo
 template <int WF, int NT>
 __device__ __forceinline__ void mma_group(const WSlot<WF, NT>& r, const u32x4 (&xb)[4], float xs,
                                           f32x4 (&acc)[NT], bool use) {
+#pragma clang fp contract(off)
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     f32x4 tmp;
@@ -675,6 +680,147 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
 }
 
 // ---------------------------------------------------------------------------
+// Decode gate_up that routes its tokens itself (2 .. kSrMaxTokens tokens,
+// given bf16 logits), so no routing launch precedes it.  Grid: x = blocks of
+// P row sets, y = 1 + lanes.
+//   * Workgroup (0, 0) runs K1 + K2 for every token (route_group_body, the
+//     routing kernels' code) and writes their outputs for the down GEMV and
+//     the combine, which run after this launch; workgroups (x > 0, 0) end.
+//   * Every other workgroup finds the token sets itself: wave w selects
+//     tokens w, w + waves, ... (route_mask: K1's selection bits), wave 0
+//     transposes the token masks into per-expert masks M_e and scans
+//     count_e in expert order, so expert e's first position is K2's
+//     offset_e and token t's position is offset_e + its rank in M_e (K2's
+//     order); the HBM-resident experts with tokens are listed in id order.
+//     Lane y - 1 of the row set block takes listed experts y - 1,
+//     y - 1 + lanes, ...: each is one tile of at most 16 positions (its rows
+//     gathered from x by M_e), computed as gemv_kernel computes a routed
+//     tile, the K parts added in order, h stored at the positions.
+// The lane loop meets at two workgroup barriers per expert (the K-part sums
+// in LDS, then the LDS regions free for the next expert's staging).
+// ---------------------------------------------------------------------------
+template <int S, int P, int kRegion>
+struct SrLds {
+  uint8_t region[S * P][kRegion];
+  uint32_t selmask[kSrMaxTokens][8];
+  int32_t act_e[kMaxExperts];
+  int32_t act_off[kMaxExperts];
+  uint32_t act_m[kMaxExperts];
+  int32_t n_act;
+};
+
+template <int WF, int RT, int S, int NG, int P, int VPL>
+__global__ void __launch_bounds__(S * P * 64) gemv_sr_kernel(GemmArgs a, int n_rowsets) {
+  constexpr int NT = 2 * RT;
+  constexpr int kWaves = S * P;
+  constexpr int D = (WF == WF_BF16) ? 2 : 3;
+  constexpr int kStageX = NG * 1024;
+  constexpr int kStageS = (WF == WF_I4) ? NT * NG * 32 : 0;
+  constexpr int kRed = S > 1 ? NT * 1024 : 0;
+  constexpr int kRegion = (kStageX + kStageS > kRed ? kStageX + kStageS : kRed) > 16
+                              ? (kStageX + kStageS > kRed ? kStageX + kStageS : kRed)
+                              : 16;
+  union SrShared {
+    SrLds<S, P, kRegion> ex;
+    RouteGroupLds<kSrMaxTokens, kSrMaxTokens * kMaxTopK, kWaves> rt;
+  };
+  __shared__ __attribute__((aligned(16))) SrShared lds;
+
+  const int T = a.route_T;
+  const int E = a.route_E;
+  const int k = a.topk;
+  const int wave = threadIdx.x >> 6;
+  const uint32_t lane = threadIdx.x & 63;
+  if (blockIdx.y == 0) {
+    if (blockIdx.x != 0) return;
+    route_group_body<VPL, true, kWaves>(a.route_logits, T, E, k, a.route_flags, kTileSrcCols, a.ro_max_tiles,
+                                        a.ro_ids, a.ro_w, a.ro_counts, a.ro_offsets, a.ro_perm, a.ro_inv, a.ro_tiles,
+                                        a.ro_n_tiles, a.ro_tile_src, a.ro_resident, a.ro_wpos, lds.rt);
+    return;
+  }
+  SrLds<S, P, kRegion>& L = lds.ex;
+  // residency of the scan lane's experts, read before the selection
+  unsigned res = 0;
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int e = VPL * (int)lane + i;
+      res |= (unsigned)(!a.ro_resident || (e < E && a.ro_resident[e])) << i;
+    }
+  }
+  for (int t = wave; t < T; t += kWaves) route_mask<VPL, true>(a.route_logits, t, E, k, a.route_flags, L.selmask[t]);
+  __syncthreads();
+  if (wave == 0) {
+    uint32_t m[VPL];
+    int cnt[VPL], act[VPL];
+    int lane_val = 0;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int e = VPL * (int)lane + i;
+      m[i] = 0u;
+      for (int t = 0; t < T; ++t) m[i] |= ((L.selmask[t][(e >> 5) & 7] >> (e & 31)) & 1u) << t;
+      if (e >= E) m[i] = 0u;
+      cnt[i] = __popc(m[i]);
+      act[i] = (cnt[i] > 0 && ((res >> i) & 1u)) ? 1 : 0;
+      lane_val += cnt[i] | (act[i] << 16);
+    }
+    const int incl = wave_inclusive_scan(lane_val);
+    int run = incl - lane_val;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int r = run >> 16;
+      if (act[i]) {
+        L.act_e[r] = VPL * (int)lane + i;
+        L.act_off[r] = run & 0xffff;
+        L.act_m[r] = m[i];
+      }
+      run += cnt[i] | (act[i] << 16);
+    }
+    if (lane == 63) L.n_act = incl >> 16;
+  }
+  __syncthreads();
+
+  const int n_act = L.n_act;
+  const int lanes = gridDim.y - 1;
+  const int col = lane & 15;
+  const int kpart = wave % S;
+  const int rs_raw = blockIdx.x * P + wave / S;
+  const bool rs_ok = rs_raw < n_rowsets;
+  const int rowset = rs_ok ? rs_raw : 0;
+  const int orow0 = rowset * RT * 16;
+  uint8_t* region = L.region[__builtin_amdgcn_readfirstlane(wave)];
+  for (int j = blockIdx.y - 1; j < n_act; j += lanes) {
+    const int expert = L.act_e[j];
+    const int row0 = L.act_off[j];
+    const uint32_t msk = L.act_m[j];
+    const int rows = __popc(msk);
+    const int src = nth_set_bit(msk, col < rows ? col : 0);
+    const int srcq = nth_set_bit(msk, (int)(col & 3) < rows ? (col & 3) : 0);
+    const TileSrc ts = routed_src(a, expert);
+    f32x4 acc[NT];
+    gemv_accumulate<WF, PHASE_GATE_UP, RT, S, NG, D, true>(a, ts, rows, src, srcq, kpart, rowset, region, lane, acc);
+    if (S > 1) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) *(f32x4*)(region + t * 1024 + lane * 16) = acc[t];
+      __syncthreads();
+      if (kpart == 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          f32x4 sum = *(const f32x4*)(L.region[wave] + t * 1024 + lane * 16);
+#pragma unroll
+          for (int kk = 1; kk < S; ++kk) sum += *(const f32x4*)(L.region[wave + kk] + t * 1024 + lane * 16);
+          acc[t] = sum;
+        }
+        if (rs_ok) gemv_epilogue<WF, PHASE_GATE_UP, RT>(a, acc, rows, row0, orow0, ts.s, ts.up, a.out, ts.hstride, lane, 0);
+      }
+      __syncthreads();
+    } else if (rs_ok) {
+      gemv_epilogue<WF, PHASE_GATE_UP, RT>(a, acc, rows, row0, orow0, ts.s, ts.up, a.out, ts.hstride, lane, 0);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Down projection + combine for a few tokens (T <= kDcMaxTokens).  Workgroup
 // (row set, t) owns 16 output rows of token t: its waves take the (pair,
 // K part) items of the token's k pairs -- pair j's position inv[t k + j] (its
@@ -743,6 +889,10 @@ __global__ void __launch_bounds__(64 * kDcWaves) gemv_down_combine_kernel(GemmAr
   }
   __syncthreads();
   if (threadIdx.x >= 16) return;
+  {
+  // every product rounded before it is added, as combine_kernel adds its
+  // terms (never fused into an FMA): the same bits as the separate launches
+#pragma clang fp contract(off)
   // thread r: output row orow0 + r (tile row r = 4 (r / 4) + r % 4 of lane group r / 4)
   const int r = threadIdx.x;
   const int orow = rowset * 16 + r;
@@ -770,6 +920,7 @@ __global__ void __launch_bounds__(64 * kDcWaves) gemv_down_combine_kernel(GemmAr
   }
   if (c.residual) acc += bf16_bits_to_f32(((const uint16_t*)c.residual)[o]);
   ((uint16_t*)c.out)[o] = (uint16_t)f32_to_bf16_bits(acc);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -930,6 +1081,36 @@ hipError_t launch_gemv_wf(const GemmArgs& a, int phase, int max_tiles, hipStream
   return launch_gemv_rt<WF, PHASE_DOWN, kGemvRtDown>(a, max_tiles, stream, tm);
 }
 
+// the decode gate_up's K split (launch_gemv_rt), so h has the same bits
+void gemv_split(int wf, int K, int& S, int& NG) {
+  const int G = K / 128;
+  const int target = gemv_target_groups(wf);
+  S = (G + target - 1) / target;
+  if (S > 8) S = 8;
+  if (S == 5 || S == 7) ++S;
+  NG = (G + S - 1) / S;
+}
+
+// Lanes of the self-routing gate_up: each active expert a lane of its own
+// up to kSrLanes, more experts shared out over them.  Measured (Qwen3 int4,
+// given logits, per layer): T = 2 / 3 / 4 21.0 / 27.0 / 29.1 us with the
+// routing launch against 18.0 / 24.2 / 27.5 us at 16 lanes (24, 32, 48 and
+// 64 lanes, and 4 lanes at T = 2, slower); T = 8 / 16 40 / 53 against 40.4 / 58.5 at 16
+// lanes and more with more lanes (every workgroup selects every token, so
+// the selection work grows with both), and slower again with two or four
+// row sets per workgroup (fewer, fatter workgroups): hence at most
+// kSrMaxTokens tokens.
+constexpr int kSrLanes = 16;
+
+template <int WF>
+hipError_t launch_gemv_sr_wf(const GemmArgs& a, int lanes, hipStream_t stream, const KernelTimer* tm) {
+  constexpr int S = 4, NG = 4, P = 1;  // the split gemv_sr_supported admits, one row set per workgroup
+  const int n_rowsets = a.I / (kGemvRtGateUp * 16);
+  dim3 grid((n_rowsets + P - 1) / P, 1 + lanes);
+  launch_timed(gemv_sr_kernel<WF, kGemvRtGateUp, S, NG, P, 2>, grid, dim3(S * P * 64), 0, stream, tm, a, n_rowsets);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 bool gemv_supported(int wf, int phase, int N, int K, int I) {
@@ -983,6 +1164,31 @@ hipError_t launch_down_combine(const GemmArgs& a, const CombineTail& c, int wf, 
     default:
       return hipErrorInvalidValue;
   }
+}
+
+bool gemv_sr_supported(int wf, int N, int K, int I, int T, int E, int k) {
+  // int8 (Qwen3 shape, T = 2 / 3 / 4): 30.3 / 35.5 / 40.4 us with the
+  // routing launch against 30.3 / 35.6 / 43.6 self-routed -- the longer
+  // int8 GEMV gains nothing from the launch it saves
+  if (wf != WF_I4) return false;
+  if (!gemv_supported(wf, PHASE_GATE_UP, N, K, I)) return false;
+  int S = 0, NG = 0;
+  gemv_split(wf, K, S, NG);
+  if (S != 4 || NG != 4 || K != 128 * S * NG) return false;
+  return T >= 2 && T <= kSrMaxTokens && E > 64 && E <= 128 && k >= 1 && k <= kMaxTopK;
+}
+
+hipError_t launch_gemv_sr(const GemmArgs& a, int wf, int lanes, hipStream_t stream, const KernelTimer* tm) {
+  if (!gemv_sr_supported(wf, a.N, a.K, a.I, a.route_T, a.route_E, a.topk) || !a.route_logits || !a.act_bf16 ||
+      !a.out || !a.ro_ids || !a.ro_w || !a.ro_counts || !a.ro_offsets || !a.ro_perm || !a.ro_inv || !a.ro_tiles ||
+      !a.ro_n_tiles || a.ro_max_tiles < 1 || a.sh_chunks != 0)
+    return hipErrorInvalidValue;
+  if (lanes <= 0) {
+    const int most = a.route_T * a.topk < a.route_E ? a.route_T * a.topk : a.route_E;
+    lanes = most < kSrLanes ? most : kSrLanes;
+  }
+  if (lanes > kMaxExperts) lanes = kMaxExperts;
+  return launch_gemv_sr_wf<WF_I4>(a, lanes, stream, tm);
 }
 
 hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream,

@@ -78,6 +78,11 @@ struct GemmArgs {
   int32_t* ro_n_tiles;
   int32_t* ro_tile_src;
   float* ro_wpos;
+  // decode gate_up of 2 .. kSrMaxTokens tokens that routes them itself
+  // (launch_gemv_sr): route_T tokens of route_logits [route_T, route_E];
+  // ro_resident (nullable) the experts' HBM residency, as K2 takes it
+  int route_T;
+  const uint8_t* ro_resident;
   // decode form with a shared expert of intermediate size sh_I =
   // sh_chunks x I (sh_chunks > 0): the shared expert rides in the routed
   // launches.  Chunk c is an expert of the routed shape cut from the shared
@@ -201,6 +206,17 @@ hipError_t launch_gemv(const GemmArgs& a, int wf, int phase, int max_tiles, hipS
 // Workgroups of a decode-form launch (gemv_supported shapes; the down
 // launch at its two-tile row sets).
 int64_t gemv_workgroups(int wf, int phase, int N, int K, int I, int max_tiles);
+
+// Decode gate_up that routes its own tokens (given bf16 logits, 2 ..
+// kSrMaxTokens tokens, so every expert's tokens make one tile): one launch does
+// K1 + K2 (one workgroup, writing the ro_* outputs as the routing kernels
+// do) and the gate_up GEMV, whose workgroups each find the experts' token
+// sets from the logits themselves.  gemv_sr_supported says which shapes it
+// takes; lanes: workgroups per row set block sharing the active experts
+// (0: the library's choice).
+constexpr int kSrMaxTokens = 4;
+bool gemv_sr_supported(int wf, int N, int K, int I, int T, int E, int k);
+hipError_t launch_gemv_sr(const GemmArgs& a, int wf, int lanes, hipStream_t stream, const KernelTimer* tm = nullptr);
 
 // The combine's inputs beyond y for the down + combine kernel of T tokens:
 // routing weights w, expert ids and pair positions inv [T, k] (written by

@@ -41,18 +41,14 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Route one token with the whole wavefront.  sv/si: this wave's 16-entry LDS
-// scratch (selected values / ids in slot order).  Returns, in lanes < k, the
-// slot's expert id and weight; lanes >= k return id -1.
-// selmask (nullable, LDS): the token's selected experts as a bit mask, bit
-// e of 32-bit word e / 32, written by lane 0.
+// The selection of one token with the whole wavefront: lane l's values
+// v[j] (expert l + 64 j; the rounded probabilities for softmax arches, else
+// the logits) and whether that expert is among the token's k.
 template <int VPL, bool BF16>
-__device__ __forceinline__ void route_token(const void* __restrict__ logits, int t, int E, int k,
-                                            unsigned flags, float* sv, int* si, int* out_id,
-                                            float* out_w, uint32_t* selmask = nullptr) {
+__device__ __forceinline__ void route_select(const void* __restrict__ logits, int t, int E, int k, unsigned flags,
+                                             float (&v)[VPL], bool (&sel)[VPL]) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  float v[VPL];
   bool valid[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
@@ -68,8 +64,6 @@ __device__ __forceinline__ void route_token(const void* __restrict__ logits, int
   }
 
   const bool use_softmax = flags & 1u;
-  const bool renorm = flags & 2u;
-
   if (use_softmax) {
     float m = v[0];
 #pragma unroll
@@ -113,7 +107,6 @@ __device__ __forceinline__ void route_token(const void* __restrict__ logits, int
 #pragma unroll
   for (int j = 0; j < VPL; ++j) above += __popcll(ballot64(key[j] > tau));
   const int need_eq = k - above;  // >= 1 ties at tau, lowest ids first
-  bool sel[VPL];
   int eq_before = 0;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
@@ -122,6 +115,44 @@ __device__ __forceinline__ void route_token(const void* __restrict__ logits, int
     sel[j] = key[j] > tau || (key[j] == tau && r < need_eq);
     eq_before += __popcll(m);
   }
+}
+
+// The token's selected experts as a bit mask (bit e of 32-bit word e / 32,
+// words 0 .. 2 VPL - 1), written to selmask (LDS) by lane 0: the selection of
+// route_token without its slots and weights.
+template <int VPL, bool BF16>
+__device__ __forceinline__ void route_mask(const void* __restrict__ logits, int t, int E, int k, unsigned flags,
+                                           uint32_t* selmask) {
+  float v[VPL];
+  bool sel[VPL];
+  route_select<VPL, BF16>(logits, t, E, k, flags, v, sel);
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const uint64_t m = ballot64(sel[j]);
+    if (lane == 0) {
+      selmask[2 * j] = (uint32_t)m;
+      selmask[2 * j + 1] = (uint32_t)(m >> 32);
+    }
+  }
+}
+
+// Route one token with the whole wavefront.  sv/si: this wave's 16-entry LDS
+// scratch (selected values / ids in slot order).  Returns, in lanes < k, the
+// slot's expert id and weight; lanes >= k return id -1.
+// selmask (nullable, LDS): the token's selected experts as a bit mask, bit
+// e of 32-bit word e / 32, written by lane 0.
+template <int VPL, bool BF16>
+__device__ __forceinline__ void route_token(const void* __restrict__ logits, int t, int E, int k,
+                                            unsigned flags, float* sv, int* si, int* out_id,
+                                            float* out_w, uint32_t* selmask = nullptr) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  float v[VPL];
+  bool sel[VPL];
+  route_select<VPL, BF16>(logits, t, E, k, flags, v, sel);
+  const bool use_softmax = flags & 1u;
+  const bool renorm = flags & 2u;
 
   // ---- the k selected elements into lanes 0..k-1, ascending id ----------
   int before = 0;
