@@ -251,7 +251,10 @@ int nkt_moe_route_hidden(void* handle, const void* hidden_states, int num_tokens
 /* The whole layer from hidden states alone: nkt_moe_route_hidden, then the
  * experts, shared expert and combine of nkt_moe_forward.  Replaces
  * router_logits = self.gate(x); HybridMoE.forward(x, router_logits)
- * (nano_ktrans/models/mixtral.py:212-218). */
+ * (nano_ktrans/models/mixtral.py:212-218).  Up to 16 tokens the router GEMV
+ * is a launch of its own (the logits to NKT_WS_ROUTER_LOGITS, the sync area
+ * untouched) and the layer then runs exactly as nkt_moe_forward on those
+ * logits (the same launches and bits). */
 int nkt_moe_forward_hidden(void* handle, const void* hidden_states, int num_tokens, void* out,
                            void* workspace, size_t workspace_bytes, void* stream, char* err,
                            size_t err_len);
@@ -259,10 +262,10 @@ int nkt_moe_forward_hidden(void* handle, const void* hidden_states, int num_toke
 /* The decoder layer's MoE half (nano_ktrans/models/mixtral.py:206-223):
  * x = RMSNorm(hidden_states) with norm_weight [H] (bf16, device) and eps as
  * nano_ktrans/layers/norm.py:11-17 computes it (written to NKT_WS_NORMED;
- * inside the routing launch when nkt_moe_route_hidden's one-launch form takes
- * the batch), then the layer from x as nkt_moe_forward_hidden, and out =
- * hidden_states + that output (the residual add inside the combine's fp32
- * sum).  bf16 only. */
+ * inside the router's launch -- the router GEMV alone up to 16 tokens,
+ * nkt_moe_route_hidden's one-launch form up to 64), then the layer from x as
+ * nkt_moe_forward_hidden, and out = hidden_states + that output (the
+ * residual add inside the combine's fp32 sum).  bf16 only. */
 int nkt_moe_forward_block(void* handle, const void* hidden_states, const void* norm_weight, float eps,
                           int num_tokens, void* out, void* workspace, size_t workspace_bytes, void* stream,
                           char* err, size_t err_len);

@@ -466,6 +466,35 @@ int do_route_hidden(Handle* h, const void* x, int T, void* ws, const WsLayout& L
   return do_route(h, ws_ptr<void>(ws, L, NKT_WS_ROUTER_LOGITS), T, ws, L, st, err, len);
 }
 
+// Batches of up to kLogitsFirstMaxTokens from hidden states: the router GEMV
+// (with the decoder block's RMSNorm) as a launch of its own -- phase A of
+// the single-launch router -- then the layer as from given logits (routing
+// inside the gate_up launch for one token, the self-routing gate_up for 2 ..
+// 4, the one-workgroup route + group launch up to 16).  Measured (Qwen3
+// int4, graph replays, us per layer, single launch -> this): hidden states
+// T = 1 / 2 / 4 / 8 / 16 22.7 / 26.6 / 36.7 / 46.7 / 58.6 -> 18.8 / 22.8 /
+// 33.2 / 45.2 / 57.8, decoder block 26.7 / 31.4 / 40.9 / 51.1 / 63.5 ->
+// 23.0 / 26.8 / 37.4 / 49.6 / 62.1; at T = 24 .. 64 within +-1 us either
+// way (the decoder block up to 3 us slower), so the single launch stays there.
+constexpr int kLogitsFirstMaxTokens = 16;
+
+bool logits_first(const Handle* h, int T) {
+  return T <= kLogitsFirstMaxTokens && route_spread_ok(T, h->k, h->E, h->H, true);
+}
+
+int do_router_logits(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipStream_t st, char* err,
+                     size_t len, const void* norm_w = nullptr, float eps = 0.f) {
+  if (!check_route_hidden(h, x, err, len)) return NKT_ERR;
+  if (!check_hip(launch_route_spread(nullptr, 1, x, h->w[NKT_SLOT_ROUTER], norm_w, eps,
+                                     norm_w ? ws_ptr<void>(ws, L, NKT_WS_NORMED) : nullptr, h->H, T, h->E, h->k,
+                                     h->flags, L.bm, L.max_tiles, ws_ptr<void>(ws, L, NKT_WS_ROUTER_LOGITS), nullptr,
+                                     nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
+                                     nullptr, nullptr, nullptr, st, true),
+                 norm_w ? "rmsnorm + router kernel" : "router kernel", err, len))
+    return NKT_ERR;
+  return NKT_OK;
+}
+
 // K3 launch for one projection: the decode form for tiles of at most 16
 // positions, the prefill form for its tiles, the tiled form otherwise.
 // The prefill form's gate_up first sums the activations per 128-wide group
@@ -1254,6 +1283,12 @@ int nkt_moe_forward_hidden(void* handle, const void* hidden_states, int num_toke
   if (!check_route_hidden(h, hidden_states, err, err_len)) return NKT_ERR;
   const WsLayout L = ws_layout(h, num_tokens);
   hipStream_t st = (hipStream_t)stream;
+  if (logits_first(h, num_tokens)) {
+    if (do_router_logits(h, hidden_states, num_tokens, workspace, L, st, err, err_len) != NKT_OK) return NKT_ERR;
+    const void* lg = ws_ptr<void>(workspace, L, NKT_WS_ROUTER_LOGITS);
+    return run_layer(h, hidden_states, num_tokens, out, workspace, L, st, err, err_len,
+                     [&] { return do_route(h, lg, num_tokens, workspace, L, st, err, err_len); }, nullptr, true, lg);
+  }
   return run_layer(h, hidden_states, num_tokens, out, workspace, L, st, err, err_len,
                    [&] { return do_route_hidden(h, hidden_states, num_tokens, workspace, L, st, err, err_len); });
 }
@@ -1280,6 +1315,14 @@ int nkt_moe_forward_block(void* handle, const void* hidden_states, const void* n
   hipStream_t st = (hipStream_t)stream;
   void* x = ws_ptr<void>(workspace, L, NKT_WS_NORMED);
   if (!check_route_hidden(h, x, err, err_len) || !check_weights(h, h->Is > 0, err, err_len)) return NKT_ERR;
+  if (logits_first(h, num_tokens)) {
+    if (do_router_logits(h, hidden_states, num_tokens, workspace, L, st, err, err_len, norm_weight, eps) != NKT_OK)
+      return NKT_ERR;
+    const void* lg = ws_ptr<void>(workspace, L, NKT_WS_ROUTER_LOGITS);
+    return run_layer(h, x, num_tokens, out, workspace, L, st, err, err_len,
+                     [&] { return do_route(h, lg, num_tokens, workspace, L, st, err, err_len); }, hidden_states, true,
+                     lg);
+  }
   // the routing launch normalises x itself (and writes NKT_WS_NORMED, which
   // the experts read) whenever it takes the batch
   return run_layer(h, x, num_tokens, out, workspace, L, st, err, err_len,

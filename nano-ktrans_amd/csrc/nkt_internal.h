@@ -163,7 +163,7 @@ hipError_t launch_route_spread(const void* logits_in, int act_bf16, const void* 
                                unsigned flags, int bm, int max_tiles, void* logits_out, uint32_t* sync,
                                uint32_t* masks, int32_t* ids, float* w, int32_t* counts, int32_t* offsets,
                                int32_t* perm, int32_t* inv, int32_t* tiles, int32_t* n_tiles, int32_t* tile_src,
-                               const uint8_t* resident, float* wpos, hipStream_t stream);
+                               const uint8_t* resident, float* wpos, hipStream_t stream, bool gemv_only = false);
 
 // K2 over many workgroups (large batches): hist holds group_hist_blocks(T*k) x E int32.
 int group_hist_blocks(int P);

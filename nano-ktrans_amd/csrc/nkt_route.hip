@@ -329,6 +329,7 @@ struct SpreadArgs {
   float* wpos;
   uint32_t* cnt;      // sync words: [0, kSpMaxBlocks) per token block, [kSpMaxBlocks] all blocks
   uint32_t* masks;    // [T][8] published selection masks (zero between calls)
+  int gemv_only;      // SP_GEMV*: phase A alone (logits, normalised rows); no sync words touched
 };
 
 template <typename Tv>
@@ -470,6 +471,7 @@ __global__ void __launch_bounds__(kSpThreads) route_spread_kernel(SpreadArgs a) 
         agent_store(dst + 1, pack_bf16x2(s[2], s[3]));
       }
     }
+    if (a.gemv_only) return;  // a later launch reads the logits
     if (!arrive_last(a.cnt + tb, (uint32_t)n_eb, &flag)) return;
   }
 
@@ -713,14 +715,16 @@ hipError_t launch_route_spread(const void* logits_in, int act_bf16, const void* 
                                unsigned flags, int bm, int max_tiles, void* logits_out, uint32_t* sync,
                                uint32_t* masks, int32_t* ids, float* w, int32_t* counts, int32_t* offsets,
                                int32_t* perm, int32_t* inv, int32_t* tiles, int32_t* n_tiles, int32_t* tile_src,
-                               const uint8_t* resident, float* wpos, hipStream_t stream) {
+                               const uint8_t* resident, float* wpos, hipStream_t stream, bool gemv_only) {
   if (T <= 0) return hipSuccess;
   const bool gemv = x != nullptr;
-  if (!route_spread_ok(T, k, E, H, gemv)) return hipErrorInvalidValue;
-  if (bm <= 0 || (bm & (bm - 1)) != 0) return hipErrorInvalidValue;
-  if (tile_src && bm != kTileSrcCols) return hipErrorInvalidValue;
-  if (!sync || !masks || (gemv ? (!gate_packed || !logits_out || (norm_w && !normed)) : !logits_in))
-    return hipErrorInvalidValue;
+  if (!route_spread_ok(T, k, E, H, gemv) || (gemv_only && !gemv)) return hipErrorInvalidValue;
+  if (gemv ? (!gate_packed || !logits_out || (norm_w && !normed)) : !logits_in) return hipErrorInvalidValue;
+  if (!gemv_only) {
+    if (bm <= 0 || (bm & (bm - 1)) != 0) return hipErrorInvalidValue;
+    if (tile_src && bm != kTileSrcCols) return hipErrorInvalidValue;
+    if (!sync || !masks) return hipErrorInvalidValue;
+  }
   SpreadArgs a;
   a.logits_in = logits_in;
   a.x = (const uint16_t*)x;
@@ -749,6 +753,7 @@ hipError_t launch_route_spread(const void* logits_in, int act_bf16, const void* 
   a.wpos = wpos;
   a.cnt = sync;
   a.masks = masks;
+  a.gemv_only = gemv_only ? 1 : 0;
   const int n_tb = (T + kSpTokens - 1) / kSpTokens;
   const int n_eb = gemv ? (E + kSpExperts - 1) / kSpExperts : 1;
   dim3 grid(n_tb * n_eb), block(kSpThreads);

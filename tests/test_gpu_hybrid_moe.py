@@ -264,7 +264,7 @@ class _RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(H))
 
 
-@pytest.mark.parametrize("T", [1, 16, 300])
+@pytest.mark.parametrize("T", [1, 16, 40, 300])
 def test_fused_decoder_block(gpu_device, T):
     """FusedMoEBlock: hidden + MoE(RMSNorm(hidden)) with the fused router.  The
     RMSNorm output matches the oracle's within one bf16 step, the logits pass

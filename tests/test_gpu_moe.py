@@ -381,12 +381,15 @@ def test_timed_phases_match_untimed(gpu_device, name, T):
 
 
 @pytest.mark.parametrize("name,E,T", [("qwen3_int4", 32, 16), ("qwen3_int8", 32, 512), ("mixtral_int4", None, 1),
-                                      ("qwen15_int8_shared", None, 16), ("qwen3_int4", None, 4)])
+                                      ("qwen15_int8_shared", None, 16), ("qwen3_int4", None, 4),
+                                      # router GEMV launch, then one token routed inside gate_up / the
+                                      # self-routing gate_up; 17 .. 64 tokens: the single-launch router
+                                      ("qwen3_int4", None, 1), ("qwen3_int4", None, 2), ("qwen3_int4", None, 40)])
 def test_forward_hidden_fused_router(gpu_device, name, E, T):
     """The layer from hidden states alone (router GEMV fused): logits checked
     against the oracle's (check_router_logits), the output equal to the
     oracle's forward on the GPU's logits within the bf16 tolerance, and to
-    nkt_moe_forward on them bit for bit."""
+    nkt_moe_forward on them bit for bit; the sync area is left zero."""
     from nano_ktrans_amd import _native as N
     from moe_cases import check_router_logits
     announce(f"forward_hidden {name} E={E} T={T}")
