@@ -356,24 +356,37 @@ __device__ __forceinline__ bool arrive_last(uint32_t* c, uint32_t n, uint32_t* f
 
 // RMSNorm of one bf16 row with the whole wave (rmsnorm_kernel's order: lane
 // l adds its 8-column chunks l, l + 64, ... in order, then a fixed
-// butterfly); the result to dst0 (LDS) and, when non-null, dst1.
+// butterfly); the result to dst0 (LDS) and, when non-null, dst1.  The first
+// kNormKept chunks of the lane (H <= 4096) stay in registers for the second
+// pass, so it reads x only once (further chunks are read again).
+constexpr int kNormKept = 8;
+
 __device__ __forceinline__ void rms_norm_row(const uint16_t* __restrict__ xr, const uint16_t* __restrict__ wr,
                                              float eps, int H, uint16_t* dst0, uint16_t* dst1) {
   const int lane = threadIdx.x & 63;
-  float ss = 0.f;
-  for (int c = lane * 8; c < H; c += 512) {
-    const u32x4 v = *(const u32x4*)(xr + c);
+  u32x4 kept[kNormKept];
+#pragma unroll
+  for (int i = 0; i < kNormKept; ++i) {
+    const int c = lane * 8 + 512 * i;
+    kept[i] = c < H ? *(const u32x4*)(xr + c) : u32x4{0u, 0u, 0u, 0u};
+  }
+  auto add_sq = [](float ss, u32x4 v) {
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
       const float a = __uint_as_float(v[h] << 16), b = __uint_as_float(v[h] & 0xffff0000u);
       ss += a * a;
       ss += b * b;
     }
-  }
+    return ss;
+  };
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormKept; ++i)
+    if (lane * 8 + 512 * i < H) ss = add_sq(ss, kept[i]);
+  for (int c = lane * 8 + 512 * kNormKept; c < H; c += 512) ss = add_sq(ss, *(const u32x4*)(xr + c));
   ss = wave_sum_butterfly(ss);
   const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-  for (int c = lane * 8; c < H; c += 512) {
-    const u32x4 v = *(const u32x4*)(xr + c);
+  auto put = [&](int c, u32x4 v) {
     const u32x4 g = *(const u32x4*)(wr + c);
     u32x4 o;
 #pragma unroll
@@ -384,7 +397,11 @@ __device__ __forceinline__ void rms_norm_row(const uint16_t* __restrict__ xr, co
     }
     *(u32x4*)(dst0 + c) = o;
     if (dst1) *(u32x4*)(dst1 + c) = o;
-  }
+  };
+#pragma unroll
+  for (int i = 0; i < kNormKept; ++i)
+    if (lane * 8 + 512 * i < H) put(lane * 8 + 512 * i, kept[i]);
+  for (int c = lane * 8 + 512 * kNormKept; c < H; c += 512) put(c, *(const u32x4*)(xr + c));
 }
 
 struct SpreadGemvLds {
