@@ -326,7 +326,9 @@ def test_stages_match_forward(gpu_device):
                                       ("qwen3_int4", None, 8), ("mixtral_int4", None, 16),
                                       ("qwen15_int8_shared", None, 1024),
                                       # 17 .. 64 tokens: the several-workgroup route + group launch
-                                      ("qwen3_int4", None, 48), ("qwen15_int8_shared", None, 33)])
+                                      ("qwen3_int4", None, 48), ("qwen15_int8_shared", None, 33),
+                                      # 2 .. 4 tokens: the self-routing gate_up
+                                      ("qwen3_int4", None, 3)])
 def test_graph_replay_matches_eager(gpu_device, name, E, T):
     """The layer captured in a HIP graph (Qwen1.5-MoE at 1024 tokens: the
     prefill-form shared expert as a branch forked onto the handle's side

@@ -19,11 +19,13 @@ def announce(msg):
     sys.__stderr__.flush()
 
 
-@pytest.mark.parametrize("name,E", [("qwen3_int4", 32), ("small_int8_shared", None)])
-def test_noalloc_matches_forward(gpu_device, name, E):
+@pytest.mark.parametrize("name,E,T2", [("qwen3_int4", 32, 5), ("small_int8_shared", None, 5),
+                                       # the second call: the self-routing gate_up (3 tokens, 128 experts)
+                                       ("qwen3_int4", None, 3)])
+def test_noalloc_matches_forward(gpu_device, name, E, T2):
     layer = build_layer(CONFIGS[name], device="cuda", num_experts=E)
     native = native_layer(layer, torch.device("cuda"), max_tokens=64)
-    for T, seed in ((16, 51), (5, 52)):
+    for T, seed in ((16, 51), (T2, 52)):
         announce(f"noalloc {name} T={T}")
         x, logits = build_inputs(layer, T, seed=seed, device="cuda")
         ref = native.forward(x, logits).clone()
