@@ -534,7 +534,8 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
   }
   if (ROUTE) {
     // K1 on the token's logits by wave 0 (the same code and bits as the
-    // routing kernels); tile = position = rank of the expert id among the k.
+    // routing kernels; workgroup (0, 0) the whole of it, the others its
+    // selection alone); tile = position = rank of the expert id among the k.
     // Tiles k .. k + sh_chunks - 1 (sh_tile0 = k) are the shared expert's
     // chunks: no routing, and wave 0 of workgroup (0, k) computes its gate.
     __shared__ float rsv[kMaxTopK];
@@ -542,6 +543,7 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
     __shared__ int rids[kMaxTopK];
     __shared__ int rpos[kMaxTopK];
     __shared__ int r_expert;
+    __shared__ uint32_t rmask[8];
     const int k = a.topk;
     const bool first = blockIdx.x == 0 && tile == 0;
     if (tile >= k && tile < k + a.sh_chunks) shc = tile - k;
@@ -549,7 +551,21 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
       const float g = shared_gate_value(a.in, a.sh_gate_w, a.act_bf16, 0, a.K, (int)lane);
       if (lane == 0) a.sh_gate[0] = g;
     }
-    if (wave == 0 && shc < 0) {
+    if (wave == 0 && shc < 0 && !first) {
+      // only the tile's expert: K1's selection (route_mask, the same bits),
+      // then the tile-th selected id in ascending order
+      route_mask<2, true>(a.route_logits, 0, a.route_E, k, a.route_flags, rmask);
+      if (lane == 0) {
+        int r = tile, e = 0;
+        for (int wd = 0; wd < 4; ++wd) {
+          const int c = __popc(rmask[wd]);
+          if (r >= 0 && r < c) e = 32 * wd + nth_set_bit(rmask[wd], r);
+          r -= c;
+        }
+        r_expert = e;
+      }
+    }
+    if (wave == 0 && shc < 0 && first) {
       int id;
       float w;
       route_token<2, true>(a.route_logits, 0, a.route_E, k, a.route_flags, rsv, rsi, &id, &w);
@@ -559,13 +575,11 @@ __global__ void __launch_bounds__(S * gemv_rowsets_per_wg(S) * 64) gemv_kernel(G
         rids[lane] = id;
         rpos[lane] = pos;
         if (pos == tile) r_expert = id;
-        if (first) {
-          a.ro_ids[lane] = id;
-          a.ro_w[lane] = w;
-          a.ro_perm[pos] = lane;
-          a.ro_inv[lane] = pos;
-          a.ro_wpos[pos] = w;
-        }
+        a.ro_ids[lane] = id;
+        a.ro_w[lane] = w;
+        a.ro_perm[pos] = lane;
+        a.ro_inv[lane] = pos;
+        a.ro_wpos[pos] = w;
       }
     }
     __syncthreads();
