@@ -96,3 +96,50 @@ def test_self_routing_gate_up(gpu_device, name, T, case):
     finally:
         if resident is not None:
             native.set_residency(None)
+
+
+# (E, k, T, renorm, half the experts non-resident): E in (64, 128] and not
+# always a multiple of 64, k from 1 to 16, both sides of 4 T k <= E
+_SHAPES = [(72, 6, 4, True, False), (128, 16, 2, True, True), (127, 2, 4, False, False), (65, 8, 3, True, True),
+           (100, 1, 4, False, False), (96, 4, 4, True, True), (128, 16, 4, False, False)]
+
+
+@pytest.mark.parametrize("case", range(len(_SHAPES)))
+def test_self_routing_other_shapes(gpu_device, case):
+    """The self-routing gate_up over other shapes it takes (_SHAPES, I = 256,
+    the Qwen3 hidden size): routing outputs bit-exact against the oracle, the
+    output bit for bit against the stage entry points and within the bf16
+    tolerance of the oracle."""
+    from dataclasses import replace
+
+    from nano_ktrans_amd import _native as N
+
+    E, k, T, renorm, partial = _SHAPES[case]
+    cfg = replace(CONFIGS["qwen3_int4"], name=f"sr_shape{case}", E=E, k=k, I=256, renorm=renorm, seed=20 + case)
+    announce(f"self-routing shape {case}: E={E} k={k} T={T} renorm={renorm} partial residency={partial}")
+    _LAYERS.clear()
+    layer = build_layer(cfg, device="cuda")
+    native = native_layer(layer, torch.device("cuda"))
+    x, logits = build_inputs(layer, T, seed=400 + case, device="cuda")
+    resident = None
+    if partial:
+        resident = torch.from_numpy(np.random.default_rng(1000 + case).random(E) < 0.5)
+        native.set_residency(resident)
+    out = native.forward(x, logits).clone()
+    torch.cuda.synchronize()
+    oids, ow = O.route(logits.float().cpu().numpy(), k, cfg.softmax, cfg.renorm, True)
+    ocounts, ooffsets, operm, oinv = O.group(oids, E)
+    for r, dt, shp, want in [(N.WS_TOPK_IDS, torch.int32, (T, k), oids), (N.WS_COUNTS, torch.int32, (E,), ocounts),
+                             (N.WS_OFFSETS, torch.int32, (E + 1,), ooffsets), (N.WS_PERM, torch.int32, (T * k,), operm),
+                             (N.WS_INV, torch.int32, (T * k,), oinv)]:
+        assert np.array_equal(native.region(T, r, dt, shp).cpu().numpy(), want), r
+    got_w = native.region(T, N.WS_TOPK_WEIGHTS, torch.float32, (T, k)).cpu().numpy()
+    assert np.array_equal(got_w.view(np.uint32), np.asarray(ow, np.float32).view(np.uint32))
+    native.route(logits)
+    native.experts(x)
+    b = native.combine(T)
+    torch.cuda.synchronize()
+    assert torch.equal(out, b)
+    w_eff = ow if resident is None else np.where(resident.numpy()[oids], ow, np.float32(0.0)).astype(np.float32)
+    err_abs, err_rel = compare(out.float().cpu().numpy(), _oracle_given(layer, x, oids, w_eff), cfg)
+    announce(f"  max_abs={err_abs:.3e} rel_l2={err_rel:.3e}")
