@@ -1284,6 +1284,12 @@ int nkt_moe_forward_hidden(void* handle, const void* hidden_states, int num_toke
   const WsLayout L = ws_layout(h, num_tokens);
   hipStream_t st = (hipStream_t)stream;
   if (logits_first(h, num_tokens)) {
+    // everything run_layer checks, checked before the router's launch
+    if (!out) {
+      set_err(err, err_len, "null output");
+      return NKT_ERR;
+    }
+    if (!check_weights(h, h->Is > 0, err, err_len)) return NKT_ERR;
     if (do_router_logits(h, hidden_states, num_tokens, workspace, L, st, err, err_len) != NKT_OK) return NKT_ERR;
     const void* lg = ws_ptr<void>(workspace, L, NKT_WS_ROUTER_LOGITS);
     return run_layer(h, hidden_states, num_tokens, out, workspace, L, st, err, err_len,

@@ -205,3 +205,27 @@ def test_route_hidden_rejects_missing_router_and_fp32(gpu_device):
     f32 = _router_only(8, 2, True, True, torch.float32, gpu_device, hidden=256)
     with pytest.raises(ValueError, match="bf16 activations"):
         f32.load_router(torch.zeros(8, 256))
+
+
+@pytest.mark.parametrize("T", [4, 40])
+def test_rejected_forward_hidden_launches_nothing(gpu_device, T):
+    """nkt_moe_forward_hidden called with a null output is rejected before
+    any launch (a batch of up to 16 tokens would otherwise start with the
+    router's own launch): the error names the output and the router-logits
+    region keeps its contents."""
+    from nano_ktrans_amd import _native as N
+
+    announce(f"forward_hidden rejected before launching T={T}")
+    native = _router_only(16, 2, True, True, torch.bfloat16, gpu_device, max_tokens=64, hidden=256)
+    native.load_router((torch.randn(16, 256, generator=torch.Generator().manual_seed(5)) * 0.02).to(torch.bfloat16))
+    ws = native.workspace(T)
+    region = native.region(T, N.WS_ROUTER_LOGITS, torch.int16, (T, 16))
+    region.fill_(0x1234)
+    torch.cuda.synchronize()
+    x = torch.randn(T, 256, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).to(gpu_device)
+    with pytest.raises(N.NativeError, match="null .*output"):
+        native.err.check(native.lib.nkt_moe_forward_hidden(native.handle, x.data_ptr(), T, None, ws.data_ptr(),
+                                                           ws.numel(), native._stream(), native.err.buf,
+                                                           native.err.size), "nkt_moe_forward_hidden")
+    torch.cuda.synchronize()
+    assert bool((region == 0x1234).all())
