@@ -176,8 +176,9 @@ __device__ __forceinline__ void pin_slot(WSlot<WF, NT>& r) {
 template <int WF, int NT, class BOp>
 __device__ __forceinline__ void mma_group_b(const WSlot<WF, NT>& r, BOp bop, float xs, f32x4 (&acc)[NT], bool use,
                                             const DqConst& k) {
-  // scale x partial, then + acc, each rounded: never fused, so every kernel
-  // that accumulates a tile here gets the same bits
+  // int4: acc + scale x partial as one explicit fused multiply-add (the same
+  // instruction in every kernel that accumulates a tile here, so the same
+  // bits); otherwise acc + partial
 #pragma clang fp contract(off)
   const float c = WF == WF_I4 ? -136.0f * xs : WF == WF_I8 ? -128.0f * xs : 0.0f;
   f32x4 tmp[NT];
@@ -194,9 +195,14 @@ __device__ __forceinline__ void mma_group_b(const WSlot<WF, NT>& r, BOp bop, flo
   }
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    if (WF == WF_I4) tmp[t] = bf16x4_to_f32(r.s[t]) * tmp[t];
+    if (WF == WF_I4) {
+      const f32x4 sc = bf16x4_to_f32(r.s[t]);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) acc[t][v] = use ? acc[t][v] + tmp[t][v] : acc[t][v];
+      for (int v = 0; v < 4; ++v) acc[t][v] = use ? __builtin_fmaf(sc[v], tmp[t][v], acc[t][v]) : acc[t][v];
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[t][v] = use ? acc[t][v] + tmp[t][v] : acc[t][v];
+    }
   }
 }
 
@@ -215,7 +221,10 @@ __device__ __forceinline__ void mma_group(const WSlot<WF, NT>& r, const u32x4 (&
       tmp = f32x4{c, c, c, c};
 #pragma unroll
       for (int s = 0; s < 4; ++s) tmp = mfma_bf16(dq_i4(r.w[t][0][s]), xb[s], tmp);
-      tmp = bf16x4_to_f32(r.s[t]) * tmp;
+      const f32x4 sc = bf16x4_to_f32(r.s[t]);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[t][v] = use ? __builtin_fmaf(sc[v], tmp[v], acc[t][v]) : acc[t][v];
+      continue;
     } else if (WF == WF_I8) {
       const float c = -128.0f * xs;
       tmp = f32x4{c, c, c, c};
