@@ -30,7 +30,9 @@
 // Dequantisation is the same as the prefill kernel's: codes enter the matrix
 // core as exact bf16 integers with an offset (int4: 136 + q, int8: 128 + q),
 // the offset times the group's activation sum is removed per group, the bf16
-// scale multiplies each group's fp32 partial (int4) or the row total (int8).
+// scale multiplies each group's fp32 partial (int4: one explicit fused
+// multiply-add into the running sum, so every kernel that shares this
+// accumulation rounds alike) or the row total (int8).
 #include "nkt_common.h"
 #include "nkt_group.h"
 #include "nkt_internal.h"
