@@ -154,6 +154,33 @@ int shared_chunk_count(const Handle* h, const WsLayout& L) {
   return c <= kMaxSharedChunks ? c : 0;
 }
 
+// K parts of the shared expert's prefill-form int8 down in the layer call:
+// the smallest count that leaves at most 16 K groups per part (Qwen1.5-MoE:
+// 44 groups -> 4 parts of 11), so each (token tile, weight slab) item runs
+// K / parts deep (5632: 88 stages of 64 -> 22) on parts times the
+// workgroups; the combine adds the parts' fp32 rows in order.  Only while
+// the undivided down has at most kSharedPartsMaxItems items: beside the
+// routed experts on the side stream, a small grid of deep items ends last
+// and the parts pay; a larger one already fills what the routed launches
+// leave, and parts then only compete with them.  Measured (Qwen1.5-MoE int8,
+// graph replays, us per layer, one part -> parts): T = 320 / 512 / 640 / 768
+// 165 / 181 / 189 / 208 -> 157 / 172 / 184 / 198, T = 896 (112 items) 224
+// either way, T = 1024 236 -> 248; the parts on the caller's stream after
+// the routed experts instead: T = 512 / 1024 191 / 261.  1 (one part) when
+// the K groups admit no such count, for other weight formats and for the
+// decode form.
+constexpr int kSharedPartsMaxItems = 96;
+
+int shared_down_parts(const Handle* h, const WsLayout& L, int T) {
+  if (h->Is <= 0 || h->wf != WF_I8 || L.bm_shared != kPrefillTileM || h->Is % 128 != 0 || h->H % 256 != 0) return 1;
+  if ((int64_t)(h->H / 256) * ((T + kPrefillTileM - 1) / kPrefillTileM) > kSharedPartsMaxItems) return 1;
+  const int G = h->Is / 128;
+  if (G <= 16) return 1;
+  for (int p = 2; p <= kMaxSharedChunks; ++p)
+    if (G % p == 0 && G / p <= 16) return p;
+  return 1;
+}
+
 // int8 weights with bf16 activations: the prefill gate_up runs on the fp16
 // matrix cores from a power-of-two-scaled fp16 copy of x (H <= 4096)
 bool int8_f16_input(const Handle* h) { return h->wf == WF_I8 && h->act_bf16 && h->H <= 4096; }
@@ -197,7 +224,9 @@ WsLayout ws_layout(const Handle* h, int T) {
   sz[kWsX16] = x16 ? (size_t)T * h->H * 2 : 0;
   sz[kWsXInv] = x16 ? (size_t)T * 4 : 0;
   sz[kWsWpos] = P * 4;
-  sz[kWsShChunkY] = (size_t)shared_chunk_count(h, L) * T * h->H * 4;
+  const int parts = shared_down_parts(h, L, T);
+  const int sh_rows = parts > 1 ? parts : shared_chunk_count(h, L);  // the two never apply together
+  sz[kWsShChunkY] = (size_t)sh_rows * T * h->H * 4;
   // The sync area first, the same size and place for every handle and
   // token count (counters and status, the router's published masks): it must be
   // zero before a workspace's first use, every call of every handle leaves
@@ -591,8 +620,10 @@ int do_experts(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hip
   return do_expert_phase(h, PHASE_DOWN, x, T, ws, L, st, err, len, nullptr, compact, chunks);
 }
 
+// parts > 1 (the layer call, shared_down_parts): the down runs in K parts
+// whose fp32 rows go to the chunk-row region for the combine to add
 int do_shared(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipStream_t st,
-              char* err, size_t len, bool prep_done = false) {
+              char* err, size_t len, bool prep_done = false, int parts = 1) {
   if (h->Is <= 0) {
     set_err(err, len, "handle has no shared expert");
     return NKT_ERR;
@@ -613,6 +644,10 @@ int do_shared(Handle* h, const void* x, int T, void* ws, const WsLayout& L, hipS
                  err, len))
     return NKT_ERR;
   GemmArgs b = expert_args(h, PHASE_DOWN, true, ws_ptr<void>(ws, L, NKT_WS_SHARED_H), ws, L, T);
+  if (parts > 1) {
+    b.k_parts = parts;
+    b.out = ws_ptr<void>(ws, L, kWsShChunkY);
+  }
   if (!check_hip(launch_expert_gemm(h, b, PHASE_DOWN, bm, tiles, st), "shared down gemm", err, len))
     return NKT_ERR;
   return NKT_OK;
@@ -848,6 +883,9 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
   // dense down of few workgroups among them) run beside the routed experts'
   // on the side stream and fill what those leave idle
   bool late = false;
+  // the shared expert's prefill down in K parts (shared_down_parts), whether
+  // it forks or stays on st
+  const int parts = chunks == 0 && !side ? shared_down_parts(h, L, T) : 1;
   const bool late_ok = (prep_done && L.bm_shared != kTileSrcCols && side_stream_ready(h, st)) ||
                        (x_from_route && shared_side_ready(h, T, L, st));
   if (rc == NKT_OK && allow_side && !side && h->Is > 0 && chunks == 0 && late_ok) {
@@ -855,7 +893,7 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
     if (!check_hip(hipEventRecord(h->fork_ev, st), "fork event", err, len) ||
         !check_hip(hipStreamWaitEvent(h->side, h->fork_ev, 0), "fork wait", err, len))
       return NKT_ERR;
-    const int rs = do_shared(h, x, T, ws, L, h->side, err, len, prep_done);
+    const int rs = do_shared(h, x, T, ws, L, h->side, err, len, prep_done, parts);
     const hipError_t je = hipEventRecord(h->join_ev, h->side);
     if (je != hipSuccess) {
       if (rs == NKT_OK) check_hip(je, "join event", err, len);
@@ -872,13 +910,13 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
     rc = sr ? do_expert_phase(h, PHASE_DOWN, x, T, ws, L, st, err, len, nullptr, true, chunks)
             : do_experts(h, x, T, ws, L, st, err, len, true, chunks, prep_done);
   if (rc == NKT_OK && !side && !late && h->Is > 0 && chunks == 0)
-    rc = do_shared(h, x, T, ws, L, st, err, len, prep_done);
+    rc = do_shared(h, x, T, ws, L, st, err, len, prep_done, parts);
   if (side || late) {
     const hipError_t we = hipStreamWaitEvent(st, h->join_ev, 0);
     if (rc == NKT_OK && !check_hip(we, "join wait", err, len)) rc = NKT_ERR;
   }
   if (rc != NKT_OK) return rc;
-  return do_combine(h, T, out, ws, L, st, err, len, nullptr, residual, true, chunks);
+  return do_combine(h, T, out, ws, L, st, err, len, nullptr, residual, true, parts > 1 ? parts : chunks);
 }
 
 // ---------------------------------------------------------------------------

@@ -118,13 +118,14 @@ __global__ void __launch_bounds__(256) combine_kernel(
 // inverse scale per row and 256-column slab in yscale), eight columns per
 // thread so every row load is 16 bytes: each half of four columns goes
 // through the thread's LDS slots in turn, with combine_kernel's order and
-// arithmetic on the expanded values.
+// arithmetic on the expanded values.  The shared row: the sum of its
+// sh_rows part rows (the shared down's K parts) in part order.
 template <int K>
 __global__ void __launch_bounds__(256) combine16_kernel(
     const uint16_t* __restrict__ y16, const float* __restrict__ yscale, const int32_t* __restrict__ ids,
     const float* __restrict__ w, const int32_t* __restrict__ inv, const float* __restrict__ y_shared,
     const float* __restrict__ shared_gate, const uint8_t* __restrict__ resident, const void* __restrict__ extra,
-    const void* __restrict__ residual, int num_tokens, int H, void* __restrict__ out, int out_bf16) {
+    const void* __restrict__ residual, int num_tokens, int H, void* __restrict__ out, int out_bf16, int sh_rows) {
   __shared__ f32x4 terms[K][256];
   const int t = blockIdx.x;
   const int c = blockIdx.y * blockDim.x + threadIdx.x;  // 8-column group
@@ -175,7 +176,11 @@ __global__ void __launch_bounds__(256) combine16_kernel(
     for (int r = 1; r < K; ++r) acc += terms[r][threadIdx.x];
     const int col = 8 * c + 4 * half;
     f32x4 vs = zero;
-    if (y_shared) vs = *(const f32x4*)(y_shared + (int64_t)t * H + col);
+    if (y_shared) {
+      // the shared row (or its parts' rows, added in order)
+      vs = *(const f32x4*)(y_shared + (int64_t)t * H + col);
+      for (int j = 1; j < sh_rows; ++j) vs += *(const f32x4*)(y_shared + ((int64_t)j * num_tokens + t) * H + col);
+    }
     combine_tail(acc, t, col, H, extra, y_shared != nullptr, vs, sg, residual, out, out_bf16);
   }
 }
@@ -279,13 +284,13 @@ hipError_t launch_combine(const float* y, const int32_t* ids, const float* w, co
                           int out_bf16, hipStream_t stream, const uint16_t* y16, const float* yscale, int sh_rows) {
   if (T <= 0) return hipSuccess;
   if (y16 && (!yscale || H % 256 != 0)) return hipErrorInvalidValue;
-  if (sh_rows < 1 || sh_rows > kMaxSharedChunks || (sh_rows > 1 && (y16 || !y_shared))) return hipErrorInvalidValue;
+  if (sh_rows < 1 || sh_rows > kMaxSharedChunks || (sh_rows > 1 && !y_shared)) return hipErrorInvalidValue;
   dim3 grid(T, (H / 4 + 255) / 256), grid16(T, (H / 8 + 255) / 256), block(256);
 #define NKT_COMBINE_CASE(KK)                                                                              \
   case KK:                                                                                                \
     if (y16)                                                                                              \
       hipLaunchKernelGGL(combine16_kernel<KK>, grid16, block, 0, stream, y16, yscale, ids, w, inv, y_shared, \
-                         shared_gate, resident, extra, residual, T, H, out, out_bf16);                    \
+                         shared_gate, resident, extra, residual, T, H, out, out_bf16, sh_rows);           \
     else                                                                                                  \
       hipLaunchKernelGGL(combine_kernel<KK>, grid, block, 0, stream, y, ids, w, inv, y_shared, shared_gate,  \
                          resident, extra, residual, T, H, out, out_bf16, sh_rows);                        \

@@ -136,13 +136,14 @@ struct EpiPre {
   u32x2 s[kRT];
 };
 
+// g0, G: the item's K groups [g0, g0 + G) of the a.K / 128 per input row
 template <bool XS>
-__device__ __forceinline__ bool i8_row_terms(const GemmArgs& a, const int* srcl, float (&v)[16], float& xi) {
-  const int G = a.K / 128;
+__device__ __forceinline__ bool i8_row_terms(const GemmArgs& a, const int* srcl, float (&v)[16], float& xi, int g0,
+                                             int G) {
   if (G > 16) return false;
   const int tid = threadIdx.x;
   if (tid < kBM) {
-    const float* xr = a.xsum + (int64_t)srcl[tid] * G;
+    const float* xr = a.xsum + (int64_t)srcl[tid] * (a.K / 128) + g0;
 #pragma unroll
     for (int g = 0; g < 16; ++g) v[g] = g < G ? xr[g] : 0.f;
     if (XS) xi = a.xinv[srcl[tid]];
@@ -198,7 +199,8 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[1
                                                const int* orow_l,
                                                float (*hpart)[kBM], float* xtot_l, float* xinv_l, const int* wrow,
                                                const uint16_t* sexp, int row0, int rows, int slab,
-                                               const EpiPre<16 / kWaves>* pre = nullptr, uint8_t* stage = nullptr) {
+                                               const EpiPre<16 / kWaves>* pre = nullptr, uint8_t* stage = nullptr,
+                                               int64_t out_off = 0) {
   constexpr int kRT = 16 / kWaves;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -347,7 +349,7 @@ __device__ __forceinline__ void gemm2_epilogue(const GemmArgs& a, f32x4 (&acc)[1
         const int pl = c * 16 + (lane & 15);
         f32x4 v = acc[r][c];
         if (WF == WF_I8) v *= sr;
-        if (pl < rows) *(f32x4*)((float*)a.out + (int64_t)orow_l[pl] * a.N + wrow[r] + rq) = v;
+        if (pl < rows) *(f32x4*)((float*)a.out + out_off + (int64_t)orow_l[pl] * a.N + wrow[r] + rq) = v;
       }
     }
   }
@@ -575,8 +577,16 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
   gemm2_sources(a, it, srcl, orow_l);
   __syncthreads();
 
+  // down in K parts: item slab s is K part s / (N / 256) of slab s % (N / 256)
+  int kpart = 0;
+  if (PHASE == PHASE_DOWN && a.k_parts > 1) {
+    kpart = it.slab / (a.N / 256);
+    it.slab -= kpart * (a.N / 256);
+  }
+  const int Kp = (PHASE == PHASE_DOWN && a.k_parts > 1) ? a.K / a.k_parts : a.K;  // this item's K range
   const uint16_t* sexp = a.scales + (int64_t)it.expert * a.s_expert_elems;
-  const int NS = a.K / kI8Stage;  // stages = 1 KiB blocks per 16-row block
+  const int NS = Kp / kI8Stage;         // stages this item runs
+  const int NSrow = a.K / kI8Stage;     // 1 KiB blocks per 16-row block
   // buffer resources over this expert's weights and the activation rows; a
   // load at offset kI8Skip is out of range: it reads nothing (zeros)
   const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
@@ -590,14 +600,14 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
       wrow[r] = (r < kRT / 2 ? 0 : a.I) + it.slab * 128 + wave * (128 / kWaves) + (r % (kRT / 2)) * 16;
     else
       wrow[r] = it.slab * 256 + wave * (256 / kWaves) + r * 16;
-    wsrc[r] = (uint32_t)(wrow[r] >> 4) * (uint32_t)NS * 1024u + lane * 16u;
+    wsrc[r] = ((uint32_t)(wrow[r] >> 4) * (uint32_t)NSrow + (uint32_t)(kpart * NS)) * 1024u + lane * 16u;
   }
   uint32_t tsrc[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int p = 16 * wave + 8 * j + (lane >> 3);
     const int chunk = (lane & 7) ^ ((p >> 1) & 7);
-    tsrc[j] = (uint32_t)srcl[p] * (uint32_t)a.K * 2u + chunk * 16u;
+    tsrc[j] = ((uint32_t)srcl[p] * (uint32_t)a.K + (uint32_t)(kpart * Kp)) * 2u + chunk * 16u;
   }
   const int tofs = wave * 2048;  // this wave's slice of a token buffer
 
@@ -668,7 +678,7 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
 
   EpiPre<kRT> pre;
   float rv[16], rxi = 0.f;
-  pre.valid = i8_row_terms<F16>(a, srcl, rv, rxi);
+  pre.valid = i8_row_terms<F16>(a, srcl, rv, rxi, kpart * (Kp / 128), Kp / 128);
   if (pre.valid) {
 #pragma unroll
     for (int r = 0; r < kRT; ++r) pre.s[r] = *(const u32x2*)(sexp + wrow[r] + 4 * (lane >> 4));
@@ -678,7 +688,7 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
   issue_w(0, w0);
   issue_tok(2, tb2);
   issue_w(1, w1);
-  if (pre.valid) i8_row_terms_store(a.K / 128, xtot_l, xinv_l, rv, rxi, F16);
+  if (pre.valid) i8_row_terms_store(Kp / 128, xtot_l, xinv_l, rv, rxi, F16);
   __asm__ volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(0x0F7C);  // vmcnt(12): T0 landed
   lds_barrier();
@@ -706,7 +716,8 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
   // buffers, free once every wave has passed the barrier above
   uint8_t* stage = wave < 3 ? tb0 + wave * 2304 : tb1;
   gemm2_epilogue<WF_I8, PHASE, kWaves, F16>(a, acc, srcl, orow_l, hpart, xtot_l, xinv_l, wrow, sexp, it.row0, it.rows,
-                                            it.slab, &pre, PHASE == PHASE_DOWN ? stage : nullptr);
+                                            it.slab, &pre, PHASE == PHASE_DOWN ? stage : nullptr,
+                                            (int64_t)kpart * a.num_rows * a.N);
 }
 
 // Per-row sums of each 128-wide K group of a bf16 matrix [rows, K] -> fp32
@@ -1096,7 +1107,12 @@ constexpr int gemm2_waves(int wf) { return wf == WF_I8 ? 4 : 8; }
 hipError_t launch_gemm2(const GemmArgs& a, int wf, int phase, int max_tiles, hipStream_t stream,
                         const KernelTimer* tm) {
   if (max_tiles <= 0) return hipSuccess;
-  const int n_slabs = phase == PHASE_GATE_UP ? a.I / 128 : a.N / 256;
+  // K parts: the int8 pipeline's down only, fp32 rows, at most 16 K groups per part
+  const int kp = a.k_parts > 1 ? a.k_parts : 1;
+  if (kp > 1 && (phase != PHASE_DOWN || !gemm2_i8_pipeline(a, wf) || a.y16 || a.K % (128 * kp) != 0 ||
+                 a.K / kp > 16 * 128))
+    return hipErrorInvalidValue;
+  const int n_slabs = phase == PHASE_GATE_UP ? a.I / 128 : a.N / 256 * kp;
   const int64_t items = (int64_t)n_slabs * max_tiles;
   const int sg = slab_group(n_slabs, a.w_expert_bytes);
   dim3 grid((unsigned)((items + kXcds - 1) / kXcds * kXcds)), block(64 * gemm2_waves(wf));

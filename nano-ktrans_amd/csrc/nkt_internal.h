@@ -59,6 +59,10 @@ struct GemmArgs {
   // inverse goes to yscale [rows, N / 256]
   uint16_t* y16;
   float* yscale;
+  // prefill int8 down, k_parts > 1: the K range in k_parts equal parts, each
+  // (tile, slab) item once per part; part p's fp32 partial rows go to
+  // out + p num_rows N, and the combine adds the parts in order
+  int k_parts;
   // single-token decode gate_up that routes its token itself
   // (route_logits != nullptr, [1, route_E] bf16): every workgroup runs K1
   // on the one row of logits, workgroup (0, 0) also writes K1's and K2's

@@ -324,7 +324,7 @@ def test_stages_match_forward(gpu_device):
 @pytest.mark.parametrize("name,E,T", [("qwen15_int8_shared", None, 16), ("qwen15_int8_shared", None, 1),
                                       ("qwen3_int4", 32, 16), ("qwen3_int8", 32, 512), ("mixtral_int4", None, 300),
                                       ("qwen3_int4", None, 8), ("mixtral_int4", None, 16),
-                                      ("qwen15_int8_shared", None, 1024),
+                                      ("qwen15_int8_shared", None, 1024), ("qwen15_int8_shared", None, 512),
                                       # 17 .. 64 tokens: the several-workgroup route + group launch
                                       ("qwen3_int4", None, 48), ("qwen15_int8_shared", None, 33),
                                       # 2 .. 4 tokens: the self-routing gate_up
@@ -460,13 +460,17 @@ def test_mixtral_int4_full_prefill(gpu_device):
     _check_rows_and_prefix(layer, native, 2048, 1024, seed=31)
 
 
-def test_qwen15_shared_full_prefill(gpu_device):
-    """Qwen1.5-MoE at T=1024: the routed experts and the 23 MB shared
-    gate_up (11264 x 2048 int8) in the prefill form, the shared expert's
-    weight slabs in groups of 4."""
-    announce("forward qwen15_int8_shared full T=1024 (rows) and T=512 (prefix)")
+@pytest.mark.parametrize("T,prefix", [(1024, 896), (512, 320)])
+def test_qwen15_shared_full_prefill(gpu_device, T, prefix):
+    """Qwen1.5-MoE in the prefill form: the routed experts and the 23 MB
+    shared gate_up (11264 x 2048 int8), the shared expert's weight slabs in
+    groups of 4.  T=1024 (and its prefix 896): the shared down sums all of
+    K = 5632 in one pass; T=512 (and 320): in 4 K parts of 1408 whose rows
+    the combine adds in order -- each prefix in its batch's regime, so its
+    rows are bit-identical."""
+    announce(f"forward qwen15_int8_shared full T={T} (rows) and T={prefix} (prefix)")
     layer, native = _layer("qwen15_int8_shared")
-    _check_rows_and_prefix(layer, native, 1024, 512, seed=33)
+    _check_rows_and_prefix(layer, native, T, prefix, seed=33)
 
 
 @pytest.mark.parametrize("T", [1, 16])
@@ -506,8 +510,10 @@ def test_decode_outlier_channels(gpu_device, name, E, T):
                                       ("qwen3_int4", None, 1), ("qwen15_int8_shared", None, 1),
                                       ("qwen3_int4", None, 16), ("qwen3_int4", None, 4), ("mixtral_int4", None, 16),
                                       ("qwen3_int8", 32, 16), ("qwen3_int8", 32, 512), ("qwen15_int8_shared", None, 1024),
+                                      ("qwen15_int8_shared", None, 512),
                                       # 2 .. 16 tokens: the routing launch, then the decode launches
-                                      # (2 Qwen3 int4 tokens: the down + combine launch)
+                                      # (2 Qwen3 int4 tokens: the self-routing gate_up, no routing
+                                      # launch, then the down + combine launch)
                                       ("qwen3_int4", None, 2), ("qwen3_int4", None, 8), ("qwen3_int4", 32, 13),
                                       ("qwen15_int8_shared", None, 5), ("mixtral_int4", None, 3),
                                       ("qwen3_int8", 32, 7), ("small_int8_shared", None, 1)])
@@ -517,10 +523,12 @@ def test_forward_matches_stages_and_leaves_sync_area_zero(gpu_device, name, E, T
     int4 Qwen3 shape, the layer runs the down GEMV and the combine as one
     launch) in the decode form; in the prefill form
     the layer keeps y as fp16 with a power-of-two scale per position and
-    256-column slab (the stages keep fp32 y), and a decode-form layer runs
-    the shared expert as Is / I chunks whose down sums are added chunk by
-    chunk (the stage sums all of K at once), so there every output element
-    is within 2^-12 of the largest |y| plus one bf16 step of the stages'.
+    256-column slab (the stages keep fp32 y), and the layer runs the shared
+    expert's down in parts whose sums are added part by part (the decode
+    form: Is / I chunks; the prefill form with up to 96 (token tile, weight
+    slab) items, Qwen1.5-MoE at T = 512: 4 K parts) where the stage sums all
+    of K at once, so there every output element is within 2^-12 of the
+    largest |y| plus one bf16 step of the stages'.
     The layer leaves the workspace's sync area (the NKT_SYNC_AREA_BYTES
     before NKT_WS_TOPK_IDS) all zero."""
     import ctypes
