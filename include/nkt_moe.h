@@ -285,11 +285,12 @@ int nkt_moe_forward_block(void* handle, const void* hidden_states, const void* n
  * NKT_NOALLOC_SCRATCH_BYTES (decode batches of every supported shape fit;
  * large prefill batches do not).  Every call on one GPU shares that GPU's
  * scratch: calls that overlap on one GPU (two streams, two handles, two
- * threads) race and must be serialised by the caller.  Nothing in the
- * scratch has to start at zero: each call writes every region before it
- * reads it, and this entry point routes from given logits, so it never runs
- * the single-launch router and never reads or writes the sync area (the
- * NKT_WS_SYNC words and the router's published masks). */
+ * threads) race and must be serialised by the caller.  The scratch starts
+ * zeroed (a static device array) and, as after every layer call, its sync
+ * area (the NKT_WS_SYNC words and the router's published masks) is zero
+ * again when the call ends: from given logits, batches of 17 .. 64 tokens
+ * route in the several-workgroup launch, whose arrival counters and masks
+ * live there; every other region is written before it is read. */
 int nkt_moe_forward_noalloc(void* handle, const void* hidden_states, const void* router_logits,
                             int num_tokens, void* out, void* stream, char* err, size_t err_len);
 

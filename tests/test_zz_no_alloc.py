@@ -19,13 +19,16 @@ def announce(msg):
     sys.__stderr__.flush()
 
 
-@pytest.mark.parametrize("name,E,T2", [("qwen3_int4", 32, 5), ("small_int8_shared", None, 5),
-                                       # the second call: the self-routing gate_up (3 tokens, 128 experts)
-                                       ("qwen3_int4", None, 3)])
-def test_noalloc_matches_forward(gpu_device, name, E, T2):
+@pytest.mark.parametrize("name,E,T1,T2", [("qwen3_int4", 32, 16, 5), ("small_int8_shared", None, 16, 5),
+                                          # the second call: the self-routing gate_up (3 tokens, 128 experts)
+                                          ("qwen3_int4", None, 16, 3),
+                                          # 17 .. 64 tokens: the several-workgroup routing launch, whose
+                                          # counters and published masks live in the scratch's sync area
+                                          ("qwen3_int4", None, 40, 24)])
+def test_noalloc_matches_forward(gpu_device, name, E, T1, T2):
     layer = build_layer(CONFIGS[name], device="cuda", num_experts=E)
     native = native_layer(layer, torch.device("cuda"), max_tokens=64)
-    for T, seed in ((16, 51), (T2, 52)):
+    for T, seed in ((T1, 51), (T2, 52)):
         announce(f"noalloc {name} T={T}")
         x, logits = build_inputs(layer, T, seed=seed, device="cuda")
         ref = native.forward(x, logits).clone()
@@ -39,7 +42,7 @@ def test_noalloc_matches_forward(gpu_device, name, E, T2):
         compare(out.float().cpu().numpy(), oracle_forward(layer, x, logits), layer.cfg)
 
 
-@pytest.mark.parametrize("name,E,T", [("qwen3_int4", 32, 16), ("small_int8_shared", None, 1)])
+@pytest.mark.parametrize("name,E,T", [("qwen3_int4", 32, 16), ("small_int8_shared", None, 1), ("qwen3_int4", None, 40)])
 def test_noalloc_captures_in_a_graph(gpu_device, name, E, T):
     """The call is capture-safe: captured in a HIP graph in global capture
     mode (where a hipMalloc, hipFree or stream creation anywhere in the
