@@ -358,17 +358,19 @@ __device__ __forceinline__ bool arrive_last(uint32_t* c, uint32_t n, uint32_t* f
 // l adds its 8-column chunks l, l + 64, ... in order, then a fixed
 // butterfly); the result to dst0 (LDS) and, when non-null, dst1.  The first
 // kNormKept chunks of the lane (H <= 4096) stay in registers for the second
-// pass, so it reads x only once (further chunks are read again).
+// pass, so it reads x only once (further chunks are read again), and their
+// norm weights are loaded with them, before the reduction.
 constexpr int kNormKept = 8;
 
 __device__ __forceinline__ void rms_norm_row(const uint16_t* __restrict__ xr, const uint16_t* __restrict__ wr,
                                              float eps, int H, uint16_t* dst0, uint16_t* dst1) {
   const int lane = threadIdx.x & 63;
-  u32x4 kept[kNormKept];
+  u32x4 kept[kNormKept], gk[kNormKept];
 #pragma unroll
   for (int i = 0; i < kNormKept; ++i) {
     const int c = lane * 8 + 512 * i;
     kept[i] = c < H ? *(const u32x4*)(xr + c) : u32x4{0u, 0u, 0u, 0u};
+    gk[i] = c < H ? *(const u32x4*)(wr + c) : u32x4{0u, 0u, 0u, 0u};
   }
   auto add_sq = [](float ss, u32x4 v) {
 #pragma unroll
@@ -386,8 +388,7 @@ __device__ __forceinline__ void rms_norm_row(const uint16_t* __restrict__ xr, co
   for (int c = lane * 8 + 512 * kNormKept; c < H; c += 512) ss = add_sq(ss, *(const u32x4*)(xr + c));
   ss = wave_sum_butterfly(ss);
   const float inv = 1.0f / sqrtf(ss / (float)H + eps);
-  auto put = [&](int c, u32x4 v) {
-    const u32x4 g = *(const u32x4*)(wr + c);
+  auto put = [&](int c, u32x4 v, u32x4 g) {
     u32x4 o;
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
@@ -400,8 +401,8 @@ __device__ __forceinline__ void rms_norm_row(const uint16_t* __restrict__ xr, co
   };
 #pragma unroll
   for (int i = 0; i < kNormKept; ++i)
-    if (lane * 8 + 512 * i < H) put(lane * 8 + 512 * i, kept[i]);
-  for (int c = lane * 8 + 512 * kNormKept; c < H; c += 512) put(c, *(const u32x4*)(xr + c));
+    if (lane * 8 + 512 * i < H) put(lane * 8 + 512 * i, kept[i], gk[i]);
+  for (int c = lane * 8 + 512 * kNormKept; c < H; c += 512) put(c, *(const u32x4*)(xr + c), *(const u32x4*)(wr + c));
 }
 
 struct SpreadGemvLds {
