@@ -6,8 +6,11 @@ top-8, moe_intermediate=768, int4 group-128 weights with bf16 scales, bf16
 activations) decoding 16 tokens.  A step is one layer forward (route, group,
 gate_up GEMM + SwiGLU, down GEMM, combine) on a new weight copy: steps rotate
 over --layers distinct copies of the layer (> 2 GB in total, beyond the 256 MB
-last-level cache) and over 8 seeded inputs, the way consecutive layers of a
-model would stream their weights from HBM.  After --warmup eager steps,
+last-level cache) and over 8 seeded inputs, step i taking input
+(i + i // layers) mod 8, so 8 x layers (copy, input) pairs -- each its own set
+of routed experts -- pass before one recurs, the way consecutive layers of a
+model would stream their weights from HBM (at one token a step reads ~19 MB of
+experts: 64 pairs still exceed the last-level cache).  After --warmup eager steps,
 exactly --steps steps are timed as one replay of a HIP graph holding them,
 with HIP events between device synchronisations.
 
@@ -195,10 +198,21 @@ def active_experts(layer, logits):
 
 
 # --------------------------------------------------------------------- timing
+def step_input(i, L):
+    """Input of step i (taken modulo the input count) when steps rotate over L
+    layer copies: i + i // L, so copy i % L meets a new input on every visit
+    and L x (input count) (copy, input) pairs -- each reading its own routed
+    experts -- pass before one recurs.  With the same input on every visit a
+    one-token step over 8 copies would re-read ~150 MB of experts, which the
+    256 MB last-level cache holds."""
+    return i + i // L
+
+
 def time_steps(layers, xs, outs, steps, warmup, call):
-    """Exactly `steps` layer calls (call(layer, i, out)), layer copy i % L, timed
-    as one replay of a HIP graph that holds those calls, between device
-    synchronisations, after `warmup` eager calls.  Returns ms per step."""
+    """Exactly `steps` layer calls (call(layer, j, out): layer copy i % L,
+    input j = step_input(i, L)), timed as one replay of a HIP graph that
+    holds those calls, between device synchronisations, after `warmup` eager
+    calls.  Returns ms per step."""
     import torch
 
     L = len(layers)
@@ -206,15 +220,15 @@ def time_steps(layers, xs, outs, steps, warmup, call):
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         for i, layer in enumerate(layers):  # make every workspace before capture
-            call(layer, i, outs[i])
+            call(layer, step_input(i, L), outs[i])
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for i in range(steps):
-            call(layers[i % L], i, outs[i % L])
+            call(layers[i % L], step_input(i, L), outs[i % L])
     for i in range(warmup):
-        call(layers[i % L], i, outs[i % L])
+        call(layers[i % L], step_input(i, L), outs[i % L])
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0.record()
@@ -229,7 +243,7 @@ def time_steps(layers, xs, outs, steps, warmup, call):
 def time_graph(layers, xs, ls, outs, steps, warmup):
     """The layer from (hidden_states, router_logits): ms per step."""
     return time_steps(layers, xs, outs, steps, warmup,
-                      lambda layer, i, out: layer.forward(xs[i % len(xs)], ls[i % len(ls)], out=out))
+                      lambda layer, j, out: layer.forward(xs[j % len(xs)], ls[j % len(ls)], out=out))
 
 
 def time_graph_hidden(layers, xs, outs, steps, warmup, call=None):
@@ -237,7 +251,7 @@ def time_graph_hidden(layers, xs, outs, steps, warmup, call=None):
     call(layer, x, out)): ms per step."""
     if call is None:
         call = lambda layer, x, out: layer.forward_hidden(x, out=out)
-    return time_steps(layers, xs, outs, steps, warmup, lambda layer, i, out: call(layer, xs[i % len(xs)], out))
+    return time_steps(layers, xs, outs, steps, warmup, lambda layer, j, out: call(layer, xs[j % len(xs)], out))
 
 
 def time_stages(layers, xs, ls, outs, rounds):
@@ -248,6 +262,7 @@ def time_stages(layers, xs, ls, outs, rounds):
     acc = {n: 0.0 for n in names}
     count = 0
     stream = torch.cuda.current_stream()
+    L = len(layers)
     for r in range(rounds):
         try:
             torch.cuda._sleep(50_000_000)  # keep the device busy while the host enqueues
@@ -255,7 +270,8 @@ def time_stages(layers, xs, ls, outs, rounds):
             pass
         evs = []
         for i, layer in enumerate(layers):
-            x, lg = xs[i % len(xs)], ls[i % len(ls)]
+            j = step_input(r * L + i, L)
+            x, lg = xs[j % len(xs)], ls[j % len(ls)]
             T = x.shape[0]
             e = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
             e[0].record(stream)
@@ -278,18 +294,18 @@ def time_stages(layers, xs, ls, outs, rounds):
 
 def time_kernel(layers, xs, ls, phase, passes=5):
     """Average duration (us) of one expert-GEMM kernel (phase 0: gate_up + SwiGLU,
-    1: down).  Every layer copy is routed (and its gate_up run) first; then each
-    launch of the phase carries its own pair of HIP events, stamped by the
-    dispatch at the kernel's start and end (nkt_moe_experts_phase_timed), on the
-    stream the kernel runs on.  A sleep kernel keeps the host ahead so the
-    launches run back to back over the rotating weight copies."""
+    1: down).  Each pass routes every layer copy i on input step_input(p L + i, L)
+    (and, for the down kernel, runs its gate_up), then runs the phase once per
+    copy, back to back, each launch with its own pair of HIP events, stamped by
+    the dispatch at the kernel's start and end (nkt_moe_experts_phase_timed), on
+    the stream the kernel runs on.  A sleep kernel keeps the host ahead so the
+    launches run back to back over the rotating weight copies; a copy's routing
+    changes from pass to pass, so no pass finds the previous one's experts in
+    the last-level cache."""
     import torch
 
     T = xs[0].shape[0]
-    for i, layer in enumerate(layers):
-        layer.route(ls[i % len(ls)])
-        layer.expert_phase(0, xs[i % len(xs)], T)
-    torch.cuda.synchronize()
+    L = len(layers)
     stream = torch.cuda.current_stream()
     pairs = []
     for _ in range(passes * len(layers)):
@@ -303,10 +319,15 @@ def time_kernel(layers, xs, ls, phase, passes=5):
     except Exception:
         pass
     n = 0
-    for _ in range(passes):
-        for i, layer in enumerate(layers):
+    for p in range(passes):
+        inputs = [step_input(p * L + i, L) for i in range(L)]
+        for layer, j in zip(layers, inputs):
+            layer.route(ls[j % len(ls)])
+            if phase == 1:
+                layer.expert_phase(0, xs[j % len(xs)], T)
+        for layer, j in zip(layers, inputs):
             a, b = pairs[n]
-            layer.expert_phase_timed(phase, xs[i % len(xs)] if phase == 0 else None, T, a, b)
+            layer.expert_phase_timed(phase, xs[j % len(xs)] if phase == 0 else None, T, a, b)
             n += 1
     torch.cuda.synchronize()
     times = [a.elapsed_time(b) * 1e3 for a, b in pairs]
