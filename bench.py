@@ -638,7 +638,7 @@ def _phase_of(name):
         return None
     args = [a.strip() for a in m.group(2).split(",")]
     # template arguments: gemv_kernel<WF, PHASE, ...>, gemm2_kernel<WF, PHASE, NW>,
-    # gemm_kernel<WF, BM, NW, RT, PHASE, ...>, gemm2_i8_kernel<PHASE, F16>, gemm2_i4_kernel<PHASE>
+    # gemm_kernel<WF, BM, NW, RT, PHASE, ...>, gemm2_i8_kernel<PHASE, F16>, gemm2_i4_kernel<PHASE, NARROW>
     idx = {"gemm2_i8_kernel": 0, "gemm2_i4_kernel": 0, "gemm_kernel": 4}.get(m.group(1), 1)
     val = args[idx].split(")")[-1]
     return "gate_up" if val == "0" else "down"

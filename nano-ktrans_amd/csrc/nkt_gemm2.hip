@@ -15,6 +15,9 @@
 //     register ring);
 //   * gemm2_kernel (bf16 weights, and int8 / int4 operands past the
 //     pipelines' 32-bit buffer offsets): the register-staged form below.
+// The two pipelines also hold copies that compute only the first 16 / 32
+// positions of a tile, taken by tiles with no more (an expert's last or
+// only tile): the matrix-core work of empty column tiles is skipped.
 // Tile = 64 positions x 256 weight rows.  gate_up: the 256 rows are 128 gate
 // rows and the 128 matching up rows (a wave holds gate and up rows for the
 // same h columns, so SwiGLU is wave-local); down: 256 output rows split over
@@ -633,26 +636,31 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
 #pragma unroll
     for (int c = 0; c < kCT; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // one stage's token fragments (2 K steps x 4 column tiles)
+  // one stage's token fragments (2 K steps x the first NC of the 4 column
+  // tiles: a tile of at most 16 / 32 positions, an expert's last or only one,
+  // runs only 1 / 2 column tiles' fragment reads and matrix-core work; the
+  // other sums stay zero and are never stored)
   typedef u32x4 TokFrags[2][kCT];
-  auto read_tok = [&](TokFrags& f, const uint8_t* tb) {
+  auto read_tok = [&](auto nc, TokFrags& f, const uint8_t* tb) {
+    constexpr int NC = decltype(nc)::value;
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
-      for (int c = 0; c < kCT; ++c) {
+      for (int c = 0; c < NC; ++c) {
         const int p = c * 16 + (lane & 15);
         const int chunk = 4 * s + (lane >> 4);
         f[s][c] = *(const u32x4*)(tb + p * (kI8Stage * 2) + ((chunk ^ ((p >> 1) & 7)) * 16));
       }
   };
-  auto mma = [&](const u32x4 (&w)[kRT], const TokFrags& f) {
+  auto mma = [&](auto nc, const u32x4 (&w)[kRT], const TokFrags& f) {
+    constexpr int NC = decltype(nc)::value;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       u32x4 ad[kRT];
 #pragma unroll
       for (int r = 0; r < kRT; ++r) ad[r] = F16 ? dq_i8_f16(w[r][2 * s], w[r][2 * s + 1]) : dq_i8(w[r][2 * s], w[r][2 * s + 1]);
 #pragma unroll
-      for (int c = 0; c < kCT; ++c)
+      for (int c = 0; c < NC; ++c)
 #pragma unroll
         for (int r = 0; r < kRT; ++r)
           acc[r][c] = F16 ? mfma_f16(ad[r], f[s][c], acc[r][c]) : mfma_bf16(ad[r], f[s][c], acc[r][c]);
@@ -664,60 +672,75 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
   // issue order: T0, T1, W0, T2, W1, then per step x: T(x + 3), W(x + 2);
   // at step x the newest 6 loads are T(x + 2) and W(x + 1), so waiting for
   // all but 6 covers T(x + 1) and W(x)
-  auto step = [&](TokFrags& cur, TokFrags& nxt, const u32x4 (&wcur)[kRT], u32x4 (&wnew)[kRT], uint8_t* tb_x,
-                  const uint8_t* tb_n, int x) {
+  auto step = [&](auto nc, TokFrags& cur, TokFrags& nxt, const u32x4 (&wcur)[kRT], u32x4 (&wnew)[kRT],
+                  uint8_t* tb_x, const uint8_t* tb_n, int x) {
     __asm__ volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6)
     lds_barrier();
     issue_tok(x + 3, tb_x);
     issue_w(x + 2, wnew);
-    read_tok(nxt, tb_n);
-    mma(wcur, cur);
+    read_tok(nc, nxt, tb_n);
+    mma(nc, wcur, cur);
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  EpiPre<kRT> pre;
-  float rv[16], rxi = 0.f;
-  pre.valid = i8_row_terms<F16>(a, srcl, rv, rxi, kpart * (Kp / 128), Kp / 128);
-  if (pre.valid) {
+  // the rest of the item for the first NC column tiles, one copy of the
+  // pipeline per NC (a branch per column tile inside one copy cost more than
+  // it saved on full tiles); measured against always 4: Qwen3 int8 T = 128
+  // (even routing) 142.7 -> 134.2 us per layer, Qwen1.5-MoE T = 128 / 1024
+  // 172.4 -> 163.3 / 243.5 -> 236.8, Qwen3 int8 Zipf T = 1024 / 4096
+  // 176.2 -> 173.3 / 441.9 -> 433.5, T = 512 unchanged
+  auto run = [&](auto nc) {
+    EpiPre<kRT> pre;
+    float rv[16], rxi = 0.f;
+    pre.valid = i8_row_terms<F16>(a, srcl, rv, rxi, kpart * (Kp / 128), Kp / 128);
+    if (pre.valid) {
 #pragma unroll
-    for (int r = 0; r < kRT; ++r) pre.s[r] = *(const u32x2*)(sexp + wrow[r] + 4 * (lane >> 4));
-  }
-  issue_tok(0, tb0);
-  issue_tok(1, tb1);
-  issue_w(0, w0);
-  issue_tok(2, tb2);
-  issue_w(1, w1);
-  if (pre.valid) i8_row_terms_store(Kp / 128, xtot_l, xinv_l, rv, rxi, F16);
-  __asm__ volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0x0F7C);  // vmcnt(12): T0 landed
-  lds_barrier();
-  read_tok(f0, tb0);
-  // six steps per iteration return fragments, weight registers and buffers
-  // to their starting roles; the last NS % 6 steps follow
-  int x = 0;
-  for (; x + 6 <= NS; x += 6) {
-    step(f0, f1, w0, w2, tb0, tb1, x);
-    step(f1, f0, w1, w0, tb1, tb2, x + 1);
-    step(f0, f1, w2, w1, tb2, tb0, x + 2);
-    step(f1, f0, w0, w2, tb0, tb1, x + 3);
-    step(f0, f1, w1, w0, tb1, tb2, x + 4);
-    step(f1, f0, w2, w1, tb2, tb0, x + 5);
-  }
-  const int rest = NS - x;
-  if (rest >= 1) step(f0, f1, w0, w2, tb0, tb1, x);
-  if (rest >= 2) step(f1, f0, w1, w0, tb1, tb2, x + 1);
-  if (rest >= 3) step(f0, f1, w2, w1, tb2, tb0, x + 2);
-  if (rest >= 4) step(f1, f0, w0, w2, tb0, tb1, x + 3);
-  if (rest >= 5) step(f0, f1, w1, w0, tb1, tb2, x + 4);
-  wait_vmem();  // out-of-range loads past the last stage land before the LDS is reused
-  __syncthreads();
-  // down's compact y staging: 16 rows of 144 B per wave in the token
-  // buffers, free once every wave has passed the barrier above
-  uint8_t* stage = wave < 3 ? tb0 + wave * 2304 : tb1;
-  gemm2_epilogue<WF_I8, PHASE, kWaves, F16>(a, acc, srcl, orow_l, hpart, xtot_l, xinv_l, wrow, sexp, it.row0, it.rows,
-                                            it.slab, &pre, PHASE == PHASE_DOWN ? stage : nullptr,
-                                            (int64_t)kpart * a.num_rows * a.N);
+      for (int r = 0; r < kRT; ++r) pre.s[r] = *(const u32x2*)(sexp + wrow[r] + 4 * (lane >> 4));
+    }
+    issue_tok(0, tb0);
+    issue_tok(1, tb1);
+    issue_w(0, w0);
+    issue_tok(2, tb2);
+    issue_w(1, w1);
+    if (pre.valid) i8_row_terms_store(Kp / 128, xtot_l, xinv_l, rv, rxi, F16);
+    __asm__ volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0x0F7C);  // vmcnt(12): T0 landed
+    lds_barrier();
+    read_tok(nc, f0, tb0);
+    // six steps per iteration return fragments, weight registers and buffers
+    // to their starting roles; the last NS % 6 steps follow
+    int x = 0;
+    for (; x + 6 <= NS; x += 6) {
+      step(nc, f0, f1, w0, w2, tb0, tb1, x);
+      step(nc, f1, f0, w1, w0, tb1, tb2, x + 1);
+      step(nc, f0, f1, w2, w1, tb2, tb0, x + 2);
+      step(nc, f1, f0, w0, w2, tb0, tb1, x + 3);
+      step(nc, f0, f1, w1, w0, tb1, tb2, x + 4);
+      step(nc, f1, f0, w2, w1, tb2, tb0, x + 5);
+    }
+    const int rest = NS - x;
+    if (rest >= 1) step(nc, f0, f1, w0, w2, tb0, tb1, x);
+    if (rest >= 2) step(nc, f1, f0, w1, w0, tb1, tb2, x + 1);
+    if (rest >= 3) step(nc, f0, f1, w2, w1, tb2, tb0, x + 2);
+    if (rest >= 4) step(nc, f1, f0, w0, w2, tb0, tb1, x + 3);
+    if (rest >= 5) step(nc, f0, f1, w1, w0, tb1, tb2, x + 4);
+    wait_vmem();  // out-of-range loads past the last stage land before the LDS is reused
+    __syncthreads();
+    // down's compact y staging: 16 rows of 144 B per wave in the token
+    // buffers, free once every wave has passed the barrier above
+    uint8_t* stage = wave < 3 ? tb0 + wave * 2304 : tb1;
+    gemm2_epilogue<WF_I8, PHASE, kWaves, F16>(a, acc, srcl, orow_l, hpart, xtot_l, xinv_l, wrow, sexp, it.row0, it.rows,
+                                              it.slab, &pre, PHASE == PHASE_DOWN ? stage : nullptr,
+                                              (int64_t)kpart * a.num_rows * a.N);
+  };
+  const int urows = __builtin_amdgcn_readfirstlane(it.rows);
+  if (urows <= 16)
+    run(std::integral_constant<int, 1>{});
+  else if (urows <= 32)
+    run(std::integral_constant<int, 2>{});
+  else
+    run(std::integral_constant<int, kCT>{});
 }
 
 // Per-row sums of each 128-wide K group of a bf16 matrix [rows, K] -> fp32
@@ -798,7 +821,7 @@ bool gemm2_supported(int wf, int phase, int N, int K, int I) {
 constexpr int kI4TokBytes = kBM * 256;
 constexpr int kI4SxBytes = 8 * 512;  // per wave: 256 B scales (64 used), 256 B group sums
 
-template <int PHASE>
+template <int PHASE, bool NARROW>
 __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slabs, int sg) {
   constexpr int kWaves = 8;
   constexpr int kRT = 2;
@@ -876,12 +899,13 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
 #pragma unroll
     for (int c = 0; c < kCT; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // all 8 (row tile, column tile) temporaries advance one K step at a time,
-  // so no MFMA waits on the one before it
-  auto compute = [&](const u32x4 (&w)[kRT], const uint8_t* tb, const uint8_t* sx) {
+  // all (row tile, column tile) temporaries advance one K step at a time,
+  // so no MFMA waits on the one before it; only the first NC column tiles
+  auto compute = [&](auto nc, const u32x4 (&w)[kRT], const uint8_t* tb, const uint8_t* sx) {
+    constexpr int NC = decltype(nc)::value;
     u32x4 bf[kCT][4];
 #pragma unroll
-    for (int c = 0; c < kCT; ++c) {
+    for (int c = 0; c < NC; ++c) {
       const int p = c * 16 + (lane & 15);
 #pragma unroll
       for (int s = 0; s < 4; ++s) bf[c][s] = *(const u32x4*)(tb + p * 256 + (((4 * s + (lane >> 4)) ^ (p & 15)) * 16));
@@ -896,7 +920,7 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
     }
     f32x4 tmp[kRT][kCT];
 #pragma unroll
-    for (int c = 0; c < kCT; ++c) {
+    for (int c = 0; c < NC; ++c) {
       const float cv = -136.0f * *(const float*)(sx + sofs + 256 + (c * 16 + (lane & 15)) * 4);
 #pragma unroll
       for (int r = 0; r < kRT; ++r) tmp[r][c] = f32x4{cv, cv, cv, cv};
@@ -904,39 +928,74 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
-      for (int c = 0; c < kCT; ++c)
+      for (int c = 0; c < NC; ++c)
 #pragma unroll
         for (int r = 0; r < kRT; ++r) tmp[r][c] = mfma_bf16(ad[r][s], bf[c][s], tmp[r][c]);
 #pragma unroll
-    for (int c = 0; c < kCT; ++c)
+    for (int c = 0; c < NC; ++c)
 #pragma unroll
       for (int r = 0; r < kRT; ++r) acc[r][c] += sc[r] * tmp[r][c];
   };
 
   u32x4 w0[kRT], w1[kRT], w2[kRT];
-  auto step = [&](const u32x4 (&wcur)[kRT], u32x4 (&wn2)[kRT], const uint8_t* tb_x, const uint8_t* sx_x,
+  auto step = [&](auto nc, const u32x4 (&wcur)[kRT], u32x4 (&wn2)[kRT], const uint8_t* tb_x, const uint8_t* sx_x,
                   uint8_t* tb_n2, uint8_t* sx_n2, int x) {
     __asm__ volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6): stage x landed (stage x + 1's 6 may fly)
     lds_barrier();
     issue(x + 2, tb_n2, sx_n2, wn2);
-    compute(wcur, tb_x, sx_x);
+    compute(nc, wcur, tb_x, sx_x);
     __builtin_amdgcn_sched_barrier(0);
   };
-  issue(0, tb0, sx0, w0);
-  issue(1, tb1, sx1, w1);
-  // three steps per iteration return ring slots and buffers to their roles
-  int x = 0;
-  for (; x + 3 <= G; x += 3) {
-    step(w0, w2, tb0, sx0, tb2, sx2, x);
-    step(w1, w0, tb1, sx1, tb0, sx0, x + 1);
-    step(w2, w1, tb2, sx2, tb1, sx1, x + 2);
+  // the pipeline over the first NC column tiles, one copy per NC
+  auto run = [&](auto nc) {
+    issue(0, tb0, sx0, w0);
+    issue(1, tb1, sx1, w1);
+    // three steps per iteration return ring slots and buffers to their roles
+    int x = 0;
+    for (; x + 3 <= G; x += 3) {
+      step(nc, w0, w2, tb0, sx0, tb2, sx2, x);
+      step(nc, w1, w0, tb1, sx1, tb0, sx0, x + 1);
+      step(nc, w2, w1, tb2, sx2, tb1, sx1, x + 2);
+    }
+    if (x < G) step(nc, w0, w2, tb0, sx0, tb2, sx2, x);
+    if (x + 1 < G) step(nc, w1, w0, tb1, sx1, tb0, sx0, x + 1);
+    wait_vmem();  // out-of-range loads past the last stage land before the LDS is reused
+    __syncthreads();
+    gemm2_epilogue<WF_I4, PHASE, kWaves>(a, acc, srcl, orow_l, hpart, xtot_l, xtot_l, wrow, sexp, it.row0, it.rows,
+                                         it.slab);
+  };
+  // NARROW (experts average at most 24 positions): a tile of at most 32
+  // positions, an expert's last or only one, runs 2 of its 4 column tiles.
+  // Measured: Qwen3 int4 T = 300 (even routing) 149 -> 124.6 us per layer;
+  // at 32 positions per expert (T = 512) it gained nothing (lost 3 % with
+  // Zipf routing), and where experts hold many full tiles the second copy
+  // cost 1 - 5 % (Mixtral T = 2048, Qwen3 int4 Zipf T = 2048), hence the
+  // launch-wide switch
+  if constexpr (NARROW) {
+    if (__builtin_amdgcn_readfirstlane(it.rows) <= 32)
+      run(std::integral_constant<int, 2>{});
+    else
+      run(std::integral_constant<int, kCT>{});
+  } else {
+    // (the same pipeline written out: a launch of full tiles keeps the
+    // schedule the compiler gives it without the lambda, 1 - 2 % faster)
+    const std::integral_constant<int, kCT> nc;
+    issue(0, tb0, sx0, w0);
+    issue(1, tb1, sx1, w1);
+    int x = 0;
+    for (; x + 3 <= G; x += 3) {
+      step(nc, w0, w2, tb0, sx0, tb2, sx2, x);
+      step(nc, w1, w0, tb1, sx1, tb0, sx0, x + 1);
+      step(nc, w2, w1, tb2, sx2, tb1, sx1, x + 2);
+    }
+    if (x < G) step(nc, w0, w2, tb0, sx0, tb2, sx2, x);
+    if (x + 1 < G) step(nc, w1, w0, tb1, sx1, tb0, sx0, x + 1);
+    wait_vmem();
+    __syncthreads();
+    gemm2_epilogue<WF_I4, PHASE, kWaves>(a, acc, srcl, orow_l, hpart, xtot_l, xtot_l, wrow, sexp, it.row0, it.rows,
+                                         it.slab);
   }
-  if (x < G) step(w0, w2, tb0, sx0, tb2, sx2, x);
-  if (x + 1 < G) step(w1, w0, tb1, sx1, tb0, sx0, x + 1);
-  wait_vmem();  // out-of-range loads past the last stage land before the LDS is reused
-  __syncthreads();
-  gemm2_epilogue<WF_I4, PHASE, kWaves>(a, acc, srcl, orow_l, hpart, xtot_l, xtot_l, wrow, sexp, it.row0, it.rows, it.slab);
 }
 
 // Input of the int8 gate_up on the fp16 matrix cores, one wave per row: the
@@ -1133,10 +1192,14 @@ hipError_t launch_gemm2(const GemmArgs& a, int wf, int phase, int max_tiles, hip
     return hipGetLastError();
   }
   if (gemm2_i4_pipeline(a, wf)) {
-    if (phase == PHASE_GATE_UP)
-      launch_timed(gemm2_i4_kernel<PHASE_GATE_UP>, grid, block, 0, stream, tm, a, n_slabs, sg);
+    if (phase == PHASE_GATE_UP && a.narrow_tiles)
+      launch_timed(gemm2_i4_kernel<PHASE_GATE_UP, true>, grid, block, 0, stream, tm, a, n_slabs, sg);
+    else if (phase == PHASE_GATE_UP)
+      launch_timed(gemm2_i4_kernel<PHASE_GATE_UP, false>, grid, block, 0, stream, tm, a, n_slabs, sg);
+    else if (a.narrow_tiles)
+      launch_timed(gemm2_i4_kernel<PHASE_DOWN, true>, grid, block, 0, stream, tm, a, n_slabs, sg);
     else
-      launch_timed(gemm2_i4_kernel<PHASE_DOWN>, grid, block, 0, stream, tm, a, n_slabs, sg);
+      launch_timed(gemm2_i4_kernel<PHASE_DOWN, false>, grid, block, 0, stream, tm, a, n_slabs, sg);
     return hipGetLastError();
   }
   switch (wf) {
