@@ -106,6 +106,20 @@ def test_qwen3_int4_full(gpu_device, T):
     _check(layer, native, T)
 
 
+@pytest.mark.parametrize("name,E,T", [("qwen3_int4", None, 300), ("qwen3_int4", 32, 90),
+                                      ("qwen3_int8", 32, 40), ("qwen3_int8", 32, 100)])
+def test_prefill_short_tile_copies(gpu_device, name, E, T):
+    """Prefill tiles of at most 16 / 32 positions (an expert's last or only
+    tile) run pipeline copies over their first 1 / 2 column tiles: int8
+    always (the Zipf-skewed qwen3_int8 routing gives tiles of every size),
+    int4 where the experts average at most 24 positions (T k <= 24 E: 18.75
+    and 22.5 per expert here, tiles of 5 - 40 positions)."""
+    announce(f"forward {name} E={E} T={T} (short prefill tiles)")
+    layer, native = _layer(name, E=E)
+    assert not layer.cfg.decode_form(T)
+    _check(layer, native, T, seed=41)
+
+
 @pytest.mark.parametrize("T", [16, 200, 512])
 def test_qwen3_int8_cut_experts(gpu_device, T):
     announce(f"forward qwen3_int8 E=32 T={T}")
