@@ -78,6 +78,7 @@ int slab_group(int n_slabs, int64_t expert_bytes) { return expert_bytes > (4 << 
 
 struct TileItem {
   int expert, row0, rows, slab;
+  bool only;  // the expert's only tile: no other item reads this slab
 };
 
 __device__ __forceinline__ bool gemm2_item(const GemmArgs& a, int n_slabs, int sg, TileItem& it) {
@@ -104,13 +105,17 @@ __device__ __forceinline__ bool gemm2_item(const GemmArgs& a, int n_slabs, int s
   }
   if (a.n_tiles) {
     const int4 rec = *(const int4*)(a.tiles + 4 * tile);
+    // an expert's tiles are consecutive records, its full ones first
+    const int prev = tile > 0 ? a.tiles[4 * (tile - 1)] : -1;
     it.expert = rec.x;
     it.row0 = rec.y;
     it.rows = rec.z;
+    it.only = rec.z < kBM && prev != rec.x;
   } else {
     it.expert = 0;
     it.row0 = tile * kBM;
     it.rows = min(kBM, a.num_rows - it.row0);
+    it.only = a.num_rows <= kBM;
   }
   return true;
 }
@@ -622,12 +627,14 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
       __builtin_amdgcn_raw_ptr_buffer_load_lds(tres, (__attribute__((address_space(3))) void*)(tb + tofs + j * 1024),
                                                16, live ? tsrc[j] + st * (kI8Stage * 2u) : kI8Skip, 0, 0, 0);
   };
-  // stage st's 4 weight blocks into registers
-  auto issue_w = [&](int st, u32x4 (&w)[kRT]) {
+  // stage st's 4 weight blocks into registers, with the copy's load policy
+  // (nt for an expert's only tile: no other item reads its weights)
+  auto issue_w = [&](auto nc, int st, u32x4 (&w)[kRT]) {
+    constexpr int kPolicy = decltype(nc)::value >> 4;
     const bool live = st < NS;
 #pragma unroll
     for (int r = 0; r < kRT; ++r)
-      w[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, live ? wsrc[r] + st * 1024u : kI8Skip, 0, 0));
+      w[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, live ? wsrc[r] + st * 1024u : kI8Skip, 0, kPolicy));
   };
 
   f32x4 acc[kRT][kCT];
@@ -642,7 +649,7 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
   // other sums stay zero and are never stored)
   typedef u32x4 TokFrags[2][kCT];
   auto read_tok = [&](auto nc, TokFrags& f, const uint8_t* tb) {
-    constexpr int NC = decltype(nc)::value;
+    constexpr int NC = decltype(nc)::value & 15;
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
@@ -653,7 +660,7 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
       }
   };
   auto mma = [&](auto nc, const u32x4 (&w)[kRT], const TokFrags& f) {
-    constexpr int NC = decltype(nc)::value;
+    constexpr int NC = decltype(nc)::value & 15;
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       u32x4 ad[kRT];
@@ -678,7 +685,7 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
     __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6)
     lds_barrier();
     issue_tok(x + 3, tb_x);
-    issue_w(x + 2, wnew);
+    issue_w(nc, x + 2, wnew);
     read_tok(nc, nxt, tb_n);
     mma(nc, wcur, cur);
     __builtin_amdgcn_sched_barrier(0);
@@ -700,9 +707,9 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
     }
     issue_tok(0, tb0);
     issue_tok(1, tb1);
-    issue_w(0, w0);
+    issue_w(nc, 0, w0);
     issue_tok(2, tb2);
-    issue_w(1, w1);
+    issue_w(nc, 1, w1);
     if (pre.valid) i8_row_terms_store(Kp / 128, xtot_l, xinv_l, rv, rxi, F16);
     __asm__ volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0x0F7C);  // vmcnt(12): T0 landed
@@ -734,13 +741,27 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
                                               it.slab, &pre, PHASE == PHASE_DOWN ? stage : nullptr,
                                               (int64_t)kpart * a.num_rows * a.N);
   };
+  // copy tag: column tiles | weight load policy << 4.  Measured against
+  // short-tile copies with the default policy throughout: Qwen3 int8 T =
+  // 128 / 256 (even routing) 133 / 141 -> 126 / 131 us per layer, Qwen1.5-MoE
+  // T = 128 / 320 163 / 153 -> 155 / 144, Zipf routing and Qwen1.5 T = 1024
+  // level; the nt policy for every short tile (an expert's last of several
+  // too) lost 5 - 8 % at Qwen1.5 T = 1024, whose experts end in such tiles
   const int urows = __builtin_amdgcn_readfirstlane(it.rows);
-  if (urows <= 16)
-    run(std::integral_constant<int, 1>{});
-  else if (urows <= 32)
-    run(std::integral_constant<int, 2>{});
-  else
+  const bool only = __builtin_amdgcn_readfirstlane((int)it.only) != 0;
+  if (urows <= 16) {
+    if (only)
+      run(std::integral_constant<int, 1 | 2 << 4>{});
+    else
+      run(std::integral_constant<int, 1>{});
+  } else if (urows <= 32) {
+    if (only)
+      run(std::integral_constant<int, 2 | 2 << 4>{});
+    else
+      run(std::integral_constant<int, 2>{});
+  } else {
     run(std::integral_constant<int, kCT>{});
+  }
 }
 
 // Per-row sums of each 128-wide K group of a bf16 matrix [rows, K] -> fp32
