@@ -898,8 +898,10 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
   const int tofs = wave * 2048;  // this wave's slice of a token buffer
   const int sofs = wave * 512;   // and of a scale / group-sum buffer
 
-  // stage st's 6 loads (st >= G: out of range, no traffic)
-  auto issue = [&](int st, uint8_t* tb, uint8_t* sx, u32x4 (&w)[kRT]) {
+  // stage st's 6 loads (st >= G: out of range, no traffic), the weights
+  // with the copy's load policy (tag >> 4: nt for an expert's only tile)
+  auto issue = [&](auto nc, int st, uint8_t* tb, uint8_t* sx, u32x4 (&w)[kRT]) {
+    constexpr int kPolicy = decltype(nc)::value >> 4;
     const bool live = st < G;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -911,7 +913,7 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
                                              live ? xsrc + st * 4u : kI8Skip, 0, 0, 0);
 #pragma unroll
     for (int r = 0; r < kRT; ++r)
-      w[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, live ? wsrc[r] + st * 1024u : kI8Skip, 0, 0));
+      w[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, live ? wsrc[r] + st * 1024u : kI8Skip, 0, kPolicy));
   };
 
   f32x4 acc[kRT][kCT];
@@ -923,7 +925,7 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
   // all (row tile, column tile) temporaries advance one K step at a time,
   // so no MFMA waits on the one before it; only the first NC column tiles
   auto compute = [&](auto nc, const u32x4 (&w)[kRT], const uint8_t* tb, const uint8_t* sx) {
-    constexpr int NC = decltype(nc)::value;
+    constexpr int NC = decltype(nc)::value & 15;
     u32x4 bf[kCT][4];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
@@ -964,14 +966,14 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
     __asm__ volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0x0F76);  // vmcnt(6): stage x landed (stage x + 1's 6 may fly)
     lds_barrier();
-    issue(x + 2, tb_n2, sx_n2, wn2);
+    issue(nc, x + 2, tb_n2, sx_n2, wn2);
     compute(nc, wcur, tb_x, sx_x);
     __builtin_amdgcn_sched_barrier(0);
   };
   // the pipeline over the first NC column tiles, one copy per NC
   auto run = [&](auto nc) {
-    issue(0, tb0, sx0, w0);
-    issue(1, tb1, sx1, w1);
+    issue(nc, 0, tb0, sx0, w0);
+    issue(nc, 1, tb1, sx1, w1);
     // three steps per iteration return ring slots and buffers to their roles
     int x = 0;
     for (; x + 3 <= G; x += 3) {
@@ -987,23 +989,30 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
                                          it.slab);
   };
   // NARROW (experts average at most 24 positions): a tile of at most 32
-  // positions, an expert's last or only one, runs 2 of its 4 column tiles.
+  // positions, an expert's last or only one, runs 2 of its 4 column tiles,
+  // an only tile with nt weight loads (T = 300 / 384 a further 124.5 / 130.9
+  // -> 120.2 / 126.3 us).
   // Measured: Qwen3 int4 T = 300 (even routing) 149 -> 124.6 us per layer;
   // at 32 positions per expert (T = 512) it gained nothing (lost 3 % with
   // Zipf routing), and where experts hold many full tiles the second copy
   // cost 1 - 5 % (Mixtral T = 2048, Qwen3 int4 Zipf T = 2048), hence the
   // launch-wide switch
   if constexpr (NARROW) {
-    if (__builtin_amdgcn_readfirstlane(it.rows) <= 32)
-      run(std::integral_constant<int, 2>{});
-    else
+    // copy tag: column tiles | weight load policy << 4
+    if (__builtin_amdgcn_readfirstlane(it.rows) <= 32) {
+      if (__builtin_amdgcn_readfirstlane((int)it.only) != 0)
+        run(std::integral_constant<int, 2 | 2 << 4>{});
+      else
+        run(std::integral_constant<int, 2>{});
+    } else {
       run(std::integral_constant<int, kCT>{});
+    }
   } else {
     // (the same pipeline written out: a launch of full tiles keeps the
     // schedule the compiler gives it without the lambda, 1 - 2 % faster)
     const std::integral_constant<int, kCT> nc;
-    issue(0, tb0, sx0, w0);
-    issue(1, tb1, sx1, w1);
+    issue(nc, 0, tb0, sx0, w0);
+    issue(nc, 1, tb1, sx1, w1);
     int x = 0;
     for (; x + 3 <= G; x += 3) {
       step(nc, w0, w2, tb0, sx0, tb2, sx2, x);
