@@ -266,14 +266,14 @@ def test_shared_chunks_int4_and_bf16(gpu_device, wfmt, T):
     assert torch.equal(h_layer, h_stage)
 
 
-@pytest.mark.parametrize("T", [1, 16, 72, 75, 76, 200])
+@pytest.mark.parametrize("T", [1, 16, 64, 67, 68, 200])
 def test_qwen15_shared_full(gpu_device, T):
-    """T = 72 / 75: 4.8 / 5 positions per expert, the int8 decode form's
+    """T = 64 / 67: 4.3 / 4.47 positions per expert, the int8 decode form's
     last token counts (the shared expert as 5 chunk tiles per chunk in the
-    routed launches); T = 76 the first in the prefill form."""
+    routed launches); T = 68 the first in the prefill form."""
     announce(f"forward qwen15_int8_shared full T={T}")
     layer, native = _layer("qwen15_int8_shared")
-    assert layer.cfg.decode_form(T) == (T <= 75)
+    assert layer.cfg.decode_form(T) == (T <= 67)
     _check(layer, native, T)
 
 
