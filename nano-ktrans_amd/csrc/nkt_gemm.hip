@@ -344,12 +344,12 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(GemmArgs a) {
 // configuration table
 // ---------------------------------------------------------------------------
 // Tokens per expert (T k / E) up to which the decode form runs, from the
-// measured crossover of the two forms' layer times: int8 weights 4.5 (the
-// decode form wins at 4.3 tokens per expert, the prefill form, its short
-// tiles on copies that skip empty column tiles, at 5 under even and skewed
-// routing alike), int4 ~16 (its decode form streams half the bytes of int8
-// per MFMA operand), others 12.
-double decode_form_max_avg(int wf) { return wf == WF_I8 ? 4.5 : wf == WF_I4 ? 16.0 : 12.0; }
+// measured crossover of the two forms' layer times, with the prefill form's
+// short tiles on copies that skip empty column tiles: int8 weights 4.5 (the
+// decode form wins at 4.3 tokens per expert, the prefill form at 5 under
+// even and skewed routing alike), int4 12 (decode wins at 10, the forms are
+// level at 12, prefill wins at 16: Mixtral T = 64 285 -> 225 us), others 12.
+double decode_form_max_avg(int wf) { return wf == WF_I8 ? 4.5 : 12.0; }
 
 int gemm_tile_m(int num_tokens, int topk, int num_experts, int wf, bool prefill_form) {
   const double avg = (double)num_tokens * topk / (double)num_experts;
