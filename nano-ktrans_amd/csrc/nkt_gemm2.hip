@@ -17,7 +17,8 @@
 //     pipelines' 32-bit buffer offsets): the register-staged form below.
 // The two pipelines also hold copies that compute only the first 16 / 32
 // positions of a tile, taken by tiles with no more (an expert's last or
-// only tile): the matrix-core work of empty column tiles is skipped.
+// only tile): the matrix-core work of empty column tiles is skipped, and an
+// expert's only tile loads its weights non-temporally.
 // Tile = 64 positions x 256 weight rows.  gate_up: the 256 rows are 128 gate
 // rows and the 128 matching up rows (a wave holds gate and up rows for the
 // same h columns, so SwiGLU is wave-local); down: 256 output rows split over
@@ -988,10 +989,11 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
     gemm2_epilogue<WF_I4, PHASE, kWaves>(a, acc, srcl, orow_l, hpart, xtot_l, xtot_l, wrow, sexp, it.row0, it.rows,
                                          it.slab);
   };
-  // NARROW (experts average at most 24 positions): a tile of at most 32
-  // positions, an expert's last or only one, runs 2 of its 4 column tiles,
-  // an only tile with nt weight loads (T = 300 / 384 a further 124.5 / 130.9
-  // -> 120.2 / 126.3 us).
+  // NARROW (experts average at most 24 positions): a tile of at most 16 / 32
+  // positions, an expert's last or only one, runs 1 / 2 of its 4 column
+  // tiles, an only tile with nt weight loads (T = 300 / 384 a further 124.5 /
+  // 130.9 -> 120.2 / 126.3 us with the nt copy; the 1-tile copy then T = 200
+  // / 256 / 300 114.9 / 116 / 117.5 -> 104.8 / 112.1 / 114.1 us).
   // Measured: Qwen3 int4 T = 300 (even routing) 149 -> 124.6 us per layer;
   // at 32 positions per expert (T = 512) it gained nothing (lost 3 % with
   // Zipf routing), and where experts hold many full tiles the second copy
@@ -999,8 +1001,15 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
   // launch-wide switch
   if constexpr (NARROW) {
     // copy tag: column tiles | weight load policy << 4
-    if (__builtin_amdgcn_readfirstlane(it.rows) <= 32) {
-      if (__builtin_amdgcn_readfirstlane((int)it.only) != 0)
+    const int urows = __builtin_amdgcn_readfirstlane(it.rows);
+    const bool only = __builtin_amdgcn_readfirstlane((int)it.only) != 0;
+    if (urows <= 16) {
+      if (only)
+        run(std::integral_constant<int, 1 | 2 << 4>{});
+      else
+        run(std::integral_constant<int, 1>{});
+    } else if (urows <= 32) {
+      if (only)
         run(std::integral_constant<int, 2 | 2 << 4>{});
       else
         run(std::integral_constant<int, 2>{});
