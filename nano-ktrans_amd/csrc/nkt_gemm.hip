@@ -347,9 +347,11 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(GemmArgs a) {
 // measured crossover of the two forms' layer times, with the prefill form's
 // short tiles on copies that skip empty column tiles: int8 weights 4.5 (the
 // decode form wins at 4.3 tokens per expert, the prefill form at 5 under
-// even and skewed routing alike), int4 12 (decode wins at 10, the forms are
-// level at 12, prefill wins at 16: Mixtral T = 64 285 -> 225 us), others 12.
-double decode_form_max_avg(int wf) { return wf == WF_I8 ? 4.5 : 12.0; }
+// even and skewed routing alike), int4 8 (at 8 the forms are level under
+// even routing and the decode form wins under Zipf routing; at 10 - 16 the
+// prefill form wins: Qwen3 T = 192 107.8 -> 99.1 us, Mixtral T = 48 222 ->
+// 197, T = 64 285 -> 225), others 12.
+double decode_form_max_avg(int wf) { return wf == WF_I8 ? 4.5 : wf == WF_I4 ? 8.0 : 12.0; }
 
 int gemm_tile_m(int num_tokens, int topk, int num_experts, int wf, bool prefill_form) {
   const double avg = (double)num_tokens * topk / (double)num_experts;

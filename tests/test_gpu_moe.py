@@ -69,16 +69,17 @@ def test_qwen3_int4_cut_experts(gpu_device, T):
     _check(layer, native, T)
 
 
-@pytest.mark.parametrize("T", [32, 40, 48, 64, 72])
+@pytest.mark.parametrize("T", [17, 24, 32, 40, 64, 72])
 def test_qwen3_int4_decode_form_multi_tile_experts(gpu_device, T):
-    """Four experts picked by every token.  T = 32 .. 48: the decode form
-    (T k <= 12 E for int4 weights): each hot expert holds T positions in
+    """Four experts picked by every token.  T = 17 .. 32: the decode form
+    (T k <= 8 E for int4 weights): each hot expert holds T positions in
     ceil(T / 16) tiles, so the tile records past an expert's first tile and
-    its tiles' source columns of rank >= 16 are used; T = 64 / 72 are past
-    that form (prefill tiles: a full one and a short one per hot expert)."""
+    its tiles' source columns of rank >= 16 are used; T = 40 .. 72 are past
+    that form (prefill tiles: a full one and a short one per hot expert
+    from 64 on)."""
     announce(f"forward qwen3_int4 E=32 T={T} skewed")
     layer, native = _layer("qwen3_int4", E=32)
-    assert layer.cfg.decode_form(T) == (T <= 48)
+    assert layer.cfg.decode_form(T) == (T <= 32)
     bias = torch.zeros(32)
     bias[[3, 11, 20, 31]] = 30.0
     _check(layer, native, T, seed=9, bias=bias)
