@@ -65,7 +65,7 @@ struct GemmArgs {
   int k_parts;
   // prefill int4, nonzero: a tile of at most 16 / 32 positions (an expert's
   // last or only one) runs a copy of the pipeline over the first one / two of
-  // its four 16-position column tiles (set where experts average at most 24
+  // its four 16-position column tiles (set where experts average at most 32
   // positions)
   int narrow_tiles;
   // single-token decode gate_up that routes its token itself
