@@ -190,10 +190,17 @@ WsLayout ws_layout(const Handle* h, int T) {
   const size_t P = (size_t)T * h->k;
   const size_t es = h->act_bf16 ? 2 : 4;
   L.bm = gemm_tile_m(T > 0 ? T : 1, h->k, h->E, h->wf, prefill_form_ok(h, false));
-  // the shared expert takes every token as one group: its prefill-form grid
-  // (weight slabs x token tiles) stays far below the CU count until T is in
-  // the hundreds, while the decode form's split-K grid fills the GPU
-  L.bm_shared = (T <= kSharedDecodeMaxTokens && h->Is > 0 &&
+  // the shared expert takes every token as one group.  While the routed
+  // experts run in the decode form it does too (riding in their launches as
+  // chunk tiles where it can); once they run in the prefill form, its own
+  // prefill-form launches fork beside theirs on the side stream, which
+  // measured faster at every such T (Qwen1.5-MoE int8 T = 96 / 128 / 192 /
+  // 256 146 / 150 / 169 / 190 -> 129 / 133 / 137 / 138 us per layer), while
+  // inside the decode range the chunk tiles win (T = 48 / 64 121 / 132
+  // against 140 / 147).  Without the int8 / int4 prefill pipelines the
+  // decode form's split-K grid keeps it up to kSharedDecodeMaxTokens.
+  const bool shared_prefill = (h->wf == WF_I8 || h->wf == WF_I4) && prefill_form_ok(h, true) && L.bm != kTileSrcCols;
+  L.bm_shared = (T <= kSharedDecodeMaxTokens && h->Is > 0 && !shared_prefill &&
                  gemv_supported(h->wf, PHASE_GATE_UP, 2 * h->Is, h->H, h->Is) &&
                  gemv_supported(h->wf, PHASE_DOWN, h->H, h->Is, h->Is))
                     ? 16
