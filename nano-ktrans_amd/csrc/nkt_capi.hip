@@ -363,9 +363,11 @@ constexpr int kSpreadMinTokens = 16;
 
 // prep (nullable): the int8 gate_up's fp16 input to make in the routing
 // launch when routing takes the large-batch path (*prep_done says whether it
-// did)
+// did); prep_first: take that path for any T (a shared expert then forks
+// beside the routed experts as soon as the copy exists)
 int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, hipStream_t st,
-             char* err, size_t len, const GemmArgs* prep = nullptr, bool* prep_done = nullptr) {
+             char* err, size_t len, const GemmArgs* prep = nullptr, bool* prep_done = nullptr,
+             bool prep_first = false) {
   if (prep_done) *prep_done = false;
   if (!logits) {
     set_err(err, len, "null router_logits");
@@ -383,7 +385,8 @@ int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, 
   // more than 16 tokens: K1 on one wave per token over several workgroups,
   // the last to finish groups (Qwen3 int4 T = 64: 90 -> 83 us per layer);
   // up to 16 the one-workgroup route + group is as fast (measured T = 8 / 16)
-  if (T > kSpreadMinTokens && route_spread_ok(T, h->k, h->E, h->H, false)) {
+  const bool small_paths = !(prep && prep_first && h->act_bf16);
+  if (small_paths && T > kSpreadMinTokens && route_spread_ok(T, h->k, h->E, h->H, false)) {
     if (!check_hip(launch_route_spread(logits, h->act_bf16, nullptr, nullptr, nullptr, 0.f, nullptr, h->H, T, h->E,
                                        h->k, h->flags, L.bm, L.max_tiles, nullptr, ws_ptr<uint32_t>(ws, L, NKT_WS_SYNC),
                                        ws_ptr<uint32_t>(ws, L, kWsTagged), ids, wts, counts, offsets, perm, inv, tiles,
@@ -392,7 +395,7 @@ int do_route(Handle* h, const void* logits, int T, void* ws, const WsLayout& L, 
       return NKT_ERR;
     return NKT_OK;
   }
-  if (route_group_fused(T, h->k)) {
+  if (small_paths && route_group_fused(T, h->k)) {
     if (!check_hip(launch_route_group(logits, h->act_bf16, T, h->E, h->k, h->flags, L.bm, L.max_tiles,
                                       ids, wts, counts, offsets, perm, inv, tiles, n_tiles, tile_src,
                                       h->resident, ws_ptr<float>(ws, L, kWsWpos), st),
@@ -885,7 +888,9 @@ int run_layer(Handle* h, const void* x, int T, void* out, void* ws, const WsLayo
   // a few tokens from given logits: routing inside the gate_up launch
   const bool sr = sr_ok(h, T, L, logits, chunks);
   int rc = sr ? do_sr_gate_up(h, x, logits, T, ws, L, st, err, len)
-              : prep_in_route ? do_route(h, logits, T, ws, L, st, err, len, &g, &prep_done) : route();
+              : prep_in_route ? do_route(h, logits, T, ws, L, st, err, len, &g, &prep_done,
+                                         h->Is > 0 && chunks == 0 && allow_side && !side)
+                              : route();
   // a shared expert in the prefill form forks here, once the routing launch
   // has made the fp16 input copy both expert GEMMs read: its launches (a
   // dense down of few workgroups among them) run beside the routed experts'

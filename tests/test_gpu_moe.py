@@ -226,8 +226,12 @@ def test_mixtral_int4_cut_intermediate_prefill(gpu_device):
     _check(layer, native, 300)
 
 
-@pytest.mark.parametrize("T", [40, 600])
+@pytest.mark.parametrize("T", [20, 40, 64, 600])
 def test_small_int8_short_k(gpu_device, T):
+    """T = 20 / 40 / 64: the prefill form at a token count the one-launch
+    routing would take; with a shared expert the routing launch that makes
+    the fp16 input copy runs instead, and the shared expert forks beside
+    the routed experts."""
     announce(f"forward small_int8_shared T={T}")
     layer, native = _layer("small_int8_shared")
     _check(layer, native, T)
