@@ -76,7 +76,7 @@ extern "C" {
 #define NKT_WS_INV 5          /* int32 [T * k]  p -> pos */
 #define NKT_WS_H 6            /* act dtype [T*k, I]  SwiGLU activations by position */
 #define NKT_WS_Y 7            /* fp32 [T*k, H] expert outputs of nkt_moe_experts*: row = pair t*k + slot in the decode
-                                 form (T*k / E up to 4.5 for int8 weights, 8 for int4, 12 for the others), else
+                                 form (T*k / E up to 4.5 for int8 weights, 8 for int4 (6 for I >= 8192), 12 for the others), else
                                  position.  nkt_moe_forward* in the prefill form leaves it compact: fp16 [T*k, H] by
                                  position, each 256-column slab of a row times a power of two, then fp32 [T*k, H/256]
                                  with the inverse of each slab's factor; a one-token call (and a 2-4 token call with

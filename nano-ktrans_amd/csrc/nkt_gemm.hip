@@ -350,12 +350,16 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(GemmArgs a) {
 // even and skewed routing alike), int4 8 (at 8 the forms are level under
 // even routing and the decode form wins under Zipf routing; at 10 - 16 the
 // prefill form wins: Qwen3 T = 192 107.8 -> 99.1 us, Mixtral T = 48 222 ->
-// 197, T = 64 285 -> 225), others 12.
-double decode_form_max_avg(int wf) { return wf == WF_I8 ? 4.5 : wf == WF_I4 ? 8.0 : 12.0; }
+// 197, T = 64 285 -> 225) -- 6 for experts of I >= 8192, whose decode down
+// takes the long-K ring (Mixtral, T = 28 / 32: 189.6 / 194.8 -> 183.9 /
+// 180.5 us; level at 6, decode ahead at 5), others 12.
+double decode_form_max_avg(int wf, int I) {
+  return wf == WF_I8 ? 4.5 : wf == WF_I4 ? (I >= 8192 ? 6.0 : 8.0) : 12.0;
+}
 
-int gemm_tile_m(int num_tokens, int topk, int num_experts, int wf, bool prefill_form) {
+int gemm_tile_m(int num_tokens, int topk, int num_experts, int wf, bool prefill_form, int I) {
   const double avg = (double)num_tokens * topk / (double)num_experts;
-  if (avg <= decode_form_max_avg(wf)) return 16;
+  if (avg <= decode_form_max_avg(wf, I)) return 16;
   if (wf != WF_F32 && prefill_form) return kPrefillTileM;
   if (avg <= 40.0) return 32;
   return 64;

@@ -49,8 +49,9 @@ class MoEConfig:
     def decode_form(self, T: int) -> bool:
         """Whether the library runs a batch of T tokens in its decode form:
         up to 4.5 tokens per expert (T k / E) for int8 weights, 8 for int4
-        and 12 for the others."""
-        return T * self.k <= {"int8_per_channel": 4.5, "int4_g128": 8}.get(self.wfmt, 12) * self.E
+        (6 where I >= 8192) and 12 for the others."""
+        int4 = 6 if self.I >= 8192 else 8
+        return T * self.k <= {"int8_per_channel": 4.5, "int4_g128": int4}.get(self.wfmt, 12) * self.E
 
     def shared_in_routed_launches(self, T: int) -> bool:
         """Whether the layer runs the shared expert inside the routed experts'
