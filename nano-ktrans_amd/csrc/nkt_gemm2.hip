@@ -645,9 +645,9 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
     for (int c = 0; c < kCT; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // one stage's token fragments (2 K steps x the first NC of the 4 column
-  // tiles: a tile of at most 16 / 32 positions, an expert's last or only one,
-  // runs only 1 / 2 column tiles' fragment reads and matrix-core work; the
-  // other sums stay zero and are never stored)
+  // tiles: a tile of at most 16 / 32 / 48 positions, an expert's last or
+  // only one, runs only 1 / 2 / 3 column tiles' fragment reads and
+  // matrix-core work; the other sums stay zero and are never stored)
   typedef u32x4 TokFrags[2][kCT];
   auto read_tok = [&](auto nc, TokFrags& f, const uint8_t* tb) {
     constexpr int NC = decltype(nc)::value & 15;
@@ -747,7 +747,10 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
   // 128 / 256 (even routing) 133 / 141 -> 126 / 131 us per layer, Qwen1.5-MoE
   // T = 128 / 320 163 / 153 -> 155 / 144, Zipf routing and Qwen1.5 T = 1024
   // level; the nt policy for every short tile (an expert's last of several
-  // too) lost 5 - 8 % at Qwen1.5 T = 1024, whose experts end in such tiles
+  // too) lost 5 - 8 % at Qwen1.5 T = 1024, whose experts end in such tiles.
+  // The 3-column-tile copies (33 - 48 positions) then: Qwen3 int8 T = 512
+  // (even routing) 151.3 -> 140.5 us, Qwen1.5-MoE T = 512 / 640 174 / 189.6
+  // -> 165.3 / 183
   const int urows = __builtin_amdgcn_readfirstlane(it.rows);
   const bool only = __builtin_amdgcn_readfirstlane((int)it.only) != 0;
   if (urows <= 16) {
@@ -760,6 +763,11 @@ __global__ void __launch_bounds__(256, 2) gemm2_i8_kernel(GemmArgs a, int n_slab
       run(std::integral_constant<int, 2 | 2 << 4>{});
     else
       run(std::integral_constant<int, 2>{});
+  } else if (urows <= 48) {
+    if (only)
+      run(std::integral_constant<int, 3 | 2 << 4>{});
+    else
+      run(std::integral_constant<int, 3>{});
   } else {
     run(std::integral_constant<int, kCT>{});
   }
