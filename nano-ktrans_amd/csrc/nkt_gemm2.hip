@@ -998,8 +998,9 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
                                          it.slab);
   };
   // NARROW (experts average at most 32 positions): a tile of at most 16 / 32
-  // positions, an expert's last or only one, runs 1 / 2 of its 4 column
-  // tiles, an only tile with nt weight loads (T = 300 / 384 a further 124.5 /
+  // / 48 positions, an expert's last or only one, runs 1 / 2 / 3 of its 4
+  // column tiles (3: Qwen3 int4 T = 448 / 512 137.9 / 141.7 -> 129.1 / 133.3
+  // us, Mixtral T = 128 284.8 -> 265.7), an only tile with nt weight loads (T = 300 / 384 a further 124.5 /
   // 130.9 -> 120.2 / 126.3 us with the nt copy; the 1-tile copy then T = 200
   // / 256 / 300 114.9 / 116 / 117.5 -> 104.8 / 112.1 / 114.1 us).
   // Measured: Qwen3 int4 T = 300 (even routing) 149 -> 124.6 us per layer;
@@ -1022,6 +1023,11 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
         run(std::integral_constant<int, 2 | 2 << 4>{});
       else
         run(std::integral_constant<int, 2>{});
+    } else if (urows <= 48) {
+      if (only)
+        run(std::integral_constant<int, 3 | 2 << 4>{});
+      else
+        run(std::integral_constant<int, 3>{});
     } else {
       run(std::integral_constant<int, kCT>{});
     }
