@@ -345,7 +345,7 @@ GemmArgs expert_args(const Handle* h, int phase, bool shared, const void* in, vo
     a.n_tiles = ws_ptr<int32_t>(ws, L, kWsNTiles);
     a.num_rows = T * h->k;
     if (phase == PHASE_GATE_UP && L.bm == kTileSrcCols) a.tile_src = ws_ptr<int32_t>(ws, L, kWsTileSrc);
-    a.narrow_tiles = (int64_t)T * h->k <= 32 * (int64_t)h->E;
+    a.narrow_tiles = (int64_t)T * h->k <= 48 * (int64_t)h->E;
   }
   const int64_t in_rows = (!shared && phase == PHASE_GATE_UP) ? T : a.num_rows;
   a.in_bytes = in_rows * K * (h->act_bf16 ? 2 : 4);

@@ -997,18 +997,20 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
     gemm2_epilogue<WF_I4, PHASE, kWaves>(a, acc, srcl, orow_l, hpart, xtot_l, xtot_l, wrow, sexp, it.row0, it.rows,
                                          it.slab);
   };
-  // NARROW (experts average at most 32 positions): a tile of at most 16 / 32
+  // NARROW (experts average at most 48 positions): a tile of at most 16 / 32
   // / 48 positions, an expert's last or only one, runs 1 / 2 / 3 of its 4
   // column tiles (3: Qwen3 int4 T = 448 / 512 137.9 / 141.7 -> 129.1 / 133.3
   // us, Mixtral T = 128 284.8 -> 265.7), an only tile with nt weight loads (T = 300 / 384 a further 124.5 /
   // 130.9 -> 120.2 / 126.3 us with the nt copy; the 1-tile copy then T = 200
   // / 256 / 300 114.9 / 116 / 117.5 -> 104.8 / 112.1 / 114.1 us).
   // Measured: Qwen3 int4 T = 300 (even routing) 149 -> 124.6 us per layer;
-  // with these copies the switch at 32 positions per expert measured best
-  // (Qwen3 int4 T = 448 / 512 153.6 / 147.6 -> 139 / 144 us, Mixtral T = 128
-  // 307 -> 292.5 against 24; at 48 T = 768 173.5 -> 178.5), and where experts
-  // hold many full tiles the copies cost 1 - 5 % (Mixtral T = 2048, Qwen3
-  // int4 Zipf T = 2048), hence the launch-wide switch
+  // with the 1- and 2-tile copies the switch at 32 positions per expert
+  // measured best (Qwen3 int4 T = 448 / 512 153.6 / 147.6 -> 139 / 144 us,
+  // Mixtral T = 128 307 -> 292.5 against 24; at 48 T = 768 173.5 -> 178.5),
+  // with the 3-tile copies 48 (against 32: T = 640 / 768 154.5 / 172.6 ->
+  // 148 / 169.8, Mixtral T = 160 / 192 305.4 / 299.6 -> 279.5 / 289); where
+  // experts hold many full tiles the copies cost 1 - 5 % (Mixtral T = 2048,
+  // Qwen3 int4 Zipf T = 2048), hence the launch-wide switch
   if constexpr (NARROW) {
     // copy tag: column tiles | weight load policy << 4
     const int urows = __builtin_amdgcn_readfirstlane(it.rows);

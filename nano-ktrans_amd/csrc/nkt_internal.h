@@ -66,7 +66,7 @@ struct GemmArgs {
   // prefill int4, nonzero: a tile of at most 16 / 32 / 48 positions (an
   // expert's last or only one) runs a copy of the pipeline over the first
   // one / two / three of its four 16-position column tiles (set where experts
-  // average at most 32 positions)
+  // average at most 48 positions)
   int narrow_tiles;
   // single-token decode gate_up that routes its token itself
   // (route_logits != nullptr, [1, route_E] bf16): every workgroup runs K1
