@@ -339,7 +339,8 @@ def kernel_form(w, T):
     avg = T * w.k / w.E
     if w.wfmt == "f32":
         return "gemm_kernel"
-    if avg <= {"int8_per_channel": 4.5, "int4_g128": 6 if w.I >= 8192 else 8}.get(w.wfmt, 12):
+    int8 = 3.5 if w.shared else 4.5
+    if avg <= {"int8_per_channel": int8, "int4_g128": 6 if w.I >= 8192 else 8}.get(w.wfmt, 12):
         return "gemv_kernel"
     # int8 and int4 (bf16 activations, buffers under 4 GiB: every bench shape) have pipelined kernels
     return {"int8_per_channel": "gemm2_i8_kernel", "int4_g128": "gemm2_i4_kernel"}.get(w.wfmt, "gemm2_kernel")

@@ -76,12 +76,12 @@ extern "C" {
 #define NKT_WS_INV 5          /* int32 [T * k]  p -> pos */
 #define NKT_WS_H 6            /* act dtype [T*k, I]  SwiGLU activations by position */
 #define NKT_WS_Y 7            /* fp32 [T*k, H] expert outputs of nkt_moe_experts*: row = pair t*k + slot in the decode
-                                 form (T*k / E up to 4.5 for int8 weights, 8 for int4 (6 for I >= 8192), 12 for the others), else
-                                 position.  nkt_moe_forward* in the prefill form leaves it compact: fp16 [T*k, H] by
-                                 position, each 256-column slab of a row times a power of two, then fp32 [T*k, H/256]
-                                 with the inverse of each slab's factor; a one-token call (and a 2-4 token call with
-                                 int4 weights and 4*T*k <= E), whose down projection and combine share one launch,
-                                 does not write it */
+                                 form (T*k / E up to 4.5 for int8 weights, 3.5 with a shared expert; 8 for int4, 6 for
+                                 I >= 8192; 12 for the others), else position.  nkt_moe_forward* in the prefill form
+                                 leaves it compact: fp16 [T*k, H] by position, each 256-column slab of a row times a
+                                 power of two, then fp32 [T*k, H/256] with the inverse of each slab's factor; a
+                                 one-token call (and a 2-4 token call with int4 weights and 4*T*k <= E), whose down
+                                 projection and combine share one launch, does not write it */
 #define NKT_WS_SHARED_GATE 8  /* fp32 [T] sigmoid(x . g)                              */
 #define NKT_WS_SHARED_H 9     /* act dtype [T, I_s]                                    */
 #define NKT_WS_SHARED_Y 10    /* fp32 [T, H]; not written by a decode-form nkt_moe_forward* whose shared expert

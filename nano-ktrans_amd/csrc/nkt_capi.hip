@@ -189,7 +189,7 @@ WsLayout ws_layout(const Handle* h, int T) {
   WsLayout L;
   const size_t P = (size_t)T * h->k;
   const size_t es = h->act_bf16 ? 2 : 4;
-  L.bm = gemm_tile_m(T > 0 ? T : 1, h->k, h->E, h->wf, prefill_form_ok(h, false), h->I);
+  L.bm = gemm_tile_m(T > 0 ? T : 1, h->k, h->E, h->wf, prefill_form_ok(h, false), h->I, h->Is > 0);
   // the shared expert takes every token as one group.  While the routed
   // experts run in the decode form it does too (riding in their launches as
   // chunk tiles where it can); once they run in the prefill form, its own
@@ -204,7 +204,7 @@ WsLayout ws_layout(const Handle* h, int T) {
                  gemv_supported(h->wf, PHASE_GATE_UP, 2 * h->Is, h->H, h->Is) &&
                  gemv_supported(h->wf, PHASE_DOWN, h->H, h->Is, h->Is))
                     ? 16
-                    : gemm_tile_m(T > 0 ? T : 1, 1, 1, h->wf, prefill_form_ok(h, true), h->Is);
+                    : gemm_tile_m(T > 0 ? T : 1, 1, 1, h->wf, prefill_form_ok(h, true), h->Is, false);
   L.max_tiles = (int)(P / L.bm) + (int)(P < (size_t)h->E ? P : (size_t)h->E);
   size_t sz[kWsAll];
   sz[NKT_WS_TOPK_IDS] = P * 4;

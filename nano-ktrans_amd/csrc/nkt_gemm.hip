@@ -347,19 +347,21 @@ __global__ void __launch_bounds__(NW * 64) gemm_kernel(GemmArgs a) {
 // measured crossover of the two forms' layer times, with the prefill form's
 // short tiles on copies that skip empty column tiles: int8 weights 4.5 (the
 // decode form wins at 4.3 tokens per expert, the prefill form at 5 under
-// even and skewed routing alike), int4 8 (at 8 the forms are level under
+// even and skewed routing alike), 3.5 in a layer with a shared expert, which
+// the prefill form runs beside the routed experts on the side stream
+// (Qwen1.5-MoE T = 64 / 67: 131 / 134.2 -> 126.7 / 128.8 us), int4 8 (at 8 the forms are level under
 // even routing and the decode form wins under Zipf routing; at 10 - 16 the
 // prefill form wins: Qwen3 T = 192 107.8 -> 99.1 us, Mixtral T = 48 222 ->
 // 197, T = 64 285 -> 225) -- 6 for experts of I >= 8192, whose decode down
 // takes the long-K ring (Mixtral, T = 28 / 32: 189.6 / 194.8 -> 183.9 /
 // 180.5 us; level at 6, decode ahead at 5), others 12.
-double decode_form_max_avg(int wf, int I) {
-  return wf == WF_I8 ? 4.5 : wf == WF_I4 ? (I >= 8192 ? 6.0 : 8.0) : 12.0;
+double decode_form_max_avg(int wf, int I, bool shared) {
+  return wf == WF_I8 ? (shared ? 3.5 : 4.5) : wf == WF_I4 ? (I >= 8192 ? 6.0 : 8.0) : 12.0;
 }
 
-int gemm_tile_m(int num_tokens, int topk, int num_experts, int wf, bool prefill_form, int I) {
+int gemm_tile_m(int num_tokens, int topk, int num_experts, int wf, bool prefill_form, int I, bool shared) {
   const double avg = (double)num_tokens * topk / (double)num_experts;
-  if (avg <= decode_form_max_avg(wf, I)) return 16;
+  if (avg <= decode_form_max_avg(wf, I, shared)) return 16;
   if (wf != WF_F32 && prefill_form) return kPrefillTileM;
   if (avg <= 40.0) return 32;
   return 64;

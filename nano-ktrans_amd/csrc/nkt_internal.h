@@ -192,15 +192,15 @@ hipError_t launch_given_group(const int64_t* ids_in, const float* w_in, int T, i
                               int32_t* inv, int32_t* tiles, int32_t* n_tiles, int32_t* tile_src,
                               const uint8_t* resident, float* wpos, uint32_t* status, hipStream_t stream);
 
-// Tokens per expert up to which the decode form runs (by weight format and
-// the experts' intermediate size I).
-double decode_form_max_avg(int wf, int I);
+// Tokens per expert up to which the decode form runs (by weight format, the
+// experts' intermediate size I and whether the layer has a shared expert).
+double decode_form_max_avg(int wf, int I, bool shared);
 
 // Tile shapes: returns the token-tile height (BM) used for num_tokens:
 // 16 for decode-sized expert groups (gemv form), else kPrefillTileM when
 // the prefill form takes the shape (prefill_form), else 32 / 64 (the tiled
 // form that also serves fp32 weights).
-int gemm_tile_m(int num_tokens, int topk, int num_experts, int wf, bool prefill_form, int I);
+int gemm_tile_m(int num_tokens, int topk, int num_experts, int wf, bool prefill_form, int I, bool shared);
 
 // Rows of weights (gate_up: output columns of h) covered by one workgroup.
 int gemm_rows_per_block(int wf, int phase, int bm);

@@ -360,8 +360,8 @@ class NativeMoE:
 
     def experts(self, hidden_states: torch.Tensor):
         """K3 after ``route``: returns h [T*k, I] (act dtype) by position and y [T*k, H] (fp32), whose row is
-        the pair t*k + slot in the decode form (T*k / E up to 4.5 for int8 weights, 8 for int4 (6 for
-        I >= 8192), 12 for the others) and the position otherwise."""
+        the pair t*k + slot in the decode form (T*k / E up to 4.5 for int8 weights (3.5 with a shared
+        expert), 8 for int4 (6 for I >= 8192), 12 for the others) and the position otherwise."""
         x = self._check_input(hidden_states, self.hidden_size, "hidden_states")
         T = x.shape[0]
         ws = self.workspace(T)

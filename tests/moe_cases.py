@@ -48,10 +48,11 @@ class MoEConfig:
 
     def decode_form(self, T: int) -> bool:
         """Whether the library runs a batch of T tokens in its decode form:
-        up to 4.5 tokens per expert (T k / E) for int8 weights, 8 for int4
-        (6 where I >= 8192) and 12 for the others."""
+        up to 4.5 tokens per expert (T k / E) for int8 weights (3.5 with a
+        shared expert), 8 for int4 (6 where I >= 8192) and 12 for the others."""
+        int8 = 3.5 if self.Is > 0 else 4.5
         int4 = 6 if self.I >= 8192 else 8
-        return T * self.k <= {"int8_per_channel": 4.5, "int4_g128": int4}.get(self.wfmt, 12) * self.E
+        return T * self.k <= {"int8_per_channel": int8, "int4_g128": int4}.get(self.wfmt, 12) * self.E
 
     def shared_in_routed_launches(self, T: int) -> bool:
         """Whether the layer runs the shared expert inside the routed experts'

@@ -272,20 +272,21 @@ def test_shared_chunks_int4_and_bf16(gpu_device, wfmt, T):
     assert torch.equal(h_layer, h_stage)
 
 
-@pytest.mark.parametrize("T", [1, 16, 64, 67, 68, 200])
+@pytest.mark.parametrize("T", [1, 16, 48, 52, 53, 200])
 def test_qwen15_shared_full(gpu_device, T):
-    """T = 64 / 67: 4.3 / 4.47 positions per expert, the int8 decode form's
-    last token counts (the shared expert as 5 chunk tiles per chunk in the
-    routed launches); T = 68 the first in the prefill form."""
+    """T = 48 / 52: 3.2 / 3.47 positions per expert, the int8 decode form's
+    last token counts in a layer with a shared expert (which rides as 4
+    chunk tiles per chunk in the routed launches); T = 53 the first in the
+    prefill form, the shared expert forked beside the routed experts."""
     announce(f"forward qwen15_int8_shared full T={T}")
     layer, native = _layer("qwen15_int8_shared")
-    assert layer.cfg.decode_form(T) == (T <= 67)
+    assert layer.cfg.decode_form(T) == (T <= 52)
     _check(layer, native, T)
 
 
 @pytest.mark.parametrize("name,T", [("qwen15_int8_shared", 1), ("qwen15_int8_shared", 5),
-                                    ("qwen15_int8_shared", 16), ("qwen15_int8_shared", 60),
-                                    ("small_int8_shared", 1), ("small_int8_shared", 16)])
+                                    ("qwen15_int8_shared", 16), ("qwen15_int8_shared", 52),
+                                    ("small_int8_shared", 1), ("small_int8_shared", 12)])
 def test_shared_expert_in_routed_launches(gpu_device, name, T):
     """A decode-form batch and a shared expert whose intermediate size is a
     multiple of the routed one's (Qwen1.5-MoE: 4 chunks of 1408, the small
