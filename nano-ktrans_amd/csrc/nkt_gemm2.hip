@@ -944,11 +944,12 @@ __global__ void __launch_bounds__(512, 1) gemm2_i4_kernel(GemmArgs a, int n_slab
     }
     u32x4 ad[kRT][4];
     f32x4 sc[kRT];
+    const DqConst kdq = dq_const();
 #pragma unroll
     for (int r = 0; r < kRT; ++r) {
       sc[r] = bf16x4_to_f32(*(const u32x2*)(sx + sofs + r * 32 + (lane >> 4) * 8));
 #pragma unroll
-      for (int s = 0; s < 4; ++s) ad[r][s] = dq_i4(w[r][s]);
+      for (int s = 0; s < 4; ++s) ad[r][s] = dq_i4_k(w[r][s], kdq);
     }
     f32x4 tmp[kRT][kCT];
 #pragma unroll
