@@ -213,10 +213,14 @@ def test_qwen3_int8_batch_invariance_at_4096(gpu_device):
     compare(full[:97].float().cpu().numpy(), ref, layer.cfg)
 
 
-@pytest.mark.parametrize("T", [1, 16])
+@pytest.mark.parametrize("T", [1, 16, 24, 28])
 def test_mixtral_int4_full(gpu_device, T):
+    """T = 24: 6 positions per expert, the decode form's last count for
+    experts of I >= 8192; T = 28 the prefill form's short-tile instance
+    (tiles of about 7 positions: the one-column-tile copies)."""
     announce(f"forward mixtral_int4 full T={T}")
     layer, native = _layer("mixtral_int4")
+    assert layer.cfg.decode_form(T) == (T <= 24)
     _check(layer, native, T)
 
 
